@@ -1,0 +1,151 @@
+/*
+ * svl.h -- C ABI of the MI355X streaming-transformer step (libsvl.so).
+ *
+ * A drop-in for the per-frame decode step of semantic-voice-local's streaming transformer:
+ * the Kyutai STT language-model step and the Pocket-TTS flow-LM backbone step.  Reference
+ * paths are relative to the reference repository; SVL = crates/semantic-voice-local/src.
+ *
+ * Conventions (mirroring the crate's Rust API):
+ *  - Every function returns 0 on success, a negative svl_status on error (the message is in
+ *    svl_last_error(), thread-local), mirroring `Result<T, Error>` (SVL/error.rs:1-32).
+ *  - svl_model is immutable after creation and may be shared by host threads, as
+ *    `Stt: Send + Sync` (SVL/stt/mod.rs:159).  svl_state is per stream and used by one host
+ *    thread at a time, as `&mut TransformerState` (SVL/nn/transformer.rs:139).
+ *  - Host buffers belong to the caller.  svl_model_create copies (and repacks) the weights to
+ *    the GPU and keeps no host pointer.  Output buffers are caller-provided.
+ *  - Each state owns one HIP stream.  The *_async functions only enqueue work on it and take
+ *    device pointers; svl_state_synchronize waits for it.  The other entry points take host
+ *    pointers and return once their outputs are in host memory, like `to_scalar`
+ *    (SVL/stt/model.rs:258).
+ */
+#ifndef SVL_H
+#define SVL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* SVL/error.rs:3-30: Config, InvalidInput, Candle (tensor/device), Io. */
+typedef enum {
+    SVL_OK = 0,
+    SVL_ERR_CONFIG = -1,
+    SVL_ERR_INVALID_INPUT = -2,
+    SVL_ERR_DEVICE = -3,
+    SVL_ERR_IO = -4,
+} svl_status;
+
+/* Weight dtypes: dense, or candle QTensor block formats (GgmlDType::Q8_0 = 34-byte blocks
+ * {f16 d; i8 qs[32]}, GgmlDType::Q4K = 144-byte blocks {f16 d, dmin; u8 scales[12];
+ * u8 qs[128]}), row-major [out][in / block]. */
+typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4 } svl_dtype;
+
+typedef enum { SVL_NORM_LAYER = 0, SVL_NORM_RMS = 1 } svl_norm;          /* transformer.rs:12-16 */
+typedef enum { SVL_FF_PLAIN_GELU = 0, SVL_FF_GATED_SILU = 1 } svl_ff;    /* transformer.rs:18-24 */
+typedef enum { SVL_MODEL_TRANSFORMER = 0, SVL_MODEL_STT = 1, SVL_MODEL_TTS = 2 } svl_model_kind;
+
+/* TransformerConfig (SVL/nn/transformer.rs:26-41) plus the heads of the two backbones
+ * (SttConfig, SVL/stt/model.rs:16-34; FlowLmConfig's latent/z dims, SVL/tts/flow_lm.rs:45-126). */
+typedef struct {
+    int32_t kind;          /* svl_model_kind */
+    int32_t d_model, num_layers, num_heads, num_kv_heads, head_dim;
+    int32_t ff_kind;       /* svl_ff */
+    int32_t ff_hidden;
+    int32_t norm_kind;     /* svl_norm */
+    float norm_eps;
+    int32_t layer_scale;   /* 0/1: layers.{i}.layer_scale_{1,2}.scale */
+    int32_t context;       /* attention window; 0 = unlimited */
+    double max_period;     /* RoPE base */
+    int32_t quantize;      /* 0, SVL_Q8_0 or SVL_Q4K: dense linears are quantized on the GPU at
+                              creation (Linear::from_weight, SVL/nn/mod.rs:76-87) */
+    int32_t card, n_q, text_card;    /* STT */
+    int32_t latent_dim, z_dim;       /* TTS (z_dim 0: no z_proj) */
+    int32_t kv_dtype;      /* SVL_F32 (default) or SVL_BF16: element type of the KV ring buffers */
+} svl_config;
+
+/* One named tensor (the reference's safetensors names, e.g.
+ * "transformer.layers.3.self_attn.in_proj_weight", "emb.7.weight", "text_linear.weight"). */
+typedef struct {
+    const char* name;
+    int32_t dtype;         /* svl_dtype */
+    int32_t ndim;
+    int64_t shape[4];
+    const void* data;      /* host pointer */
+} svl_tensor;
+
+typedef struct svl_model svl_model;
+typedef struct svl_state svl_state;
+
+const char* svl_last_error(void);
+int svl_device_count(int* count);
+
+/* Transformer::new + LanguageModel::new / FlowLm::new (SVL/nn/transformer.rs:107-125,
+ * SVL/stt/model.rs:196-233, SVL/tts/flow_lm.rs:45-126) on GPU `device`. */
+int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device,
+                     svl_model** out);
+void svl_model_destroy(svl_model* model);
+
+/* The weight of linear `name` ("text_linear", "input_linear", "<layer>.in_proj",
+ * "<layer>.out_proj", "<layer>.ff1", "<layer>.ff2") as the GPU holds it: `f32` receives the
+ * dequantized (or converted) values computed by the GPU's dequantization kernel
+ * ([out][in] f32), `blocks` the candle block bytes rebuilt from the device copy (quantized
+ * linears only).  Either pointer may be NULL. */
+int svl_model_linear_weight(const svl_model* model, const char* name, float* f32, size_t f32_count,
+                            void* blocks, size_t block_bytes);
+
+/* Transformer::init_state (SVL/nn/transformer.rs:127-136) for `batch` lockstep streams.  Each
+ * stream has its own position (the reference's state has one position for the whole batch,
+ * transformer.rs:55; streams stepped together from a fresh state share it).  `capacity` bounds
+ * the positions of an unlimited-context model (ignored with a window: the ring buffer then has
+ * `context` slots). */
+int svl_state_create(const svl_model* model, int32_t batch, int32_t capacity, svl_state** out);
+/* TransformerState::duplicate (SVL/nn/transformer.rs:64-73). */
+int svl_state_duplicate(const svl_state* state, svl_state** out);
+/* TransformerState::from_layer_caches (SVL/nn/transformer.rs:81-103) for stream `stream`:
+ * per layer keys/values [num_kv_heads][len][head_dim] f32 covering positions 0..len. */
+int svl_state_load_stream(svl_state* state, int32_t stream, int64_t len, const float* const* keys,
+                          const float* const* values);
+/* TransformerState::layer_caches (SVL/nn/transformer.rs:76-78) for one stream and layer: the
+ * visible keys/values [num_kv_heads][*len][head_dim] f32 (pass NULL buffers to query *len and
+ * *first, the absolute position of the first one). */
+int svl_state_layer_cache(const svl_state* state, int32_t stream, int32_t layer, float* keys,
+                          float* values, int64_t* len, int64_t* first);
+int svl_state_positions(const svl_state* state, int64_t* positions /* [batch] */);
+int svl_state_reset(svl_state* state);
+void svl_state_destroy(svl_state* state);
+int svl_state_synchronize(svl_state* state);
+/* The state's HIP stream (hipStream_t), for callers that time or order work around it. */
+void* svl_state_stream(const svl_state* state);
+
+/* Transformer::forward (SVL/nn/transformer.rs:139-154): xs [batch][t][d_model] f32 ->
+ * ys [batch][t][d_model] f32 (host). */
+int svl_transformer_forward(const svl_model* model, svl_state* state, const float* xs, int64_t t,
+                            float* ys);
+
+/* LanguageModel::step (SVL/stt/model.rs:239-276) for every stream: text_tokens [batch],
+ * audio_tokens [batch][n_q] -> out_tokens [batch] (argmax, first index on ties) and optionally
+ * out_logits [batch][text_card] f32.  Host pointers. */
+int svl_stt_step(const svl_model* model, svl_state* state, const uint32_t* text_tokens,
+                 const uint32_t* audio_tokens, uint32_t* out_tokens, float* out_logits);
+
+/* Recognizer::step's token loop (SVL/stt/mod.rs:551-566) for n_steps steps with no host round
+ * trip: the text token of a step is the previous step's argmax (text_card before the first
+ * step of a stream), and a stream's first step (position 0) sees `card` for every audio
+ * token.  audio_tokens [n_steps][batch][n_q], out_tokens [n_steps][batch].  Host pointers. */
+int svl_stt_recognize(const svl_model* model, svl_state* state, int64_t n_steps,
+                      const uint32_t* audio_tokens, uint32_t* out_tokens);
+/* The same, enqueued on the state's stream; device pointers; returns without waiting. */
+int svl_stt_recognize_async(const svl_model* model, svl_state* state, int64_t n_steps,
+                            const uint32_t* d_audio_tokens, uint32_t* d_out_tokens);
+
+/* FlowLm::step's backbone (SVL/tts/flow_lm.rs:169-180) for every stream: latent
+ * [batch][latent_dim] f32, or NULL for the learnt `bos_emb` -> z [batch][z_dim or d_model]. */
+int svl_tts_backbone_step(const svl_model* model, svl_state* state, const float* latent,
+                          float* out_z);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,127 @@
+// Device-side scalar helpers shared by the step kernels.
+//
+// Everything here is compiled with -ffp-contract=off: a product is fused into an add only where
+// fmaf() is written, which is where the reference's CPU kernels fuse (`mul_add::<FMA>`,
+// SVL/nn/kernels/mod.rs:60-64).  The library targets gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace svl {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// IEEE binary16 -> f32 (exact).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+  uint32_t man = (uint32_t)h & 0x3ffu;
+  if (exp == 0x1fu) return u2f(sign | 0x7f800000u | (man << 13));
+  if (exp == 0) {
+    if (man == 0) return u2f(sign);
+    return u2f(sign | f2u((float)man * 0x1p-24f));
+  }
+  return u2f(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+// f32 -> binary16, round to nearest even (the `half` crate's f16::from_f32 semantics).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  uint32_t x = f2u(f);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t exp = (x >> 23) & 0xffu;
+  uint32_t man = x & 0x7fffffu;
+  if (exp == 0xffu) return (uint16_t)(man ? (sign | 0x7e00u | (man >> 13)) : (sign | 0x7c00u));
+  int e = (int)exp - 112;
+  if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    uint32_t m = man | 0x800000u;
+    int shift = 14 - e;
+    uint32_t hm = m >> shift;
+    uint32_t half = 1u << (shift - 1);
+    uint32_t rem = m & ((1u << shift) - 1u);
+    if (rem > half || (rem == half && (hm & 1u))) hm++;
+    return (uint16_t)(sign | hm);
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+  uint32_t rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)h;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = f2u(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+  if ((x & 0x8000u) && (x & 0x17fffu)) return (uint16_t)((x >> 16) + 1u);
+  return (uint16_t)(x >> 16);
+}
+
+// Rust `f as i8`: saturating, NaN -> 0.
+__device__ __forceinline__ int sat_i8(float v) {
+  if (v != v) return 0;
+  return v >= 127.0f ? 127 : (v <= -128.0f ? -128 : (int)v);
+}
+
+// The reference's branch-free exp (SVL/nn/kernels/mod.rs:93-131), FMA variant: Cody-Waite
+// reduction with a split ln2 and a degree-8 Taylor expm1, clamped to [-87, 88].
+__device__ __forceinline__ float ref_exp(float x) {
+  const float LN2_HI = 0.69314575f, LN2_LO = 1.4286068e-6f, ROUND = 12582912.0f;
+  const float LOG2E = 1.44269504088896340736f;
+  float xc = x < -87.0f ? -87.0f : x;
+  xc = xc > 88.0f ? 88.0f : xc;
+  float shifted = fmaf(xc, LOG2E, ROUND);
+  float k = shifted - ROUND;
+  int32_t k_int = (int32_t)(f2u(shifted) - f2u(ROUND));
+  float r = fmaf(-k, LN2_LO, fmaf(-k, LN2_HI, xc));
+  float p = 1.0f / 40320.0f;
+  p = fmaf(p, r, 1.0f / 5040.0f);
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  float two_k = u2f(((uint32_t)(k_int + 127)) << 23);
+  float y = fmaf(two_k, p * r, two_k);
+  if (x > 88.72f) y = __builtin_huge_valf();
+  return x < -87.0f ? 0.0f : y;
+}
+
+// SVL/nn/kernels/activation.rs:70-82.
+__device__ __forceinline__ float ref_silu(float x) { return x / (1.0f + ref_exp(-x)); }
+__device__ __forceinline__ float ref_gelu_tanh(float x) {
+  float a = 0.044715f * x;
+  float x2 = x * x;
+  float y = 0.7978846f * fmaf(a, x2, x);
+  return x / (1.0f + ref_exp(-2.0f * y));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+// Sum over the 32-lane half of the wave that the calling lane belongs to.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float half_max(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+}  // namespace svl

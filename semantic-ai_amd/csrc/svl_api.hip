@@ -1,0 +1,965 @@
+// libsvl: the C ABI of include/svl.h on top of the step kernels.
+//
+// Reference (crates/semantic-voice-local/src = SVL) behaviour mirrored here:
+//   Transformer / Layer / Attention / FeedForwardLayer   SVL/nn/transformer.rs:106-465
+//   Linear::from_weight (quantize at load)               SVL/nn/mod.rs:76-87
+//   LanguageModel::step / Recognizer::step               SVL/stt/model.rs:239-276, SVL/stt/mod.rs:551-566
+//   FlowLm::step backbone                                SVL/tts/flow_lm.rs:162-181
+//   TransformerState duplicate / from_layer_caches       SVL/nn/transformer.rs:58-104
+// The KV cache is a ring of `context` slots per layer (or `capacity` slots without a window):
+// key j of a stream lives in slot j % slots.  The reference's compacting cache
+// (transformer.rs:467-551) exposes exactly the last `context` keys to a one-step query, which
+// is the ring's content.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/svl.h"
+#include "kernels.h"
+
+using namespace svl;
+
+namespace {
+
+thread_local std::string g_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                          \
+  do {                                                                                         \
+    hipError_t e_ = (expr);                                                                    \
+    if (e_ != hipSuccess)                                                                      \
+      return set_error(SVL_ERR_DEVICE, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                       __FILE__, __LINE__);                                                    \
+  } while (0)
+
+#define TRY(expr)          \
+  do {                     \
+    int rc_ = (expr);      \
+    if (rc_ != 0) return rc_; \
+  } while (0)
+
+struct Layer {
+  float *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+  float *ls1 = nullptr, *ls2 = nullptr;
+  LinearDev in_proj, out_proj, ff1, ff2;
+};
+
+const svl_tensor* find_tensor(const svl_tensor* ts, size_t n, const std::string& name) {
+  for (size_t i = 0; i < n; ++i)
+    if (ts[i].name && name == ts[i].name) return &ts[i];
+  return nullptr;
+}
+
+size_t numel(const svl_tensor* t) {
+  size_t n = 1;
+  for (int i = 0; i < t->ndim; ++i) n *= (size_t)t->shape[i];
+  return n;
+}
+
+size_t dtype_bytes(int dtype) { return dtype == SVL_F32 ? 4 : 2; }
+
+}  // namespace
+
+struct svl_model {
+  svl_config cfg{};
+  int device = 0;
+  std::vector<void*> allocs;
+  std::vector<Layer> layers;
+  float* inv_freq = nullptr;
+  // STT
+  void* text_emb = nullptr;
+  std::vector<void*> emb;
+  void** emb_dev = nullptr;
+  int tables_bf16 = 0;
+  float* out_norm_w = nullptr;
+  float* out_norm_b = nullptr;
+  LinearDev text_linear;
+  // TTS
+  LinearDev input_linear, z_proj;
+  float* bos = nullptr;
+  hipStream_t stream = nullptr;  // used at creation only
+
+  ~svl_model() {
+    hipSetDevice(device);
+    for (void* p : allocs) hipFree(p);
+    if (stream) hipStreamDestroy(stream);
+  }
+
+  int alloc(void** p, size_t bytes) {
+    HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
+    allocs.push_back(*p);
+    return 0;
+  }
+};
+
+struct svl_state {
+  const svl_model* m = nullptr;
+  int B = 1;
+  int slots = 0;  // ring slots per stream and layer
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocs;
+  std::vector<void*> kc, vc;  // per layer [B][KVH][slots][hd]
+  int* pos = nullptr;
+  std::vector<int64_t> pos_host;
+  uint32_t* fb_tok = nullptr;
+  float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
+  float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  float* in = nullptr;        // TTS latent / forward input staging
+  uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
+  uint32_t* tok_out = nullptr;
+  int nsplit = 1;
+  int chunk = 32;
+  size_t in_cap = 0;
+
+  ~svl_state() {
+    hipSetDevice(m->device);
+    if (stream) hipStreamSynchronize(stream);
+    for (void* p : allocs) hipFree(p);
+    if (stream) hipStreamDestroy(stream);
+  }
+  int alloc(void** p, size_t bytes) {
+    HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
+    allocs.push_back(*p);
+    return 0;
+  }
+};
+
+namespace {
+
+// Uploads a dense tensor as f32 (converted on the GPU from bf16/f16).
+int upload_f32(svl_model* m, const svl_tensor* t, size_t n, float** out) {
+  if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor");
+  if (numel(t) != n)
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: %zu elements, expected %zu", t->name, numel(t), n);
+  void* dst;
+  TRY(m->alloc(&dst, n * 4));
+  if (t->dtype == SVL_F32) {
+    HIP_TRY(hipMemcpy(dst, t->data, n * 4, hipMemcpyHostToDevice));
+  } else if (t->dtype == SVL_BF16 || t->dtype == SVL_F16) {
+    void* tmp;
+    HIP_TRY(hipMalloc(&tmp, n * 2));
+    HIP_TRY(hipMemcpy(tmp, t->data, n * 2, hipMemcpyHostToDevice));
+    hipError_t e = t->dtype == SVL_BF16 ? launch_bf16_to_f32((const uint16_t*)tmp, (float*)dst, n, m->stream)
+                                         : launch_f16_to_f32((const uint16_t*)tmp, (float*)dst, n, m->stream);
+    hipError_t e2 = hipStreamSynchronize(m->stream);
+    hipFree(tmp);
+    HIP_TRY(e);
+    HIP_TRY(e2);
+  } else {
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: dense dtype expected", t->name);
+  }
+  *out = (float*)dst;
+  return 0;
+}
+
+int load_vec(svl_model* m, const svl_tensor* ts, size_t n, const std::string& name, size_t count, float** out) {
+  const svl_tensor* t = find_tensor(ts, n, name);
+  if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", name.c_str());
+  return upload_f32(m, t, count, out);
+}
+
+// Linear::from_weight (SVL/nn/mod.rs:76-87): candle blocks are repacked; dense weights are
+// quantized on the GPU when `quantize` asks for it and the input width is a multiple of the
+// block, kept dense (f32 or bf16) otherwise.
+int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string& name, int out_f, int in_f,
+                int quantize, LinearDev* L) {
+  const svl_tensor* t = find_tensor(ts, n, name);
+  if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", name.c_str());
+  if (t->ndim != 2 || t->shape[0] != out_f || t->shape[1] != in_f)
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: shape mismatch (expected [%d, %d])", name.c_str(), out_f, in_f);
+  L->out = out_f;
+  L->in = in_f;
+  const size_t count = (size_t)out_f * in_f;
+  if (t->dtype == SVL_Q4K || (t->dtype != SVL_Q8_0 && quantize == SVL_Q4K && in_f % 256 == 0))
+    return set_error(SVL_ERR_CONFIG, "tensor %s: Q4K linears are not supported yet", name.c_str());
+  if (t->dtype == SVL_Q8_0) {
+    if (in_f % 32) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: Q8_0 needs in %% 32 == 0", name.c_str());
+    void *qs, *d, *tmp;
+    TRY(m->alloc(&qs, count));
+    TRY(m->alloc(&d, count / 32 * 2));
+    HIP_TRY(hipMalloc(&tmp, count / 32 * 34));
+    HIP_TRY(hipMemcpy(tmp, t->data, count / 32 * 34, hipMemcpyHostToDevice));
+    hipError_t e = launch_q8_from_blocks((const uint8_t*)tmp, out_f, in_f, (int8_t*)qs, (uint16_t*)d, m->stream);
+    hipError_t e2 = hipStreamSynchronize(m->stream);
+    hipFree(tmp);
+    HIP_TRY(e);
+    HIP_TRY(e2);
+    L->fmt = FMT_Q8_0;
+    L->w = qs;
+    L->scale = (uint16_t*)d;
+    return 0;
+  }
+  if (t->dtype != SVL_F32 && t->dtype != SVL_BF16 && t->dtype != SVL_F16)
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: unsupported dtype %d", name.c_str(), t->dtype);
+  if (quantize == SVL_Q8_0 && in_f % 32 == 0) {
+    float* f = nullptr;
+    TRY(upload_f32(m, t, count, &f));
+    void *qs, *d;
+    TRY(m->alloc(&qs, count));
+    TRY(m->alloc(&d, count / 32 * 2));
+    HIP_TRY(launch_q8_quantize(f, out_f, in_f, (int8_t*)qs, (uint16_t*)d, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    // the f32 staging copy is released right away
+    m->allocs.pop_back();
+    m->allocs.pop_back();
+    m->allocs.pop_back();
+    hipFree(f);
+    m->allocs.push_back(qs);
+    m->allocs.push_back(d);
+    L->fmt = FMT_Q8_0;
+    L->w = qs;
+    L->scale = (uint16_t*)d;
+    return 0;
+  }
+  if (t->dtype == SVL_BF16) {
+    if (in_f % 8) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: bf16 rows need in %% 8 == 0", name.c_str());
+    void* w;
+    TRY(m->alloc(&w, count * 2));
+    HIP_TRY(hipMemcpy(w, t->data, count * 2, hipMemcpyHostToDevice));
+    L->fmt = FMT_BF16;
+    L->w = w;
+    return 0;
+  }
+  if (in_f % 4) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: f32 rows need in %% 4 == 0", name.c_str());
+  float* f = nullptr;
+  TRY(upload_f32(m, t, count, &f));
+  L->fmt = FMT_F32;
+  L->w = f;
+  return 0;
+}
+
+// Embedding tables: kept bf16 when every table is bf16, f32 otherwise.
+int load_table(svl_model* m, const svl_tensor* ts, size_t n, const std::string& name, size_t count, void** out) {
+  const svl_tensor* t = find_tensor(ts, n, name);
+  if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", name.c_str());
+  if (numel(t) != count)
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: %zu elements, expected %zu", name.c_str(), numel(t), count);
+  if (m->tables_bf16) {
+    void* w;
+    TRY(m->alloc(&w, count * 2));
+    HIP_TRY(hipMemcpy(w, t->data, count * 2, hipMemcpyHostToDevice));
+    *out = w;
+    return 0;
+  }
+  float* f;
+  TRY(upload_f32(m, t, count, &f));
+  *out = f;
+  return 0;
+}
+
+int check_config(const svl_config* c) {
+  if (c->d_model <= 0 || c->num_layers <= 0 || c->num_heads <= 0 || c->num_kv_heads <= 0 || c->head_dim <= 0)
+    return set_error(SVL_ERR_CONFIG, "invalid transformer dimensions");
+  if (c->num_heads % c->num_kv_heads) return set_error(SVL_ERR_CONFIG, "num_heads must be a multiple of num_kv_heads");
+  if (c->head_dim != 64 && c->head_dim != 128) return set_error(SVL_ERR_CONFIG, "head_dim must be 64 or 128");
+  if (c->d_model % 32) return set_error(SVL_ERR_CONFIG, "d_model must be a multiple of 32");
+  if (c->ff_hidden <= 0 || c->ff_hidden % 32) return set_error(SVL_ERR_CONFIG, "ff_hidden must be a positive multiple of 32");
+  if ((c->num_heads * c->head_dim) % 32) return set_error(SVL_ERR_CONFIG, "attention width must be a multiple of 32");
+  // the GEMV prologue stages one input row in LDS (5 bytes per element, 64 KiB per workgroup)
+  if (c->d_model > 12288 || c->ff_hidden > 12288 || c->num_heads * c->head_dim > 12288)
+    return set_error(SVL_ERR_CONFIG, "d_model, ff_hidden and num_heads * head_dim must be <= 12288");
+  if (c->norm_kind != SVL_NORM_LAYER && c->norm_kind != SVL_NORM_RMS) return set_error(SVL_ERR_CONFIG, "unknown norm");
+  if (c->ff_kind != SVL_FF_PLAIN_GELU && c->ff_kind != SVL_FF_GATED_SILU) return set_error(SVL_ERR_CONFIG, "unknown feed-forward");
+  if (c->context < 0) return set_error(SVL_ERR_CONFIG, "context must be >= 0");
+  if (c->kv_dtype != SVL_F32 && c->kv_dtype != SVL_BF16) return set_error(SVL_ERR_CONFIG, "kv_dtype must be F32 or BF16");
+  if (c->kind == SVL_MODEL_STT && (c->n_q <= 0 || c->card <= 0 || c->text_card <= 0))
+    return set_error(SVL_ERR_CONFIG, "invalid STT heads");
+  if (c->kind == SVL_MODEL_TTS && c->latent_dim <= 0) return set_error(SVL_ERR_CONFIG, "invalid TTS latent_dim");
+  if (c->kind == SVL_MODEL_TTS && c->latent_dim % 4) return set_error(SVL_ERR_CONFIG, "latent_dim must be a multiple of 4");
+  return 0;
+}
+
+int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_model* m) {
+  const svl_config& c = *cfg;
+  TRY(check_config(cfg));
+  HIP_TRY(hipStreamCreate(&m->stream));
+  const std::string pre = c.kind == SVL_MODEL_TRANSFORMER ? "" : "transformer.";
+  const int d = c.d_model, hd = c.head_dim;
+  const int qdim = c.num_heads * hd, kvdim = c.num_kv_heads * hd;
+  m->layers.resize(c.num_layers);
+  for (int i = 0; i < c.num_layers; ++i) {
+    Layer& L = m->layers[i];
+    const std::string p = pre + "layers." + std::to_string(i) + ".";
+    if (c.norm_kind == SVL_NORM_RMS) {
+      TRY(load_vec(m, ts, n, p + "norm1.alpha", d, &L.n1w));
+      TRY(load_vec(m, ts, n, p + "norm2.alpha", d, &L.n2w));
+    } else {
+      TRY(load_vec(m, ts, n, p + "norm1.weight", d, &L.n1w));
+      TRY(load_vec(m, ts, n, p + "norm1.bias", d, &L.n1b));
+      TRY(load_vec(m, ts, n, p + "norm2.weight", d, &L.n2w));
+      TRY(load_vec(m, ts, n, p + "norm2.bias", d, &L.n2b));
+    }
+    if (c.layer_scale) {
+      TRY(load_vec(m, ts, n, p + "layer_scale_1.scale", d, &L.ls1));
+      TRY(load_vec(m, ts, n, p + "layer_scale_2.scale", d, &L.ls2));
+    }
+    std::string inp = p + "self_attn.in_proj_weight";
+    if (!find_tensor(ts, n, inp)) inp = p + "self_attn.in_proj.weight";
+    TRY(load_linear(m, ts, n, inp, qdim + 2 * kvdim, d, c.quantize, &L.in_proj));
+    TRY(load_linear(m, ts, n, p + "self_attn.out_proj.weight", d, qdim, c.quantize, &L.out_proj));
+    if (c.ff_kind == SVL_FF_GATED_SILU) {
+      TRY(load_linear(m, ts, n, p + "gating.linear_in.weight", 2 * c.ff_hidden, d, c.quantize, &L.ff1));
+      TRY(load_linear(m, ts, n, p + "gating.linear_out.weight", d, c.ff_hidden, c.quantize, &L.ff2));
+    } else {
+      TRY(load_linear(m, ts, n, p + "linear1.weight", c.ff_hidden, d, c.quantize, &L.ff1));
+      TRY(load_linear(m, ts, n, p + "linear2.weight", d, c.ff_hidden, c.quantize, &L.ff2));
+    }
+  }
+  // inv_freq in f64 then f32 (SVL/nn/transformer.rs:114-118)
+  {
+    std::vector<float> inv(hd / 2);
+    for (int i = 0; i < hd / 2; ++i)
+      inv[i] = (float)std::exp(-(std::log(c.max_period)) * 2.0 * (double)i / (double)hd);
+    void* p;
+    TRY(m->alloc(&p, inv.size() * 4));
+    HIP_TRY(hipMemcpy(p, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
+    m->inv_freq = (float*)p;
+  }
+  if (c.kind == SVL_MODEL_STT) {
+    bool all_bf16 = true;
+    const svl_tensor* te = find_tensor(ts, n, "text_emb.weight");
+    if (!te) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor text_emb.weight");
+    all_bf16 = te->dtype == SVL_BF16;
+    for (int i = 0; i < c.n_q && all_bf16; ++i) {
+      const svl_tensor* t = find_tensor(ts, n, "emb." + std::to_string(i) + ".weight");
+      all_bf16 = t && t->dtype == SVL_BF16;
+    }
+    m->tables_bf16 = all_bf16 ? 1 : 0;
+    TRY(load_table(m, ts, n, "text_emb.weight", (size_t)(c.text_card + 1) * d, &m->text_emb));
+    m->emb.resize(c.n_q);
+    for (int i = 0; i < c.n_q; ++i)
+      TRY(load_table(m, ts, n, "emb." + std::to_string(i) + ".weight", (size_t)(c.card + 1) * d, &m->emb[i]));
+    void* p;
+    TRY(m->alloc(&p, sizeof(void*) * c.n_q));
+    HIP_TRY(hipMemcpy(p, m->emb.data(), sizeof(void*) * c.n_q, hipMemcpyHostToDevice));
+    m->emb_dev = (void**)p;
+    TRY(load_vec(m, ts, n, "out_norm.alpha", d, &m->out_norm_w));
+    TRY(load_linear(m, ts, n, "text_linear.weight", c.text_card, d, c.quantize, &m->text_linear));
+  } else if (c.kind == SVL_MODEL_TTS) {
+    // input_linear, z_proj: always dense (Linear::new, SVL/tts/flow_lm.rs:72-74)
+    TRY(load_linear(m, ts, n, "input_linear.weight", d, c.latent_dim, 0, &m->input_linear));
+    TRY(load_vec(m, ts, n, "out_norm.weight", d, &m->out_norm_w));
+    TRY(load_vec(m, ts, n, "out_norm.bias", d, &m->out_norm_b));
+    if (c.z_dim > 0) TRY(load_linear(m, ts, n, "z_proj.weight", c.z_dim, d, 0, &m->z_proj));
+    TRY(load_vec(m, ts, n, "bos_emb", c.latent_dim, &m->bos));
+  }
+  HIP_TRY(hipDeviceSynchronize());
+  return 0;
+}
+
+const LinearDev* find_linear(const svl_model* m, const char* name) {
+  if (!strcmp(name, "text_linear")) return m->cfg.kind == SVL_MODEL_STT ? &m->text_linear : nullptr;
+  if (!strcmp(name, "input_linear")) return m->cfg.kind == SVL_MODEL_TTS ? &m->input_linear : nullptr;
+  if (!strcmp(name, "z_proj")) return m->cfg.z_dim > 0 ? &m->z_proj : nullptr;
+  int layer = -1;
+  char which[64] = {0};
+  if (sscanf(name, "%d.%63s", &layer, which) != 2 || layer < 0 || layer >= m->cfg.num_layers) return nullptr;
+  const Layer& L = m->layers[layer];
+  if (!strcmp(which, "in_proj")) return &L.in_proj;
+  if (!strcmp(which, "out_proj")) return &L.out_proj;
+  if (!strcmp(which, "ff1")) return &L.ff1;
+  if (!strcmp(which, "ff2")) return &L.ff2;
+  return nullptr;
+}
+
+int norm_code(const svl_config& c) { return c.norm_kind == SVL_NORM_RMS ? NORM_RMS : NORM_LAYER; }
+
+// One step of every stream through all layers, from s->x (the embedded input) to s->x (the
+// transformer output).  Advances the positions at the end.
+int run_layers(const svl_model* m, svl_state* s) {
+  const svl_config& c = m->cfg;
+  const int d = c.d_model, hd = c.head_dim, H = c.num_heads, KVH = c.num_kv_heads;
+  for (int i = 0; i < c.num_layers; ++i) {
+    const Layer& L = m->layers[i];
+    GemvArgs g{};
+    g.B = s->B;
+    // norm1 -> in_proj -> RoPE(q, k) -> q buffer, KV ring
+    g.L = L.in_proj;
+    g.x = s->x;
+    g.x_stride = d;
+    g.norm = norm_code(c);
+    g.nw = L.n1w;
+    g.nb = L.n1b;
+    g.eps = c.norm_eps;
+    g.epi = EPI_QKV_ROPE;
+    g.pos = s->pos;
+    g.inv_freq = m->inv_freq;
+    g.H = H;
+    g.KVH = KVH;
+    g.hd = hd;
+    g.q_out = s->q;
+    g.kc = s->kc[i];
+    g.vc = s->vc[i];
+    g.cap = s->slots;
+    g.kv_bf16 = c.kv_dtype == SVL_BF16;
+    HIP_TRY(launch_gemv(g, s->stream));
+    // attention over the ring
+    AttnArgs a{};
+    a.q = s->q;
+    a.kc = s->kc[i];
+    a.vc = s->vc[i];
+    a.pos = s->pos;
+    a.B = s->B;
+    a.H = H;
+    a.KVH = KVH;
+    a.hd = hd;
+    a.cap = s->slots;
+    a.window = c.context;
+    a.kv_bf16 = c.kv_dtype == SVL_BF16;
+    a.scale = std::pow((float)hd, -0.5f);
+    a.chunk = s->chunk;
+    a.nsplit = s->nsplit;
+    a.pm = s->pm;
+    a.pl = s->pl;
+    a.po = s->po;
+    a.out = s->att;
+    HIP_TRY(launch_attention(a, s->stream));
+    // out_proj + residual
+    GemvArgs o{};
+    o.B = s->B;
+    o.L = L.out_proj;
+    o.x = s->att;
+    o.x_stride = H * hd;
+    o.norm = NORM_NONE;
+    o.epi = EPI_RESID;
+    o.resid = s->x;
+    o.resid_stride = d;
+    o.lscale = L.ls1;
+    HIP_TRY(launch_gemv(o, s->stream));
+    // norm2 -> feed-forward in
+    GemvArgs f{};
+    f.B = s->B;
+    f.L = L.ff1;
+    f.x = s->x;
+    f.x_stride = d;
+    f.norm = norm_code(c);
+    f.nw = L.n2w;
+    f.nb = L.n2b;
+    f.eps = c.norm_eps;
+    f.y = s->h;
+    f.y_stride = c.ff_hidden;
+    if (c.ff_kind == SVL_FF_GATED_SILU) {
+      f.epi = EPI_SILU_GATE;
+      f.ff_hidden = c.ff_hidden;
+    } else {
+      f.epi = EPI_GELU;
+    }
+    HIP_TRY(launch_gemv(f, s->stream));
+    // feed-forward out + residual (the last layer advances the positions: no later kernel of
+    // the step reads them)
+    GemvArgs f2{};
+    f2.B = s->B;
+    f2.L = L.ff2;
+    f2.x = s->h;
+    f2.x_stride = c.ff_hidden;
+    f2.norm = NORM_NONE;
+    f2.epi = EPI_RESID;
+    f2.resid = s->x;
+    f2.resid_stride = d;
+    f2.lscale = L.ls2;
+    f2.pos = s->pos;
+    f2.advance_pos = i == c.num_layers - 1;
+    HIP_TRY(launch_gemv(f2, s->stream));
+  }
+  for (auto& p : s->pos_host) p += 1;
+  return 0;
+}
+
+int check_room(const svl_state* s, int64_t steps) {
+  if (s->m->cfg.context > 0) return 0;
+  for (int64_t p : s->pos_host)
+    if (p + steps > s->slots)
+      return set_error(SVL_ERR_INVALID_INPUT, "state capacity %d exceeded (position %lld + %lld steps)", s->slots,
+                       (long long)p, (long long)steps);
+  return 0;
+}
+
+// text_linear over out_norm(x), then argmax into the feedback tokens (and `out` if given).
+int run_stt_head(const svl_model* m, svl_state* s, uint32_t* out) {
+  const svl_config& c = m->cfg;
+  GemvArgs g{};
+  g.B = s->B;
+  g.L = m->text_linear;
+  g.x = s->x;
+  g.x_stride = c.d_model;
+  g.norm = NORM_RMS;
+  g.nw = m->out_norm_w;
+  g.eps = 1e-8f;  // SVL/stt/model.rs:252
+  g.epi = EPI_STORE;
+  g.y = s->logits;
+  g.y_stride = c.text_card;
+  HIP_TRY(launch_gemv(g, s->stream));
+  HIP_TRY(launch_argmax(s->logits, s->B, c.text_card, s->fb_tok, out, nullptr, s->stream));
+  return 0;
+}
+
+int stt_steps(const svl_model* m, svl_state* s, int64_t n, const uint32_t* d_audio, uint32_t* d_out) {
+  const svl_config& c = m->cfg;
+  TRY(check_room(s, n));
+  for (int64_t i = 0; i < n; ++i) {
+    EmbedArgs e{};
+    e.text_emb = m->text_emb;
+    e.emb = m->emb_dev;
+    e.tables_bf16 = m->tables_bf16;
+    e.d = c.d_model;
+    e.n_q = c.n_q;
+    e.card = c.card;
+    e.text_card = c.text_card;
+    e.B = s->B;
+    e.text_tok = nullptr;
+    e.fb_tok = s->fb_tok;
+    e.audio = d_audio + (size_t)i * s->B * c.n_q;
+    e.initial_at_zero = 1;
+    e.pos = s->pos;
+    e.x = s->x;
+    HIP_TRY(launch_embed(e, s->stream));
+    TRY(run_layers(m, s));
+    TRY(run_stt_head(m, s, d_out + (size_t)i * s->B));
+  }
+  return 0;
+}
+
+int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** out) {
+  const svl_config& c = m->cfg;
+  if (batch <= 0) return set_error(SVL_ERR_INVALID_INPUT, "batch must be positive");
+  int slots = c.context > 0 ? c.context : capacity;
+  if (slots <= 0) return set_error(SVL_ERR_INVALID_INPUT, "an unlimited-context model needs a positive capacity");
+  HIP_TRY(hipSetDevice(m->device));
+  svl_state* s = new svl_state();
+  s->m = m;
+  s->B = batch;
+  s->slots = slots;
+  s->chunk = 32;
+  s->nsplit = (slots + s->chunk - 1) / s->chunk;
+  auto fail = [&](int rc) {
+    delete s;
+    return rc;
+  };
+  if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
+    return fail(set_error(SVL_ERR_DEVICE, "hipStreamCreate failed"));
+  const size_t kvb = (size_t)batch * c.num_kv_heads * slots * c.head_dim * (c.kv_dtype == SVL_BF16 ? 2 : 4);
+  s->kc.resize(c.num_layers);
+  s->vc.resize(c.num_layers);
+  int rc = 0;
+  for (int i = 0; i < c.num_layers && !rc; ++i) {
+    rc = s->alloc(&s->kc[i], kvb);
+    if (!rc) rc = s->alloc(&s->vc[i], kvb);
+    if (!rc && hipMemsetAsync(s->kc[i], 0, kvb, s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
+    if (!rc && hipMemsetAsync(s->vc[i], 0, kvb, s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
+  }
+  const int qdim = c.num_heads * c.head_dim;
+  const int width = std::max(std::max(c.d_model, qdim), c.ff_hidden);
+  void* p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * sizeof(int)), s->pos = (int*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->fb_tok = (uint32_t*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * c.d_model * 4), s->x = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * qdim * 4), s->q = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * qdim * 4), s->att = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * width * 4), s->h = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.text_card, 1) * 4), s->logits = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.d_model, c.z_dim) * 4), s->z = (float*)p;
+  const size_t np = (size_t)batch * c.num_heads * s->nsplit;
+  if (!rc) rc = s->alloc(&p, np * 4), s->pm = (float*)p;
+  if (!rc) rc = s->alloc(&p, np * 4), s->pl = (float*)p;
+  if (!rc) rc = s->alloc(&p, np * c.head_dim * 4), s->po = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;
+  if (rc) return fail(rc);
+  s->pos_host.assign(batch, 0);
+  if (launch_fill_i32(s->pos, 0, batch, s->stream) != hipSuccess ||
+      launch_fill_u32(s->fb_tok, (uint32_t)std::max(c.text_card, 0), batch, s->stream) != hipSuccess ||
+      hipStreamSynchronize(s->stream) != hipSuccess)
+    return fail(set_error(SVL_ERR_DEVICE, "state initialisation failed"));
+  *out = s;
+  return 0;
+}
+
+int ensure_in(svl_state* s, size_t bytes) {
+  if (s->in_cap >= bytes) return 0;
+  void* p;
+  TRY(s->alloc(&p, bytes));
+  s->in = (float*)p;
+  s->in_cap = bytes;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* svl_last_error(void) { return g_error.c_str(); }
+
+int svl_device_count(int* count) {
+  HIP_TRY(hipGetDeviceCount(count));
+  return 0;
+}
+
+int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {
+  if (!cfg || !out || (!tensors && count)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  *out = nullptr;
+  TRY(check_config(cfg));
+  int ndev = 0;
+  HIP_TRY(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) return set_error(SVL_ERR_DEVICE, "device %d not available (%d devices)", device, ndev);
+  HIP_TRY(hipSetDevice(device));
+  svl_model* m = new svl_model();
+  m->cfg = *cfg;
+  m->device = device;
+  int rc = create_model(cfg, tensors, count, m);
+  if (rc) {
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return 0;
+}
+
+void svl_model_destroy(svl_model* model) { delete model; }
+
+int svl_model_linear_weight(const svl_model* m, const char* name, float* f32, size_t f32_count, void* blocks,
+                            size_t block_bytes) {
+  if (!m || !name) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  const LinearDev* L = find_linear(m, name);
+  if (!L) return set_error(SVL_ERR_INVALID_INPUT, "unknown linear %s", name);
+  HIP_TRY(hipSetDevice(m->device));
+  const size_t n = (size_t)L->out * L->in;
+  if (f32) {
+    if (f32_count != n) return set_error(SVL_ERR_INVALID_INPUT, "f32 buffer holds %zu values, need %zu", f32_count, n);
+    float* tmp;
+    HIP_TRY(hipMalloc(&tmp, n * 4));
+    hipError_t e = launch_dequant(*L, tmp, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e == hipSuccess) e = hipMemcpy(f32, tmp, n * 4, hipMemcpyDeviceToHost);
+    hipFree(tmp);
+    HIP_TRY(e);
+  }
+  if (blocks) {
+    if (L->fmt != FMT_Q8_0) return set_error(SVL_ERR_INVALID_INPUT, "linear %s is not quantized", name);
+    if (block_bytes != n / 32 * 34) return set_error(SVL_ERR_INVALID_INPUT, "block buffer size mismatch");
+    uint8_t* tmp;
+    HIP_TRY(hipMalloc(&tmp, block_bytes));
+    hipError_t e = launch_q8_to_blocks((const int8_t*)L->w, L->scale, L->out, L->in, tmp, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e == hipSuccess) e = hipMemcpy(blocks, tmp, block_bytes, hipMemcpyDeviceToHost);
+    hipFree(tmp);
+    HIP_TRY(e);
+  }
+  return 0;
+}
+
+int svl_state_create(const svl_model* model, int32_t batch, int32_t capacity, svl_state** out) {
+  if (!model || !out) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  *out = nullptr;
+  return make_state(model, batch, capacity, out);
+}
+
+int svl_state_duplicate(const svl_state* s, svl_state** out) {
+  if (!s || !out) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  svl_state* c = nullptr;
+  TRY(make_state(s->m, s->B, s->slots, &c));
+  const svl_config& cfg = s->m->cfg;
+  const size_t kvb = (size_t)s->B * cfg.num_kv_heads * s->slots * cfg.head_dim * (cfg.kv_dtype == SVL_BF16 ? 2 : 4);
+  hipError_t e = hipStreamSynchronize(s->stream);
+  for (int i = 0; i < cfg.num_layers && e == hipSuccess; ++i) {
+    e = hipMemcpyAsync(c->kc[i], s->kc[i], kvb, hipMemcpyDeviceToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->vc[i], s->vc[i], kvb, hipMemcpyDeviceToDevice, c->stream);
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(c->pos, s->pos, s->B * sizeof(int), hipMemcpyDeviceToDevice, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(c->fb_tok, s->fb_tok, s->B * 4, hipMemcpyDeviceToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    delete c;
+    return set_error(SVL_ERR_DEVICE, "state copy failed: %s", hipGetErrorString(e));
+  }
+  c->pos_host = s->pos_host;
+  *out = c;
+  return 0;
+}
+
+int svl_state_load_stream(svl_state* s, int32_t stream, int64_t len, const float* const* keys,
+                          const float* const* values) {
+  if (!s || (len > 0 && (!keys || !values))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (stream < 0 || stream >= s->B) return set_error(SVL_ERR_INVALID_INPUT, "stream %d out of range", stream);
+  if (len < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative length");
+  const svl_config& c = s->m->cfg;
+  if (c.context == 0 && len > s->slots)
+    return set_error(SVL_ERR_INVALID_INPUT, "cache length %lld exceeds the state capacity %d", (long long)len, s->slots);
+  HIP_TRY(hipSetDevice(s->m->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  const int KVH = c.num_kv_heads, hd = c.head_dim, S = s->slots;
+  const size_t per = (size_t)KVH * S * hd;
+  std::vector<float> hk(per, 0.0f), hv(per, 0.0f);
+  float* tmp;
+  HIP_TRY(hipMalloc(&tmp, per * 4));
+  const int64_t keep = len < S ? len : S;
+  hipError_t e = hipSuccess;
+  const int esz = c.kv_dtype == SVL_BF16 ? 2 : 4;
+  for (int i = 0; i < c.num_layers && e == hipSuccess; ++i) {
+    for (int kv = 0; kv < 2 && e == hipSuccess; ++kv) {
+      const float* src = kv == 0 ? keys[i] : values[i];
+      std::vector<float>& h = kv == 0 ? hk : hv;
+      std::fill(h.begin(), h.end(), 0.0f);
+      for (int g = 0; g < KVH; ++g)
+        for (int64_t j = len - keep; j < len; ++j)
+          memcpy(&h[((size_t)g * S + (size_t)(j % S)) * hd], src + ((size_t)g * len + j) * hd, (size_t)hd * 4);
+      e = hipMemcpyAsync(tmp, h.data(), per * 4, hipMemcpyHostToDevice, s->stream);
+      void* dst = (char*)(kv == 0 ? s->kc[i] : s->vc[i]) + (size_t)stream * per * esz;
+      if (e == hipSuccess) e = launch_f32_to_kv(tmp, dst, c.kv_dtype == SVL_BF16, per, s->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    }
+  }
+  int p32 = (int)len;
+  if (e == hipSuccess) e = hipMemcpyAsync(s->pos + stream, &p32, sizeof(int), hipMemcpyHostToDevice, s->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  hipFree(tmp);
+  HIP_TRY(e);
+  s->pos_host[stream] = len;
+  return 0;
+}
+
+int svl_state_layer_cache(const svl_state* s, int32_t stream, int32_t layer, float* keys, float* values, int64_t* len,
+                          int64_t* first) {
+  if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  const svl_config& c = s->m->cfg;
+  if (stream < 0 || stream >= s->B || layer < 0 || layer >= c.num_layers)
+    return set_error(SVL_ERR_INVALID_INPUT, "stream or layer out of range");
+  const int64_t p = s->pos_host[stream];
+  const int64_t L = p < s->slots ? p : s->slots;
+  if (len) *len = L;
+  if (first) *first = p - L;
+  if (!keys && !values) return 0;
+  HIP_TRY(hipSetDevice(s->m->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  const int KVH = c.num_kv_heads, hd = c.head_dim, S = s->slots;
+  const size_t per = (size_t)KVH * S * hd;
+  const int esz = c.kv_dtype == SVL_BF16 ? 2 : 4;
+  std::vector<float> h(per);
+  float* tmp;
+  HIP_TRY(hipMalloc(&tmp, per * 4));
+  hipError_t e = hipSuccess;
+  for (int kv = 0; kv < 2 && e == hipSuccess; ++kv) {
+    float* dst = kv == 0 ? keys : values;
+    if (!dst) continue;
+    const void* src = (const char*)(kv == 0 ? s->kc[layer] : s->vc[layer]) + (size_t)stream * per * esz;
+    e = launch_kv_to_f32(src, c.kv_dtype == SVL_BF16, tmp, per, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e == hipSuccess) e = hipMemcpy(h.data(), tmp, per * 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) break;
+    for (int g = 0; g < KVH; ++g)
+      for (int64_t j = 0; j < L; ++j)
+        memcpy(dst + ((size_t)g * L + j) * hd, &h[((size_t)g * S + (size_t)((p - L + j) % S)) * hd], (size_t)hd * 4);
+  }
+  hipFree(tmp);
+  HIP_TRY(e);
+  return 0;
+}
+
+int svl_state_positions(const svl_state* s, int64_t* positions) {
+  if (!s || !positions) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  for (int b = 0; b < s->B; ++b) positions[b] = s->pos_host[b];
+  return 0;
+}
+
+int svl_state_reset(svl_state* s) {
+  if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  HIP_TRY(hipSetDevice(s->m->device));
+  HIP_TRY(launch_fill_i32(s->pos, 0, s->B, s->stream));
+  HIP_TRY(launch_fill_u32(s->fb_tok, (uint32_t)std::max(s->m->cfg.text_card, 0), s->B, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  s->pos_host.assign(s->B, 0);
+  return 0;
+}
+
+void svl_state_destroy(svl_state* s) { delete s; }
+
+int svl_state_synchronize(svl_state* s) {
+  if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  HIP_TRY(hipSetDevice(s->m->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return 0;
+}
+
+void* svl_state_stream(const svl_state* s) { return s ? (void*)s->stream : nullptr; }
+
+int svl_transformer_forward(const svl_model* m, svl_state* s, const float* xs, int64_t t, float* ys) {
+  if (!m || !s || (t > 0 && (!xs || !ys))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  if (t < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative length");
+  if (t == 0) return 0;
+  TRY(check_room(s, t));
+  HIP_TRY(hipSetDevice(m->device));
+  const int d = m->cfg.d_model;
+  const size_t bytes = (size_t)s->B * t * d * 4;
+  TRY(ensure_in(s, 2 * bytes));
+  float* din = s->in;
+  float* dout = s->in + (size_t)s->B * t * d;
+  HIP_TRY(hipMemcpyAsync(din, xs, bytes, hipMemcpyHostToDevice, s->stream));
+  // One position at a time: causal attention makes this the same computation as the
+  // reference's block forward (transformer.rs:139-186).
+  for (int64_t i = 0; i < t; ++i) {
+    HIP_TRY(hipMemcpy2DAsync(s->x, (size_t)d * 4, din + (size_t)i * d, (size_t)t * d * 4, (size_t)d * 4, s->B,
+                             hipMemcpyDeviceToDevice, s->stream));
+    TRY(run_layers(m, s));
+    HIP_TRY(hipMemcpy2DAsync(dout + (size_t)i * d, (size_t)t * d * 4, s->x, (size_t)d * 4, (size_t)d * 4, s->B,
+                             hipMemcpyDeviceToDevice, s->stream));
+  }
+  HIP_TRY(hipMemcpyAsync(ys, dout, bytes, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return 0;
+}
+
+int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
+                 uint32_t* out_tokens, float* out_logits) {
+  if (!m || !s || !text_tokens || !audio_tokens || !out_tokens) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  const svl_config& c = m->cfg;
+  if (c.kind != SVL_MODEL_STT) return set_error(SVL_ERR_CONFIG, "not an STT model");
+  for (int b = 0; b < s->B; ++b) {
+    if (text_tokens[b] > (uint32_t)c.text_card)
+      return set_error(SVL_ERR_INVALID_INPUT, "text token %u out of range", text_tokens[b]);
+    for (int i = 0; i < c.n_q; ++i)
+      if (audio_tokens[(size_t)b * c.n_q + i] > (uint32_t)c.card)
+        return set_error(SVL_ERR_INVALID_INPUT, "audio token %u out of range", audio_tokens[(size_t)b * c.n_q + i]);
+  }
+  TRY(check_room(s, 1));
+  HIP_TRY(hipSetDevice(m->device));
+  uint32_t* dtext = s->tok_in;
+  uint32_t* daudio = s->tok_in + s->B;
+  HIP_TRY(hipMemcpyAsync(dtext, text_tokens, (size_t)s->B * 4, hipMemcpyHostToDevice, s->stream));
+  HIP_TRY(hipMemcpyAsync(daudio, audio_tokens, (size_t)s->B * c.n_q * 4, hipMemcpyHostToDevice, s->stream));
+  EmbedArgs e{};
+  e.text_emb = m->text_emb;
+  e.emb = m->emb_dev;
+  e.tables_bf16 = m->tables_bf16;
+  e.d = c.d_model;
+  e.n_q = c.n_q;
+  e.card = c.card;
+  e.text_card = c.text_card;
+  e.B = s->B;
+  e.text_tok = dtext;
+  e.fb_tok = s->fb_tok;
+  e.audio = daudio;
+  e.initial_at_zero = 0;
+  e.pos = s->pos;
+  e.x = s->x;
+  HIP_TRY(launch_embed(e, s->stream));
+  TRY(run_layers(m, s));
+  TRY(run_stt_head(m, s, s->tok_out));
+  HIP_TRY(hipMemcpyAsync(out_tokens, s->tok_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
+  if (out_logits)
+    HIP_TRY(hipMemcpyAsync(out_logits, s->logits, (size_t)s->B * c.text_card * 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return 0;
+}
+
+int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+                            uint32_t* d_out_tokens) {
+  if (!m || !s || (n_steps > 0 && (!d_audio_tokens || !d_out_tokens)))
+    return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  if (m->cfg.kind != SVL_MODEL_STT) return set_error(SVL_ERR_CONFIG, "not an STT model");
+  if (n_steps < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative step count");
+  HIP_TRY(hipSetDevice(m->device));
+  return stt_steps(m, s, n_steps, d_audio_tokens, d_out_tokens);
+}
+
+int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                      uint32_t* out_tokens) {
+  if (!m || !s || (n_steps > 0 && (!audio_tokens || !out_tokens))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  const svl_config& c = m->cfg;
+  if (c.kind != SVL_MODEL_STT) return set_error(SVL_ERR_CONFIG, "not an STT model");
+  if (n_steps < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative step count");
+  if (n_steps == 0) return 0;
+  const size_t na = (size_t)n_steps * s->B * c.n_q;
+  for (size_t i = 0; i < na; ++i)
+    if (audio_tokens[i] > (uint32_t)c.card) return set_error(SVL_ERR_INVALID_INPUT, "audio token %u out of range", audio_tokens[i]);
+  HIP_TRY(hipSetDevice(m->device));
+  uint32_t *da, *dout;
+  HIP_TRY(hipMalloc(&da, na * 4));
+  hipError_t e = hipMalloc(&dout, (size_t)n_steps * s->B * 4);
+  if (e != hipSuccess) {
+    hipFree(da);
+    HIP_TRY(e);
+  }
+  int rc = 0;
+  e = hipMemcpyAsync(da, audio_tokens, na * 4, hipMemcpyHostToDevice, s->stream);
+  if (e == hipSuccess) rc = stt_steps(m, s, n_steps, da, dout);
+  if (e == hipSuccess && rc == 0)
+    e = hipMemcpyAsync(out_tokens, dout, (size_t)n_steps * s->B * 4, hipMemcpyDeviceToHost, s->stream);
+  hipError_t e2 = hipStreamSynchronize(s->stream);
+  hipFree(da);
+  hipFree(dout);
+  if (rc) return rc;
+  HIP_TRY(e);
+  HIP_TRY(e2);
+  return 0;
+}
+
+int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
+  if (!m || !s || !out_z) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  const svl_config& c = m->cfg;
+  if (c.kind != SVL_MODEL_TTS) return set_error(SVL_ERR_CONFIG, "not a TTS model");
+  TRY(check_room(s, 1));
+  HIP_TRY(hipSetDevice(m->device));
+  const int d = c.d_model, ld = c.latent_dim;
+  TRY(ensure_in(s, (size_t)s->B * ld * 4));
+  const float* in;
+  if (latent) {
+    HIP_TRY(hipMemcpyAsync(s->in, latent, (size_t)s->B * ld * 4, hipMemcpyHostToDevice, s->stream));
+    in = s->in;
+  } else {
+    for (int b = 0; b < s->B; ++b)
+      HIP_TRY(hipMemcpyAsync(s->in + (size_t)b * ld, m->bos, (size_t)ld * 4, hipMemcpyDeviceToDevice, s->stream));
+    in = s->in;
+  }
+  GemvArgs g{};
+  g.B = s->B;
+  g.L = m->input_linear;
+  g.x = in;
+  g.x_stride = ld;
+  g.norm = NORM_NONE;
+  g.epi = EPI_STORE;
+  g.y = s->x;
+  g.y_stride = d;
+  HIP_TRY(launch_gemv(g, s->stream));
+  TRY(run_layers(m, s));
+  const int zd = c.z_dim > 0 ? c.z_dim : d;
+  if (c.z_dim > 0) {
+    GemvArgs z{};
+    z.B = s->B;
+    z.L = m->z_proj;
+    z.x = s->x;
+    z.x_stride = d;
+    z.norm = NORM_LAYER;
+    z.nw = m->out_norm_w;
+    z.nb = m->out_norm_b;
+    z.eps = 1e-5f;  // SVL/tts/flow_lm.rs:176
+    z.epi = EPI_STORE;
+    z.y = s->z;
+    z.y_stride = zd;
+    HIP_TRY(launch_gemv(z, s->stream));
+  } else {
+    HIP_TRY(launch_norm(s->x, d, s->z, d, s->B, d, NORM_LAYER, m->out_norm_w, m->out_norm_b, 1e-5f, s->stream));
+  }
+  HIP_TRY(hipMemcpyAsync(out_z, s->z, (size_t)s->B * zd * 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return 0;
+}
+
+}  // extern "C"

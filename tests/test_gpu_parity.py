@@ -1,0 +1,245 @@
+"""GPU parity: libsvl (HIP, through the C ABI) against the oracle on the same seeded inputs.
+
+Bars (from the step's contract):
+  * quantization / dequantization of weights: bit-exact to the oracle's candle restatement
+  * logits: max-abs 1e-4 for f32 models; 2e-2 for bf16 and Q8_0 models (reduced-precision
+    weights: an activation re-quantization can round one Q8_0 step differently when inputs
+    differ in the last ulp)
+  * greedy tokens: identical over 256 steps
+  * lockstep batches: bit-identical to the same streams run one by one
+Reduced shapes keep the structure (GQA/windows wrap, gated SiLU, RMSNorm / LayerNorm) and let
+the oracle finish in seconds; the full-size STT-1B Q8_0 run checks the 256-step greedy
+identity at the benchmark shape.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import svl
+from svl import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+LOWP_TOL = 2e-2
+
+
+def build(shape, dtype, seed=0, fast=False, kv_dtype=svl.F32):
+    t = (W.make_weights_fast if fast else W.make_weights)(shape, dtype, seed=seed)
+    q = W.quantize_code(dtype)
+    return t, svl.Model(shape.config(q), t, kv_dtype=kv_dtype), oracle.Model(shape.config(q), t)
+
+
+def _tensor_for(name, shape):
+    if name == "text_linear":
+        return "text_linear.weight"
+    layer, which = name.split(".")
+    p = f"transformer.layers.{layer}."
+    return p + {"in_proj": "self_attn.in_proj_weight", "out_proj": "self_attn.out_proj.weight",
+                "ff1": "gating.linear_in.weight", "ff2": "gating.linear_out.weight"}[which]
+
+
+def test_q8_0_quantize_and_dequantize_bit_exact():
+    s = W.S1_SMALL
+    t, g, _ = build(s, "q8_0", seed=1)
+    for name in ["text_linear", "0.in_proj", "1.out_proj", "2.ff1", "2.ff2"]:
+        w = t[_tensor_for(name, s)][2]
+        f32, blocks = g.linear_weight(name)
+        ob = oracle.quantize_q8_0(w)
+        assert np.array_equal(blocks, ob), name
+        assert np.array_equal(f32.view(np.uint32), oracle.dequantize_q8_0(ob, w.shape[1]).view(np.uint32)), name
+
+
+def test_q8_0_candle_blocks_round_trip():
+    s = W.S1_SMALL
+    t = W.make_weights(s, "q8_0", seed=2)
+    blocked = dict(t)
+    for name, (dt, shp, data) in t.items():
+        if dt == W.F32 and len(shp) == 2:
+            blocked[name] = (W.Q8_0, shp, oracle.quantize_q8_0(data))
+    g = svl.Model(s.config(0), blocked)
+    f32, blocks = g.linear_weight("0.in_proj")
+    assert np.array_equal(blocks, blocked["transformer.layers.0.self_attn.in_proj_weight"][2])
+
+
+@pytest.mark.parametrize("dtype,tol", [("q8_0", LOWP_TOL), ("bf16", LOWP_TOL), ("f32", F32_TOL)])
+def test_stt_small_steps_match_oracle(dtype, tol):
+    """64 steps through a window of 24 (the ring wraps twice): logits within tolerance, tokens equal."""
+    s = W.S1_SMALL
+    _, g, o = build(s, dtype, seed=3)
+    gs, os_ = g.init_state(), o.new_state()
+    audio = W.audio_tokens(s, 64, seed=4)[0]
+    text = s.text_card
+    worst = 0.0
+    for i in range(64):
+        tg, lg = g.step([text], audio[i][None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, audio[i], want_logits=True)
+        worst = max(worst, float(np.max(np.abs(lg[0] - lo))))
+        assert tg[0] == to, f"step {i}"
+        text = int(tg[0])
+    assert worst < tol, worst
+    print(f"{dtype}: max |logit diff| over 64 steps = {worst:.3g}")
+
+
+def test_stt_small_recognize_matches_oracle_greedy():
+    s = W.S1_SMALL
+    _, g, o = build(s, "q8_0", seed=5)
+    audio = W.audio_tokens(s, 200, seed=6)[0]
+    got = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    assert np.array_equal(got, o.new_state().stt_greedy(audio))
+
+
+def test_lockstep_batch_equals_independent_streams():
+    s = W.S1_SMALL
+    _, g, _ = build(s, "q8_0", seed=7)
+    B, n = 5, 40
+    audio = W.audio_tokens(s, n, seed=8, batch=B)  # [B, n, n_q]
+    st = g.init_state(batch=B)
+    # streams start at different positions: prefill stream b with b*3 seeded keys
+    caches = {}
+    for b in range(B):
+        ks, vs = W.prefill_caches(s, 3 * b, seed=20 + b)
+        caches[b] = (ks, vs)
+        st.load_stream(b, ks, vs)
+    batched = g.recognize(audio.transpose(1, 0, 2), st)
+    for b in range(B):
+        one = g.init_state()
+        one.load_stream(0, *caches[b])
+        assert np.array_equal(g.recognize(audio[b][:, None, :], one)[:, 0], batched[:, b]), b
+
+
+def test_state_duplicate_reset_and_caches():
+    s = W.S1_SMALL
+    _, g, o = build(s, "f32", seed=9)
+    audio = W.audio_tokens(s, 30, seed=10)[0]
+    st = g.init_state()
+    g.recognize(audio[:10, None], st)
+    dup = st.duplicate()
+    a = g.recognize(audio[10:, None], st)
+    b = g.recognize(audio[10:, None], dup)
+    assert np.array_equal(a, b)
+    # layer caches: the last `context` keys, equal to the oracle's within f32 tolerance
+    os_ = o.new_state()
+    os_.stt_greedy(audio)
+    for layer, (k, v, first) in enumerate(st.layer_caches()):
+        ok, ov, ostart = os_.cache(layer)
+        n = k.shape[1]
+        assert first == 30 - n and n == s.context
+        assert np.max(np.abs(k - ok[0, :, -n:])) < 1e-4 and np.max(np.abs(v - ov[0, :, -n:])) < 1e-4
+    st.reset()
+    assert np.array_equal(g.recognize(audio[:10, None], st), g.recognize(audio[:10, None], g.init_state()))
+
+
+def test_tts_small_prefilled_matches_oracle():
+    s = W.T1_SMALL
+    _, g, o = build(s, "f32", seed=11)
+    ks, vs = W.prefill_caches(s, 40, seed=12)
+    gs = g.state_from_layer_caches(ks, vs, capacity=128)
+    os_ = o.state_from_layer_caches(ks, vs)
+    lat = W.latents(s, 12, seed=13)
+    for i in range(12):
+        z = g.backbone_step(None if i == 0 else lat[i][None], gs)[0]
+        zo = os_.tts_step(None if i == 0 else lat[i])
+        assert np.max(np.abs(z - zo)) < F32_TOL, i
+
+
+def test_transformer_forward_matches_oracle():
+    s = W.Shape("fwd", W.MODEL_TRANSFORMER, 128, 2, 2, 1, 64, W.FF_PLAIN, 256, W.NORM_LAYER, 1e-5, 7,
+                layer_scale=1)
+    t = W.make_weights(s, "f32", seed=14)
+    g, o = svl.Model(s.config(0), t), oracle.Model(s.config(0), t)
+    xs = np.random.default_rng(15).standard_normal((1, 20, 128)).astype(np.float32)
+    gs, os_ = g.init_state(), o.new_state()
+    y1 = g.forward(xs[:, :13], gs)
+    y2 = g.forward(xs[:, 13:], gs)
+    yo = os_.forward(xs)
+    assert np.max(np.abs(np.concatenate([y1, y2], axis=1) - yo)) < F32_TOL
+    assert gs.positions[0] == 20
+
+
+def test_bf16_kv_cache_stays_within_low_precision_bar():
+    s = W.S1_SMALL
+    _, g, o = build(s, "f32", seed=16, kv_dtype=svl.BF16)
+    gs, os_ = g.init_state(), o.new_state()
+    audio = W.audio_tokens(s, 30, seed=17)[0]
+    text = s.text_card
+    for i in range(30):
+        tg, lg = g.step([text], audio[i][None], gs, want_logits=True)
+        _, lo = os_.stt_step(text, audio[i], want_logits=True)
+        assert np.max(np.abs(lg[0] - lo)) < LOWP_TOL
+        text = int(tg[0])
+
+
+def test_input_errors():
+    s = W.S1_SMALL
+    _, g, _ = build(s, "f32", seed=18)
+    st = g.init_state()
+    with pytest.raises(svl.SvlError) as e:
+        g.step([s.text_card + 1], np.zeros((1, s.n_q)), st)
+    assert e.value.code == svl.ERR_INVALID_INPUT
+    with pytest.raises(svl.SvlError) as e:
+        g.recognize(np.full((2, 1, s.n_q), s.card + 1), st)
+    assert e.value.code == svl.ERR_INVALID_INPUT
+    assert st.positions[0] == 0  # rejected inputs leave the state untouched
+    t = W.make_weights(W.T1_SMALL, "f32")
+    gt = svl.Model(W.T1_SMALL.config(0), t)
+    full = gt.init_state(capacity=2)
+    gt.backbone_step(None, full)
+    gt.backbone_step(None, full)
+    with pytest.raises(svl.SvlError) as e:
+        gt.backbone_step(None, full)
+    assert e.value.code == svl.ERR_INVALID_INPUT
+    with pytest.raises(svl.SvlError):
+        gt.init_state(capacity=0)
+    bad = dict(t)
+    bad["input_linear.weight"] = (W.F32, (3, 3), np.zeros((3, 3), np.float32))
+    with pytest.raises(svl.SvlError) as e:
+        svl.Model(W.T1_SMALL.config(0), bad)
+    assert e.value.code == svl.ERR_INVALID_INPUT
+
+
+# ---- benchmark shapes -------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def s1_q8():
+    oracle.set_threads(min(16, os.cpu_count() or 4))
+    t, g, o = build(W.S1, "q8_0", seed=0, fast=True)
+    del t
+    return g, o
+
+
+def test_s1_q8_0_256_greedy_steps_token_identical(s1_q8):
+    """STT-1B shape, Q8_0, batch 1, window 750: 256 greedy steps equal the oracle's."""
+    g, o = s1_q8
+    audio = W.audio_tokens(W.S1, 256, seed=1)[0]
+    got = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    expected = o.new_state().stt_greedy(audio)
+    assert np.array_equal(got, expected), np.flatnonzero(got != expected)[:5]
+
+
+def test_s1_q8_0_logits_within_bar(s1_q8):
+    g, o = s1_q8
+    audio = W.audio_tokens(W.S1, 6, seed=2)[0]
+    gs, os_ = g.init_state(), o.new_state()
+    text = W.S1.text_card
+    for i in range(6):
+        tg, lg = g.step([text], audio[i][None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, audio[i], want_logits=True)
+        assert np.max(np.abs(lg[0] - lo)) < LOWP_TOL and tg[0] == to
+        text = to
+
+
+def test_t1_f32_prefilled_256_within_f32_bar():
+    """Pocket-TTS shape, f32, 256 prefilled positions, 16 steps: z within 1e-4."""
+    s = W.T1
+    t, g, o = build(s, "f32", seed=0, fast=True)
+    ks, vs = W.prefill_caches(s, 256, seed=3)
+    gs = g.state_from_layer_caches(ks, vs, capacity=512)
+    os_ = o.state_from_layer_caches(ks, vs)
+    lat = W.latents(s, 16, seed=4)
+    for i in range(16):
+        z = g.backbone_step(lat[i][None], gs)[0]
+        zo = os_.tts_step(lat[i])
+        assert np.max(np.abs(z - zo)) < F32_TOL, i

@@ -1,0 +1,62 @@
+"""libsvl.so loads and exports every function include/svl.h declares; host-side validation
+that needs no GPU (configuration errors are reported before any device call)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import svl
+from svl import workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "svl.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(svl_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_surface():
+    assert declared_functions() == sorted(svl.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(svl.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_oracle_library_loads():
+    import oracle
+
+    L = oracle.lib()
+    for name in ["svlo_model_create", "svlo_stt_step", "svlo_quantize_q8_0", "svlo_attention"]:
+        assert hasattr(L, name)
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 96, svl.ERR_CONFIG),
+    ("num_kv_heads", 3, svl.ERR_CONFIG),
+    ("ff_hidden", 100, svl.ERR_CONFIG),
+    ("context", -1, svl.ERR_CONFIG),
+    ("kv_dtype", svl.Q8_0, svl.ERR_CONFIG),
+    ("n_q", 0, svl.ERR_CONFIG),
+])
+def test_config_errors_before_device_access(field, value, code):
+    cfg = W.S1_SMALL.config(0)
+    cfg[field] = value
+    with pytest.raises(svl.SvlError) as e:
+        svl.Model(cfg, {}, kv_dtype=cfg.get("kv_dtype", 0))
+    assert e.value.code == code
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(svl.SvlError):
+        saved = svl._lib
+        svl._lib = None
+        try:
+            svl.load_library(str(tmp_path / "libsvl.so"))
+        finally:
+            svl._lib = saved

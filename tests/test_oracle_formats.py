@@ -1,0 +1,208 @@
+"""Pins the oracle's weight formats (f16/bf16 conversion, candle Q8_0 / Q4K / Q8K blocks).
+
+The reference ships no golden vectors for these (candle is not vendored); they are pinned by
+library routines (numpy float16, torch bfloat16), hand-built known answers whose expected values
+come from exact rational arithmetic, and invariants chosen so that a plausible mistake (wrong
+rounding mode, swapped scale/min bits, dropped min term) fails.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+
+def test_f16_to_f32_exhaustive_matches_numpy():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    expected = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_bits_to_f32(int(b)) for b in bits], dtype=np.float32)
+    finite = np.isfinite(expected)
+    assert np.array_equal(got[finite].view(np.uint32), expected[finite].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(expected)]))
+    assert np.array_equal(np.isinf(got), np.isinf(expected))
+
+
+def test_f32_to_f16_round_to_nearest_even_matches_numpy():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200_000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 200_000).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, 6e-8, 3e-8, 2.9802322e-08,
+                  5.960464477539063e-08, 1.0009765625, 1.00048828125, 1.00146484375, np.inf, -np.inf],
+                 dtype=np.float32),
+    ])
+    got = oracle.f32_to_f16_bits(x)
+    expected = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, expected)
+    # every f16 value round-trips
+    halfs = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    halfs = halfs[np.isfinite(halfs)]
+    assert np.array_equal(oracle.f32_to_f16_bits(halfs.astype(np.float32)), halfs.view(np.uint16))
+
+
+def test_bf16_round_to_nearest_even_matches_torch():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(300_000).astype(np.float32) * np.float32(3.0) ** rng.integers(-20, 20, 300_000).astype(np.float32)
+    # exact ties: low 16 bits 0x8000, both parities of the kept lsb
+    ties = (np.arange(1000, dtype=np.uint32) << 16 | 0x3F800000 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties])
+    got = oracle.f32_to_bf16_bits(x)
+    expected = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, expected)
+
+
+# ---- Q8_0 ---------------------------------------------------------------------------------
+
+def _blocks(raw: np.ndarray):
+    """Splits [n*34] bytes into (f16 scales as f32, int8 quants [n, 32])."""
+    raw = raw.reshape(-1, 34)
+    d = raw[:, :2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    q = raw[:, 2:].copy().view(np.int8)
+    return d, q
+
+
+def test_q8_0_known_answer_rounds_half_away_from_zero():
+    # amax 127 -> d = 1 exactly, so q = round(x) with ties away from zero (f32::round).
+    x = np.zeros(32, dtype=np.float32)
+    x[:8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -3.49, 3.51]
+    d, q = _blocks(oracle.quantize_q8_0(x))
+    assert d[0] == 1.0
+    assert q[0, :8].tolist() == [127, 3, -3, 1, -1, 2, -3, 4]
+    assert np.all(q[0, 8:] == 0)
+
+
+def test_q8_0_known_answer_exact_rationals():
+    # x_j = (j - 16) / 100: the expected quants from exact arithmetic on the f32 inputs.
+    x = (np.arange(32, dtype=np.float32) - 16) / np.float32(100.0)
+    d, q = _blocks(oracle.quantize_q8_0(x))
+    amax = max(abs(Fraction(float(v))) for v in x)
+    d_exact = amax / 127
+    assert d[0] == np.float32(np.float16(np.float32(float(d_exact))))
+    for j in range(32):
+        r = Fraction(float(x[j])) / d_exact
+        frac = abs(r - int(r))
+        if abs(frac - Fraction(1, 2)) < Fraction(1, 10_000):
+            continue  # too close to a tie for f32 arithmetic to be decided by rationals
+        expected = int(r + (Fraction(1, 2) if r > 0 else Fraction(-1, 2)))
+        assert q[0, j] == expected, j
+
+
+def test_q8_0_invariants():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((64, 256)) * 0.02).astype(np.float32)
+    raw = oracle.quantize_q8_0(x)
+    d, q = _blocks(raw)
+    xb = x.reshape(-1, 32)
+    # the largest magnitude of every block maps to +-127; zero block -> zero scale
+    assert np.all(np.abs(q).max(axis=1) == 127)
+    # dequantization is the closed form q * f32(f16 d), bit for bit
+    deq = oracle.dequantize_q8_0(raw, 256).reshape(-1, 32)
+    assert np.array_equal(deq.view(np.uint32), (q.astype(np.float32) * d[:, None]).view(np.uint32))
+    # reconstruction within half a step (plus the f16 rounding of d)
+    step = np.abs(xb).max(axis=1) / 127
+    assert np.all(np.abs(deq - xb) <= 0.51 * step[:, None] + 127 * np.abs(d - step)[:, None] + 1e-12)
+    # odd symmetry
+    _, qn = _blocks(oracle.quantize_q8_0(-x))
+    assert np.array_equal(qn, -q)
+    z_d, z_q = _blocks(oracle.quantize_q8_0(np.zeros(32, np.float32)))
+    assert z_d[0] == 0 and np.all(z_q == 0)
+
+
+def test_q8_0_vec_dot():
+    # integer-valued blocks with unit scales: the dot is an exact integer
+    w = np.zeros(64, np.float32)
+    x = np.zeros(64, np.float32)
+    w[0], x[0] = 127.0, 127.0
+    w[1:32] = np.arange(1, 32)
+    x[1:32] = -np.arange(1, 32)[::-1]
+    w[32], x[32] = -127.0, 127.0
+    w[40], x[40] = 5.0, 7.0
+    wb, xb = oracle.quantize_q8_0(w), oracle.quantize_q8_0(x)
+    expected = 127 * 127 + float(np.dot(np.arange(1, 32), -np.arange(1, 32)[::-1])) - 127 * 127 + 35
+    assert oracle.vec_dot_q8_0(wb, xb, 64) == expected
+    # random rows: equals sum_b (sum_i qw qx) * dw * dx up to f32 rounding
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal(2048) * 0.02).astype(np.float32)
+    x = rng.standard_normal(2048).astype(np.float32)
+    wb, xb = oracle.quantize_q8_0(w), oracle.quantize_q8_0(x)
+    dw, qw = _blocks(wb)
+    dx, qx = _blocks(xb)
+    exact = float(np.sum((qw.astype(np.int64) * qx).sum(axis=1) * dw.astype(np.float64) * dx.astype(np.float64)))
+    assert abs(oracle.vec_dot_q8_0(wb, xb, 2048) - exact) <= 1e-5 * abs(exact) + 1e-6
+    # and approximates the float dot
+    assert abs(exact - float(np.dot(w.astype(np.float64), x))) < 0.02 * np.linalg.norm(w) * np.linalg.norm(x)
+
+
+# ---- Q4K / Q8K ------------------------------------------------------------------------------
+
+def _pack_scales(sc, mn):
+    """GGML Q4K 12-byte packing of eight 6-bit scales and mins (inverse of get_scale_min_k4)."""
+    s = [0] * 12
+    for j in range(8):
+        if j < 4:
+            s[j] = sc[j]
+            s[j + 4] = mn[j]
+        else:
+            s[j + 4] = (sc[j] & 0xF) | ((mn[j] & 0xF) << 4)
+            s[j - 4] |= (sc[j] >> 4) << 6
+            s[j] |= (mn[j] >> 4) << 6
+    return bytes(s)
+
+
+def _q4k_block(d, dmin, sc, mn, q):
+    """q: 256 nibbles in value order; element 64*i + l uses byte 32*i + l, low nibble for
+    l < 32, high nibble for the next 32."""
+    qs = bytearray(128)
+    for i in range(4):
+        for l in range(32):
+            qs[32 * i + l] = q[64 * i + l] | (q[64 * i + 32 + l] << 4)
+    head = np.array([d, dmin], dtype=np.float16).tobytes()
+    return np.frombuffer(head + _pack_scales(sc, mn) + bytes(qs), dtype=np.uint8)
+
+
+def test_q4k_dequant_known_answer():
+    sc = [1, 7, 13, 63, 33, 48, 2, 60]
+    mn = [0, 5, 63, 17, 40, 1, 31, 62]
+    q = [(3 * i + i // 32) % 16 for i in range(256)]
+    blk = _q4k_block(0.25, 0.125, sc, mn, q)
+    got = oracle.dequantize_q4k(blk, 256)
+    expected = np.array([0.25 * sc[i // 32] * q[i] - 0.125 * mn[i // 32] for i in range(256)], dtype=np.float64)
+    assert np.array_equal(got.astype(np.float64), expected)
+
+
+def test_q4k_quantize_reconstruction_and_vec_dot():
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((16, 512)) * 0.02).astype(np.float32)
+    raw = oracle.quantize_q4k(w)
+    deq = oracle.dequantize_q4k(raw, 512)
+    # 4-bit codes over each 32-value sub-block's range: error within about one step
+    sub = w.reshape(-1, 32)
+    rng_sub = sub.max(axis=1) - np.minimum(sub.min(axis=1), 0)
+    err = np.abs(deq.reshape(-1, 32) - sub).max(axis=1)
+    assert np.all(err <= rng_sub / 15 * 1.05 + 1e-7)
+    # Q8K activation blocks: d * q reconstructs x; the largest magnitude maps to -128
+    x = rng.standard_normal(512).astype(np.float32)
+    xb = oracle.quantize_q8k(x).reshape(2, 292)
+    d = xb[:, :4].copy().view(np.float32).reshape(-1)
+    qx = xb[:, 4:260].copy().view(np.int8)
+    bsums = xb[:, 260:].copy().view(np.int16)
+    assert np.array_equal(bsums, qx.reshape(2, 16, 16).astype(np.int32).sum(axis=2).astype(np.int16))
+    for b in range(2):
+        i = np.argmax(np.abs(x[256 * b:256 * (b + 1)]))
+        assert qx[b, i] == -128
+    assert np.all(np.abs(d[:, None] * qx - x.reshape(2, 256)) <= np.abs(d)[:, None] * 0.5 + 1e-6)
+    # vec_dot == dot of the dequantized operands (integer parts exact, f32 scaling rounding)
+    xdeq = (d[:, None].astype(np.float64) * qx).reshape(-1)
+    for r in range(16):
+        exact = float(np.dot(deq[r].astype(np.float64), xdeq))
+        got = oracle.vec_dot_q4k_q8k(raw[r], oracle.quantize_q8k(x), 512)
+        assert abs(got - exact) <= 2e-6 * (np.abs(deq[r]).astype(np.float64) @ np.abs(xdeq)) + 1e-7
+
+
+def test_q4k_min_term_matters():
+    # A sub-block shifted far from zero needs its min: a dropped min term would fail this.
+    x = np.full(256, 0.5, dtype=np.float32) + np.linspace(0, 0.1, 256, dtype=np.float32)
+    x[:32] -= 1.0
+    deq = oracle.dequantize_q4k(oracle.quantize_q4k(x), 256)
+    assert np.max(np.abs(deq - x)) < 0.02
