@@ -184,17 +184,38 @@ int svlo_attention(const float* q, const float* k, const float* v, float* out, s
                                   position, first_key, context);
 }
 
-/* [candle hypothesis] candle-nn ops::rms_norm CPU: sum of squares in f32, m = sqrt(sum2 / dim
- * + eps), y = x / m * alpha.  Call sites SVL/nn/transformer.rs:286, SVL/stt/model.rs:252. */
+/* Sum of f(x_i) over a row in the order shared with the GPU kernels: 64 strided partials
+ * (partial l sums x[l], x[l+64], ... sequentially), then a butterfly over the partials
+ * (p[l] + p[l ^ o] for o = 32, 16, 8, 4, 2, 1; every lane ends with the same value, lane 0's
+ * is returned).  candle's CPU reductions (Iterator::sum) are not available here to pin
+ * their order; this is the one order both sides of the parity check use. */
+static float blocked_sum(const float* x, size_t n, int squares) {
+    float p[64];
+    for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (size_t i = (size_t)l; i < n; i += 64) {
+            float v = x[i];
+            if (squares) v = v * v;
+            acc += v;
+        }
+        p[l] = acc;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ o];
+        memcpy(p, q, sizeof(p));
+    }
+    return p[0];
+}
+
+/* [candle hypothesis] candle-nn ops::rms_norm CPU: m = sqrt(sum(x^2) / dim + eps),
+ * y = x / m * alpha (sum in the blocked order above).  Call sites SVL/nn/transformer.rs:286,
+ * SVL/stt/model.rs:252. */
 void svlo_rms_norm(const float* x, const float* alpha, float* y, size_t rows, size_t dim, float eps) {
     for (size_t r = 0; r < rows; ++r) {
         const float* s = x + r * dim;
         float* d = y + r * dim;
-        float sum2 = 0.0f;
-        for (size_t i = 0; i < dim; ++i) {
-            float p = s[i] * s[i];
-            sum2 += p;
-        }
+        float sum2 = blocked_sum(s, dim, 1);
         float m = sqrtf(sum2 / (float)dim + eps);
         for (size_t i = 0; i < dim; ++i) {
             float t = s[i] / m;
@@ -203,20 +224,16 @@ void svlo_rms_norm(const float* x, const float* alpha, float* y, size_t rows, si
     }
 }
 
-/* [candle hypothesis] candle-nn ops::layer_norm CPU: single pass sum and sum of squares,
- * var = E[x^2] - mean^2, y = (x - mean) * (1/sqrt(var + eps)) * w + b.
- * Call sites SVL/nn/transformer.rs:284, SVL/tts/flow_lm.rs:176. */
+/* [candle hypothesis] candle-nn ops::layer_norm CPU: mean = sum(x) / dim,
+ * var = sum(x^2) / dim - mean^2, y = (x - mean) * (1 / sqrt(var + eps)) * w + b (sums in the
+ * blocked order above).  Call sites SVL/nn/transformer.rs:284, SVL/tts/flow_lm.rs:176. */
 void svlo_layer_norm(const float* x, const float* w, const float* b, float* y, size_t rows,
                      size_t dim, float eps) {
     for (size_t r = 0; r < rows; ++r) {
         const float* s = x + r * dim;
         float* d = y + r * dim;
-        float sum = 0.0f, sum2 = 0.0f;
-        for (size_t i = 0; i < dim; ++i) {
-            sum += s[i];
-            float p = s[i] * s[i];
-            sum2 += p;
-        }
+        float sum = blocked_sum(s, dim, 0);
+        float sum2 = blocked_sum(s, dim, 1);
         float mean = sum / (float)dim;
         float mm = mean * mean;
         float var = sum2 / (float)dim - mm;

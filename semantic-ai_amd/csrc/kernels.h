@@ -24,6 +24,7 @@ struct LinearDev {
 struct GemvArgs {
   LinearDev L;
   int B;               // batch rows (grid.y)
+  int ipw;             // work items per workgroup (set by launch_gemv)
   const float* x;      // input [B][x_stride]
   int x_stride;
   int norm;            // NormKind applied to x in the prologue
@@ -39,7 +40,7 @@ struct GemvArgs {
   int ff_hidden;       // SILU: gate rows j, value rows j + ff_hidden
   // QKV_ROPE
   int* pos;            // [B] positions (read by QKV_ROPE, advanced when advance_pos)
-  const float* inv_freq;
+  const float* rope;   // [positions][hd/2][cos, sin] computed on the host
   int H, KVH, hd;
   float* q_out;        // [B][H*hd]
   void* kc;            // [B][KVH][cap][hd]
@@ -57,17 +58,13 @@ struct AttnArgs {
   int B, H, KVH, hd, cap, window;  // window 0 = unlimited
   int kv_bf16;
   float scale;
-  int chunk;           // keys per workgroup
-  int nsplit;          // grid.x (max splits)
-  float* pm;           // [B][H][nsplit]
-  float* pl;
-  float* po;           // [B][H][nsplit][hd]
+  float* scores;       // [B][H][cap] scratch: scaled q.k of the visible keys
   float* out;          // [B][H*hd]
 };
 
 struct EmbedArgs {
   const void* text_emb;     // [text_card+1][d]
-  const void* const* emb;   // device array of n_q table pointers, each [card+1][d]
+  const void* emb;          // n_q tables back to back, [n_q][card+1][d]
   int tables_bf16;
   int d, n_q, card, text_card, B;
   const uint32_t* text_tok; // [B] or null: use fb_tok

@@ -21,68 +21,61 @@ constexpr int kThreads = 256;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-constexpr int kWaves = kThreads / kWave;
 
 // ---------------------------------------------------------------------------------------------
-// GEMV prologue: x (one batch row) -> LDS, optional norm, optional Q8_0 quantization.
+// Row statistics in the order shared with the oracle: 64 strided partials (lane l sums
+// x[l], x[l+64], ... sequentially), then a butterfly over the partials (offsets 32 .. 1).
+// Every lane of every wave computes the same value, so no cross-wave exchange is needed.
 
-__device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
-  a = wave_sum(a);
-  b = wave_sum(b);
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (lane == 0) {
-    red[wave] = a;
-    red[kWaves + wave] = b;
+__device__ __forceinline__ float blocked_sum(const float* xs, int K, bool squares) {
+  const int lane = threadIdx.x % kWave;
+  float acc = 0.0f;
+  for (int i = lane; i < K; i += kWave) {
+    float v = xs[i];
+    if (squares) v = v * v;
+    acc = acc + v;
   }
-  __syncthreads();
-  a = 0.0f;
-  b = 0.0f;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    a += red[w];
-    b += red[kWaves + w];
-  }
-  __syncthreads();
+  for (int o = 32; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, kWave);
+  return acc;
 }
 
-// Normalizes xs[0..K) in LDS in place (candle-nn rms_norm / layer_norm CPU formulas).
-__device__ void norm_lds(float* xs, int K, int norm, const float* nw, const float* nb, float eps,
-                         float* red) {
-  float s = 0.0f, s2 = 0.0f;
-  for (int i = threadIdx.x; i < K; i += kThreads) {
-    float v = xs[i];
-    s += v;
-    float p = v * v;
-    s2 += p;
-  }
-  block_sum2(s, s2, red);
+// Normalizes xs[0..K) in LDS in place: candle-nn rms_norm (x / m * alpha,
+// m = sqrt(sum(x^2) / K + eps)) or layer_norm ((x - mean) * (1 / sqrt(var + eps)) * w + b,
+// var = sum(x^2) / K - mean^2).  Callers synchronize before and after.
+__device__ void norm_lds(float* xs, int K, int norm, const float* nw, const float* nb, float eps) {
   if (norm == NORM_RMS) {
-    float m = sqrtf(s2 / (float)K + eps);
-    for (int i = threadIdx.x; i < K; i += kThreads) {
+    const float s2 = blocked_sum(xs, K, true);
+    const float m = sqrtf(s2 / (float)K + eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
       float t = xs[i] / m;
       xs[i] = t * nw[i];
     }
   } else {
-    float mean = s / (float)K;
-    float mm = mean * mean;
-    float var = s2 / (float)K - mm;
-    float inv_std = 1.0f / sqrtf(var + eps);
-    for (int i = threadIdx.x; i < K; i += kThreads) {
+    const float s = blocked_sum(xs, K, false);
+    const float s2 = blocked_sum(xs, K, true);
+    const float mean = s / (float)K;
+    const float mm = mean * mean;
+    const float var = s2 / (float)K - mm;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
       float t = (xs[i] - mean) * inv_std;
       t = t * nw[i];
       xs[i] = t + nb[i];
     }
   }
-  __syncthreads();
 }
 
 // Q8_0 activation quantization of xs[0..K) into xq (int8) and xdq (the f16-rounded block
-// scales as f32).  Each half-wave quantizes one 32-value block: lane = element.
+// scales as f32): candle's BlockQ8_0::from_float.  A half-wave owns one block per iteration
+// (lane = element); the shuffles stay inside the half.
 __device__ void quantize_lds(const float* xs, int K, int8_t* xq, float* xdq) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int nwaves = blockDim.x / kWave;
   const int nb = K / 32;
-  // A half-wave owns one block per iteration; shuffles stay inside the half.
-  for (int blk = wave * 2 + lane / 32; blk < nb; blk += kWaves * 2) {
+  for (int blk = wave * 2 + lane / 32; blk < nb; blk += nwaves * 2) {
     float v = xs[blk * 32 + (lane % 32)];
     float amax = half_max(fabsf(v));
     float d = amax / 127.0f;
@@ -90,146 +83,62 @@ __device__ void quantize_lds(const float* xs, int K, int8_t* xq, float* xdq) {
     xq[blk * 32 + (lane % 32)] = (int8_t)sat_i8(roundf(v * id));
     if ((lane % 32) == 0) xdq[blk] = f16_to_f32(f32_to_f16(d));
   }
+}
+
+// Loads one batch row of the input into LDS and applies the prologue norm.
+__device__ void stage_input(const GemvArgs& a, int b, float* xs) {
+  const int K = a.L.in;
+  const float* x = a.x + (size_t)b * a.x_stride;
+  for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = x[i];
   __syncthreads();
+  if (a.norm != NORM_NONE) {
+    norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
-// GEMV main loops.  Each wave computes R consecutive work items; a work item is one output
-// row, or for the SiLU gate a (gate row j, value row j + F) pair.
+// Epilogues.  `item` is the workgroup-local work item; `y` its row value and `yp` the value of
+// the RoPE partner row (row ^ 1), both from the workgroup's row results.
 
-__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-
-template <int NR>
-__device__ __forceinline__ void dot_rows_q8(const LinearDev& L, const int* rows, const int8_t* xq,
-                                            const float* xdq, float* acc) {
-  const int lane = threadIdx.x % kWave;
-  const int K = L.in, nb = K / 32;
-  const int8_t* wq = (const int8_t*)L.w;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
-  for (int b = lane; b < nb; b += kWave) {
-    v4i wa[NR], wb[NR];
-    uint16_t wd[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const v4i* p = (const v4i*)(wq + (size_t)rows[r] * K + (size_t)b * 32);
-      wa[r] = __builtin_nontemporal_load(p);
-      wb[r] = __builtin_nontemporal_load(p + 1);
-      wd[r] = L.scale[(size_t)rows[r] * nb + b];
-    }
-    const v4i xa = *(const v4i*)(xq + b * 32);
-    const v4i xb = *(const v4i*)(xq + b * 32 + 16);
-    const float dx = xdq[b];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      int s = sdot4(wa[r].x, xa.x, 0);
-      s = sdot4(wa[r].y, xa.y, s);
-      s = sdot4(wa[r].z, xa.z, s);
-      s = sdot4(wa[r].w, xa.w, s);
-      s = sdot4(wb[r].x, xb.x, s);
-      s = sdot4(wb[r].y, xb.y, s);
-      s = sdot4(wb[r].z, xb.z, s);
-      s = sdot4(wb[r].w, xb.w, s);
-      float t = (float)s * f16_to_f32(wd[r]);
-      t = t * dx;
-      acc[r] = acc[r] + t;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
-}
-
-template <int NR>
-__device__ __forceinline__ void dot_rows_bf16(const LinearDev& L, const int* rows, const float* xs,
-                                              float* acc) {
-  const int lane = threadIdx.x % kWave;
-  const int K = L.in, nc = K / 8;
-  const uint16_t* w = (const uint16_t*)L.w;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
-  for (int c = lane; c < nc; c += kWave) {
-    v4u wv[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) wv[r] = __builtin_nontemporal_load((const v4u*)(w + (size_t)rows[r] * K) + c);
-    const float4 x0 = *(const float4*)(xs + c * 8);
-    const float4 x1 = *(const float4*)(xs + c * 8 + 4);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float a = acc[r];
-      a = fmaf(u2f(wv[r].x << 16), x0.x, a);
-      a = fmaf(u2f(wv[r].x & 0xffff0000u), x0.y, a);
-      a = fmaf(u2f(wv[r].y << 16), x0.z, a);
-      a = fmaf(u2f(wv[r].y & 0xffff0000u), x0.w, a);
-      a = fmaf(u2f(wv[r].z << 16), x1.x, a);
-      a = fmaf(u2f(wv[r].z & 0xffff0000u), x1.y, a);
-      a = fmaf(u2f(wv[r].w << 16), x1.z, a);
-      a = fmaf(u2f(wv[r].w & 0xffff0000u), x1.w, a);
-      acc[r] = a;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
-}
-
-template <int NR>
-__device__ __forceinline__ void dot_rows_f32(const LinearDev& L, const int* rows, const float* xs,
-                                             float* acc) {
-  const int lane = threadIdx.x % kWave;
-  const int K = L.in, nc = K / 4;
-  const float* w = (const float*)L.w;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
-  for (int c = lane; c < nc; c += kWave) {
-    v4f wv[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) wv[r] = __builtin_nontemporal_load((const v4f*)(w + (size_t)rows[r] * K) + c);
-    const float4 x0 = *(const float4*)(xs + c * 4);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float a = acc[r];
-      a = fmaf(wv[r].x, x0.x, a);
-      a = fmaf(wv[r].y, x0.y, a);
-      a = fmaf(wv[r].z, x0.z, a);
-      a = fmaf(wv[r].w, x0.w, a);
-      acc[r] = a;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = wave_sum(acc[r]);
-}
-
-// Applies the epilogue to physical row `row` with value `v`; `vp` is the value of the RoPE
-// partner row (row ^ 1) for EPI_QKV_ROPE.
-__device__ __forceinline__ void epilogue_row(const GemvArgs& a, int b, int row, float v, float vp) {
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int b, int row, float y, float yp, float yv) {
   switch (a.epi) {
     case EPI_STORE:
-      a.y[(size_t)b * a.y_stride + row] = v;
+      a.y[(size_t)b * a.y_stride + row] = y;
       break;
     case EPI_GELU:
-      a.y[(size_t)b * a.y_stride + row] = ref_gelu_tanh(v);
+      a.y[(size_t)b * a.y_stride + row] = ref_gelu_tanh(y);
       break;
+    case EPI_SILU_GATE: {
+      // FeedForwardLayer::forward gated branch (SVL/nn/transformer.rs:453-461): silu(gate) * value
+      float g = ref_silu(y);
+      a.y[(size_t)b * a.y_stride + row] = g * yv;
+      break;
+    }
     case EPI_RESID: {
-      float u = v;
+      float u = y;
       if (a.lscale) u = u * a.lscale[row];
       float* r = a.resid + (size_t)b * a.resid_stride + row;
       *r = *r + u;
       break;
     }
     case EPI_QKV_ROPE: {
+      // split q | k | v (transformer.rs:330-338); interleaved RoPE on q and k (rope_i); k, v
+      // into the ring slot of the current position.
       const int qdim = a.H * a.hd, kvdim = a.KVH * a.hd;
       const int p = a.pos[b];
-      int region = row < qdim ? 0 : (row < qdim + kvdim ? 1 : 2);
-      int rr = region == 0 ? row : (region == 1 ? row - qdim : row - qdim - kvdim);
-      int head = rr / a.hd, dim = rr % a.hd;
-      float out = v;
+      const int region = row < qdim ? 0 : (row < qdim + kvdim ? 1 : 2);
+      const int rr = region == 0 ? row : (region == 1 ? row - qdim : row - qdim - kvdim);
+      const int head = rr / a.hd, dim = rr % a.hd;
+      float out = y;
       if (region < 2) {
-        float theta = (float)p * a.inv_freq[dim / 2];
-        float c = cosf(theta), s = sinf(theta);
+        const float* cs = a.rope + ((size_t)p * (a.hd / 2) + dim / 2) * 2;
+        const float c = cs[0], s = cs[1];
         if ((dim & 1) == 0) {
-          float t0 = v * c, t1 = vp * s;
+          float t0 = y * c, t1 = yp * s;
           out = t0 - t1;
         } else {
-          float t0 = vp * s, t1 = v * c;
+          float t0 = yp * s, t1 = y * c;
           out = t0 + t1;
         }
       }
@@ -246,220 +155,317 @@ __device__ __forceinline__ void epilogue_row(const GemvArgs& a, int b, int row, 
   }
 }
 
-template <int FMT, int NR>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int K = a.L.in;
-  float* xs = (float*)smem;                         // K floats
-  int8_t* xq = (int8_t*)(xs + K);                   // K bytes
-  float* xdq = (float*)(xq + K);                    // K/32 floats
-  float* red = xdq + (K / 32);                      // 2 * kWaves floats
-  const int b = blockIdx.y;
-  const float* x = a.x + (size_t)b * a.x_stride;
-  for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = x[i];
-  __syncthreads();
-  if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps, red);
-  if (FMT == FMT_Q8_0) quantize_lds(xs, K, xq, xdq);
-
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int items = a.epi == EPI_SILU_GATE ? a.ff_hidden : a.L.out;
-  const int item0 = (blockIdx.x * kWaves + wave) * NR;
-  if (item0 < items) {
-    constexpr int NROWS = NR;  // rows per item group (SiLU handled with two passes)
-    int rows[NROWS];
-    float acc[NROWS], acc2[NROWS];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      int it = item0 + r < items ? item0 + r : items - 1;
-      rows[r] = it;
-    }
-    if (FMT == FMT_Q8_0) dot_rows_q8<NR>(a.L, rows, xq, xdq, acc);
-    else if (FMT == FMT_BF16) dot_rows_bf16<NR>(a.L, rows, xs, acc);
-    else dot_rows_f32<NR>(a.L, rows, xs, acc);
-    if (a.epi == EPI_SILU_GATE) {
-#pragma unroll
-      for (int r = 0; r < NR; ++r) rows[r] += a.ff_hidden;
-      if (FMT == FMT_Q8_0) dot_rows_q8<NR>(a.L, rows, xq, xdq, acc2);
-      else if (FMT == FMT_BF16) dot_rows_bf16<NR>(a.L, rows, xs, acc2);
-      else dot_rows_f32<NR>(a.L, rows, xs, acc2);
-    }
-    if (lane < NR && item0 + lane < items) {
-      float v = 0.0f, vp = 0.0f, v2 = 0.0f;
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        if (r == lane) v = acc[r];
-        if (r == (lane ^ 1)) vp = acc[r];
-        if (a.epi == EPI_SILU_GATE && r == lane) v2 = acc2[r];
-      }
-      if (a.epi == EPI_SILU_GATE) {
-        float g = ref_silu(v);
-        a.y[(size_t)b * a.y_stride + item0 + lane] = g * v2;
-      } else {
-        epilogue_row(a, b, item0 + lane, v, vp);
-      }
-    }
-  }
-  if (a.advance_pos && blockIdx.x == 0 && threadIdx.x == 0) a.pos[b] += 1;
+// Physical row of workgroup-local row r: the SiLU gate takes `ni` gate rows then their `ni`
+// value rows (j + ff_hidden).
+__device__ __forceinline__ int phys_row(const GemvArgs& a, int i0, int ni, int r) {
+  if (a.epi == EPI_SILU_GATE) return r < ni ? i0 + r : i0 + (r - ni) + a.ff_hidden;
+  return i0 + r;
 }
 
-static size_t gemv_smem(int K) { return (size_t)K * 4 + K + (K / 32) * 4 + 2 * kWaves * 4 + 16; }
-
-template <int FMT>
-static hipError_t launch_gemv_fmt(const GemvArgs& a, hipStream_t s) {
-  const int items = a.epi == EPI_SILU_GATE ? a.ff_hidden : a.L.out;
-  // Rows per wave: enough waves to cover the GPU, and pairs for RoPE.
-  int nr = items >= 4 * 4096 ? 4 : (items >= 2 * 4096 || a.epi == EPI_QKV_ROPE ? 2 : 1);
-  if (a.epi == EPI_QKV_ROPE && nr < 2) nr = 2;
-  dim3 block(kThreads);
-  size_t smem = gemv_smem(a.L.in);
-  if (nr == 4) {
-    dim3 grid((items + kWaves * 4 - 1) / (kWaves * 4), a.B);
-    hipLaunchKernelGGL((gemv_kernel<FMT, 4>), grid, block, smem, s, a);
-  } else if (nr == 2) {
-    dim3 grid((items + kWaves * 2 - 1) / (kWaves * 2), a.B);
-    hipLaunchKernelGGL((gemv_kernel<FMT, 2>), grid, block, smem, s, a);
-  } else {
-    dim3 grid((items + kWaves - 1) / kWaves, a.B);
-    hipLaunchKernelGGL((gemv_kernel<FMT, 1>), grid, block, smem, s, a);
+__device__ __forceinline__ void run_epilogues(const GemvArgs& a, int b, int i0, int ni, const float* Y) {
+  const int t = threadIdx.x;
+  if (t < ni) {
+    const float y = Y[t];
+    const float yp = a.epi == EPI_QKV_ROPE ? Y[t ^ 1] : 0.0f;
+    const float yv = a.epi == EPI_SILU_GATE ? Y[ni + t] : 0.0f;
+    epilogue(a, b, i0 + t, y, yp, yv);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
-  switch (a.L.fmt) {
-    case FMT_Q8_0: return launch_gemv_fmt<FMT_Q8_0>(a, s);
-    case FMT_BF16: return launch_gemv_fmt<FMT_BF16>(a, s);
-    case FMT_F32: return launch_gemv_fmt<FMT_F32>(a, s);
-    default: return hipErrorInvalidValue;
-  }
+  if (a.advance_pos && blockIdx.x == 0 && t == 0) a.pos[b] += 1;
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention: one query per (stream, head) over the visible keys of the ring buffer, split in
-// chunks of keys across workgroups (grid (nsplit, H, B)); each half-wave runs an online
-// softmax over its keys, the workgroup merges its half-waves, and attn_combine merges splits.
-// Visible keys of the query at position p: max(0, p - window + 1) ..= p
-// (SVL/nn/transformer.rs:385, SVL/nn/kernels/attention.rs:107-113).
+// Q8_0 GEMV (candle's quantized CPU matmul, SVL/nn/mod.rs:97): every block term is
+// (exact i32 dot as f32 * d_w) * d_x, and each row sums its terms in block order
+// (BlockQ8_0::vec_dot_unopt).  A workgroup owns `ipw` work items; its weight blocks are loaded
+// before the prologue (they do not depend on the input), one 32-byte block per thread and
+// round, the terms go to LDS, and one thread per row adds them up in order.
 
-template <int DPL, bool BF16KV>
-__device__ __forceinline__ void load_row(const void* base, size_t off, float* out) {
-  if (BF16KV) {
-    const uint16_t* p = (const uint16_t*)base + off;
-    if (DPL == 4) {
-      uint2 u = *(const uint2*)p;
-      out[0] = u2f(u.x << 16); out[1] = u2f(u.x & 0xffff0000u);
-      out[2] = u2f(u.y << 16); out[3] = u2f(u.y & 0xffff0000u);
-    } else {
-      uint32_t u = *(const uint32_t*)p;
-      out[0] = u2f(u << 16); out[1] = u2f(u & 0xffff0000u);
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <int MAXB>
+__global__ __launch_bounds__(kThreads) void gemv_q8_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int K = a.L.in, nb = K / 32;
+  const int b = blockIdx.y;
+  const bool silu = a.epi == EPI_SILU_GATE;
+  const int items = silu ? a.ff_hidden : a.L.out;
+  const int i0 = blockIdx.x * a.ipw;
+  const int ni = min(a.ipw, items - i0);
+  const int NR = silu ? 2 * ni : ni;
+  const int total = NR * nb;
+  const int ts = nb + 1;  // padded term-row stride
+  float* xs = (float*)smem;                   // K
+  int8_t* xq = (int8_t*)(xs + K);             // K
+  float* xdq = (float*)(xq + K);              // nb
+  float* T = xdq + nb;                        // NR * (nb + 1)
+  float* Y = T + 2 * a.ipw * ts;              // NR
+
+  const int8_t* wq = (const int8_t*)a.L.w;
+  v4i wa[MAXB], wb[MAXB];
+  uint16_t wd[MAXB];
+#pragma unroll
+  for (int k = 0; k < MAXB; ++k) {
+    const int idx = threadIdx.x + k * kThreads;
+    if (idx < total) {
+      const int r = idx / nb, blk = idx - r * nb;
+      const size_t row = (size_t)phys_row(a, i0, ni, r);
+      const v4i* p = (const v4i*)(wq + row * K + (size_t)blk * 32);
+      wa[k] = __builtin_nontemporal_load(p);
+      wb[k] = __builtin_nontemporal_load(p + 1);
+      wd[k] = a.L.scale[row * nb + blk];
     }
-  } else {
-    const float* p = (const float*)base + off;
-    if (DPL == 4) {
-      float4 v = *(const float4*)p;
-      out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
-    } else {
-      float2 v = *(const float2*)p;
-      out[0] = v.x; out[1] = v.y;
+  }
+  stage_input(a, b, xs);
+  quantize_lds(xs, K, xq, xdq);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < MAXB; ++k) {
+    const int idx = threadIdx.x + k * kThreads;
+    if (idx < total) {
+      const int r = idx / nb, blk = idx - r * nb;
+      const v4i xa = *(const v4i*)(xq + blk * 32);
+      const v4i xb = *(const v4i*)(xq + blk * 32 + 16);
+      int s = sdot4(wa[k].x, xa.x, 0);
+      s = sdot4(wa[k].y, xa.y, s);
+      s = sdot4(wa[k].z, xa.z, s);
+      s = sdot4(wa[k].w, xa.w, s);
+      s = sdot4(wb[k].x, xb.x, s);
+      s = sdot4(wb[k].y, xb.y, s);
+      s = sdot4(wb[k].z, xb.z, s);
+      s = sdot4(wb[k].w, xb.w, s);
+      float t = (float)s * f16_to_f32(wd[k]);
+      T[r * ts + blk] = t * xdq[blk];
     }
+  }
+  __syncthreads();
+  if (threadIdx.x < NR) {
+    const float* tr = T + threadIdx.x * ts;
+    float acc = 0.0f;
+    for (int blk = 0; blk < nb; ++blk) acc = acc + tr[blk];
+    Y[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  run_epilogues(a, b, i0, ni, Y);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dense GEMV (f32 or bf16 weights): the reference's matvec (SVL/nn/kernels/matvec.rs:239-246)
+// row by row with its 16-lane dot (kernels/mod.rs:66-91): 16 threads per row, thread i
+// accumulating x[16c + i] * w[16c + i] with FMA over c, then the pairwise lane sum and the
+// scalar tail.  A workgroup owns 16 rows (8 gate/value pairs for the SiLU gate).
+
+template <bool BF16W>
+__global__ __launch_bounds__(kThreads) void gemv_dense_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int K = a.L.in;
+  const int b = blockIdx.y;
+  const bool silu = a.epi == EPI_SILU_GATE;
+  const int items = silu ? a.ff_hidden : a.L.out;
+  const int i0 = blockIdx.x * a.ipw;
+  const int ni = min(a.ipw, items - i0);
+  const int NR = silu ? 2 * ni : ni;
+  float* xs = (float*)smem;   // K
+  float* Y = xs + K;          // 16
+  stage_input(a, b, xs);
+  const int g = threadIdx.x / 16, li = threadIdx.x % 16;
+  const int chunks = K / 16;
+  if (g < NR) {
+    const size_t row = (size_t)phys_row(a, i0, ni, g);
+    float acc = 0.0f;
+    if (BF16W) {
+      const uint16_t* w = (const uint16_t*)a.L.w + row * K + li;
+      int c = 0;
+      for (; c + 8 <= chunks; c += 8) {
+        uint16_t wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(xs[(c + u) * 16 + li], bf16_to_f32(wv[u]), acc);
+      }
+      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], bf16_to_f32(w[(size_t)c * 16]), acc);
+    } else {
+      const float* w = (const float*)a.L.w + row * K + li;
+      int c = 0;
+      for (; c + 8 <= chunks; c += 8) {
+        float wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(xs[(c + u) * 16 + li], wv[u], acc);
+      }
+      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], w[(size_t)c * 16], acc);
+    }
+    // pairwise lane sum: acc[i] += acc[i + width] for width 8, 4, 2, 1
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
+    if (li == 0) {
+      float tail = 0.0f;
+      for (int i = chunks * 16; i < K; ++i) {
+        float wv = BF16W ? bf16_to_f32(((const uint16_t*)a.L.w)[row * K + i]) : ((const float*)a.L.w)[row * K + i];
+        float p = xs[i] * wv;
+        tail = tail + p;
+      }
+      Y[g] = acc + tail;
+    }
+  }
+  __syncthreads();
+  run_epilogues(a, b, i0, ni, Y);
+}
+
+static int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+hipError_t launch_gemv(const GemvArgs& a0, hipStream_t s) {
+  GemvArgs a = a0;
+  const bool silu = a.epi == EPI_SILU_GATE;
+  const int items = silu ? a.ff_hidden : a.L.out;
+  const int K = a.L.in;
+  if (a.L.fmt == FMT_Q8_0) {
+    const int nb = K / 32;
+    // As many items per workgroup as keep 16 rows, 8 blocks per thread and 256 workgroups.
+    int ipw = silu ? 8 : 16;
+    while (ipw > 2 && ((silu ? 2 * ipw : ipw) * nb > 8 * kThreads || items / ipw < 256)) ipw /= 2;
+    a.ipw = ipw;
+    const int NR = silu ? 2 * ipw : ipw;
+    const int maxb = pow2_at_least((NR * nb + kThreads - 1) / kThreads);
+    const size_t smem = (size_t)K * 4 + K + (size_t)nb * 4 + (size_t)2 * ipw * (nb + 1) * 4 + (size_t)NR * 4 + 64;
+    dim3 grid((items + ipw - 1) / ipw, a.B);
+    switch (maxb) {
+      case 1: hipLaunchKernelGGL((gemv_q8_kernel<1>), grid, dim3(kThreads), smem, s, a); break;
+      case 2: hipLaunchKernelGGL((gemv_q8_kernel<2>), grid, dim3(kThreads), smem, s, a); break;
+      case 4: hipLaunchKernelGGL((gemv_q8_kernel<4>), grid, dim3(kThreads), smem, s, a); break;
+      case 8: hipLaunchKernelGGL((gemv_q8_kernel<8>), grid, dim3(kThreads), smem, s, a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
+  if (a.L.fmt == FMT_F32 || a.L.fmt == FMT_BF16) {
+    a.ipw = silu ? 8 : 16;
+    const size_t smem = (size_t)K * 4 + 16 * 4 + 64;
+    dim3 grid((items + a.ipw - 1) / a.ipw, a.B);
+    if (a.L.fmt == FMT_BF16) hipLaunchKernelGGL((gemv_dense_kernel<true>), grid, dim3(kThreads), smem, s, a);
+    else hipLaunchKernelGGL((gemv_dense_kernel<false>), grid, dim3(kThreads), smem, s, a);
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Attention (SVL/nn/kernels/attention.rs:103-168): the query at position p attends to keys
+// max(0, p - window + 1) ..= p (transformer.rs:385) in the ring.  Same order of operations as
+// the reference's `attend`:
+//   attn_scores:    w_j = scale * dot(q, k_j) with the 16-lane dot       (parallel over keys)
+//   attn_softmax_v: max, e_j = exp(w_j - max), sum_j e_j in key order, then
+//                   out = sum over keys in order of mul_add(e_j / sum, v_j, out)
+
+template <bool BF16KV>
+__device__ __forceinline__ float kv_at(const void* base, size_t idx) {
+  if (BF16KV) return bf16_to_f32(((const uint16_t*)base)[idx]);
+  return ((const float*)base)[idx];
+}
+
+constexpr int kKeysPerScoreBlock = 64;
+
+template <int HD, bool BF16KV>
+__global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int p = a.pos[b];
+  const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
+  const int first = p + 1 - L;
+  const int g = threadIdx.x / 16, li = threadIdx.x % 16;
+  const int kvh = h / (a.H / a.KVH);
+  constexpr int C = HD / 16;
+  float q[C];
+  const float* qp = a.q + (size_t)b * a.H * HD + (size_t)h * HD + li;
+#pragma unroll
+  for (int c = 0; c < C; ++c) q[c] = qp[c * 16];
+  const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
+  for (int jj = blockIdx.x * kKeysPerScoreBlock + g; jj < min(L, (int)(blockIdx.x + 1) * kKeysPerScoreBlock); jj += 16) {
+    const int j = first + jj;
+    const size_t base = (head_base + (size_t)(j % a.cap)) * HD + li;
+    float kv[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) kv[c] = kv_at<BF16KV>(a.kc, base + c * 16);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc = fmaf(q[c], kv[c], acc);
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
+    if (li == 0) a.scores[((size_t)b * a.H + h) * a.cap + jj] = a.scale * (acc + 0.0f);
   }
 }
 
 template <int HD, bool BF16KV>
-__global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
-  constexpr int DPL = HD / 32;
-  __shared__ float sm[8], sl[8];
-  __shared__ float so[8][HD];
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int hw = threadIdx.x / 32, l32 = threadIdx.x % 32;
+__global__ __launch_bounds__(kWave) void attn_softmax_v_kernel(AttnArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* w = (float*)smem;  // L weights
+  __shared__ float s_sum;
+  const int h = blockIdx.y, b = blockIdx.z;
   const int p = a.pos[b];
   const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
   const int first = p + 1 - L;
-  const int k0 = first + split * a.chunk;
-  const int k1 = min(k0 + a.chunk, p + 1);
-  const int kvh = h / (a.H / a.KVH);
-  float q[DPL];
-  const float* qp = a.q + (size_t)b * a.H * HD + (size_t)h * HD + l32 * DPL;
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) q[i] = qp[i];
-  float m = -__builtin_huge_valf(), l = 0.0f, o[DPL];
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) o[i] = 0.0f;
-  const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
-  for (int j = k0 + hw; j < k1; j += 8) {
-    const size_t off = (head_base + (size_t)(j % a.cap)) * HD + l32 * DPL;
-    float kv[DPL], vv[DPL];
-    load_row<DPL, BF16KV>(a.kc, off, kv);
-    load_row<DPL, BF16KV>(a.vc, off, vv);
-    float d = 0.0f;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) d = fmaf(q[i], kv[i], d);
-    float s = a.scale * half_sum(d);
-    float mn = fmaxf(m, s);
-    float c = ref_exp(m - mn);
-    float e = ref_exp(s - mn);
-    l = l * c + e;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) o[i] = fmaf(e, vv[i], o[i] * c);
-    m = mn;
+  const int lane = threadIdx.x;
+  const float* sc = a.scores + ((size_t)b * a.H + h) * a.cap;
+  float mx = -__builtin_huge_valf();
+  for (int j = lane; j < L; j += kWave) {
+    float v = sc[j];
+    w[j] = v;
+    mx = fmaxf(mx, v);
   }
-  if (l32 == 0) {
-    sm[hw] = m;
-    sl[hw] = l;
-  }
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) so[hw][l32 * DPL + i] = o[i];
+  mx = wave_max(mx);
+  for (int j = lane; j < L; j += kWave) w[j] = ref_exp(w[j] - mx);
   __syncthreads();
-  const size_t pidx = ((size_t)b * a.H + h) * a.nsplit + split;
-  if (threadIdx.x < HD) {
-    float M = sm[0];
-#pragma unroll
-    for (int w = 1; w < 8; ++w) M = fmaxf(M, sm[w]);
-    float lsum = 0.0f, osum = 0.0f;
-    if (M != -__builtin_huge_valf()) {
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        float f = ref_exp(sm[w] - M);
-        lsum += sl[w] * f;
-        osum += so[w][threadIdx.x] * f;
-      }
-    }
-    a.po[pidx * HD + threadIdx.x] = osum;
-    if (threadIdx.x == 0) {
-      a.pm[pidx] = M;
-      a.pl[pidx] = lsum;
-    }
+  if (lane == 0) {
+    float sum = 0.0f;
+    for (int j = 0; j < L; ++j) sum = sum + w[j];
+    s_sum = sum;
   }
-}
-
-template <int HD>
-__global__ void attn_combine_kernel(AttnArgs a) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int p = a.pos[b];
-  const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
-  const int ns = (L + a.chunk - 1) / a.chunk;
-  const size_t base = ((size_t)b * a.H + h) * a.nsplit;
-  float M = -__builtin_huge_valf();
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.pm[base + s]);
-  float lsum = 0.0f, osum = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    float f = ref_exp(a.pm[base + s] - M);
-    lsum += a.pl[base + s] * f;
-    osum += a.po[(base + s) * HD + d] * f;
+  __syncthreads();
+  const float sum = s_sum;
+  for (int j = lane; j < L; j += kWave) w[j] = w[j] / sum;
+  __syncthreads();
+  if (lane < 32) {
+    const int d = blockIdx.x * 32 + lane;
+    const int kvh = h / (a.H / a.KVH);
+    const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
+    float acc = 0.0f;
+    int j = 0;
+    for (; j + 8 <= L; j += 8) {
+      float vv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vv[u] = kv_at<BF16KV>(a.vc, (head_base + (size_t)((first + j + u) % a.cap)) * HD + d);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = fmaf(w[j + u], vv[u], acc);
+    }
+    for (; j < L; ++j) acc = fmaf(w[j], kv_at<BF16KV>(a.vc, (head_base + (size_t)((first + j) % a.cap)) * HD + d), acc);
+    a.out[(size_t)b * a.H * HD + (size_t)h * HD + d] = acc;
   }
-  a.out[(size_t)b * a.H * HD + (size_t)h * HD + d] = lsum > 0.0f ? osum / lsum : 0.0f;
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  dim3 grid(a.nsplit, a.H, a.B);
+  const int lmax = a.cap;
+  dim3 gs((lmax + kKeysPerScoreBlock - 1) / kKeysPerScoreBlock, a.H, a.B);
+  dim3 gv(a.hd / 32, a.H, a.B);
+  const size_t smem = (size_t)lmax * 4 + 64;
   if (a.hd == 128) {
-    if (a.kv_bf16) hipLaunchKernelGGL((attn_partial_kernel<128, true>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_partial_kernel<128, false>), grid, dim3(kThreads), 0, s, a);
-    hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(a.H, a.B), dim3(128), 0, s, a);
+    if (a.kv_bf16) {
+      hipLaunchKernelGGL((attn_scores_kernel<128, true>), gs, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((attn_softmax_v_kernel<128, true>), gv, dim3(kWave), smem, s, a);
+    } else {
+      hipLaunchKernelGGL((attn_scores_kernel<128, false>), gs, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((attn_softmax_v_kernel<128, false>), gv, dim3(kWave), smem, s, a);
+    }
   } else if (a.hd == 64) {
-    if (a.kv_bf16) hipLaunchKernelGGL((attn_partial_kernel<64, true>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_partial_kernel<64, false>), grid, dim3(kThreads), 0, s, a);
-    hipLaunchKernelGGL((attn_combine_kernel<64>), dim3(a.H, a.B), dim3(64), 0, s, a);
+    if (a.kv_bf16) {
+      hipLaunchKernelGGL((attn_scores_kernel<64, true>), gs, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((attn_softmax_v_kernel<64, true>), gv, dim3(kWave), smem, s, a);
+    } else {
+      hipLaunchKernelGGL((attn_scores_kernel<64, false>), gs, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((attn_softmax_v_kernel<64, false>), gv, dim3(kWave), smem, s, a);
+    }
   } else {
     return hipErrorInvalidValue;
   }
@@ -477,16 +483,27 @@ __global__ void embed_kernel(EmbedArgs a) {
   uint32_t t = a.text_tok ? a.text_tok[b] : a.fb_tok[b];
   t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
   const bool initial = a.initial_at_zero && a.pos[b] == 0;
+  const size_t rows = (size_t)a.card + 1;
   float x;
   if (a.tables_bf16) x = bf16_to_f32(((const uint16_t*)a.text_emb)[(size_t)t * a.d + i]);
   else x = ((const float*)a.text_emb)[(size_t)t * a.d + i];
-  for (int c = 0; c < a.n_q; ++c) {
-    uint32_t tok = initial ? (uint32_t)a.card : a.audio[(size_t)b * a.n_q + c];
-    tok = tok > (uint32_t)a.card ? (uint32_t)a.card : tok;
-    float e;
-    if (a.tables_bf16) e = bf16_to_f32(((const uint16_t*)a.emb[c])[(size_t)tok * a.d + i]);
-    else e = ((const float*)a.emb[c])[(size_t)tok * a.d + i];
-    x = x + e;
+  const uint32_t* au = a.audio + (size_t)b * a.n_q;
+  for (int c0 = 0; c0 < a.n_q; c0 += 8) {
+    float e[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = c0 + u;
+      e[u] = 0.0f;
+      if (c < a.n_q) {
+        uint32_t tok = initial ? (uint32_t)a.card : au[c];
+        tok = tok > (uint32_t)a.card ? (uint32_t)a.card : tok;
+        const size_t idx = ((size_t)c * rows + tok) * a.d + i;
+        e[u] = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.emb)[idx]) : ((const float*)a.emb)[idx];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (c0 + u < a.n_q) x = x + e[u];
   }
   a.x[(size_t)b * a.d + i] = x;
 }
@@ -503,17 +520,17 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const float* x, int x_st
                                                         int d, int norm, const float* w, const float* nb, float eps) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* xs = (float*)smem;
-  float* red = xs + d;
   const int b = blockIdx.x;
   for (int i = threadIdx.x; i < d; i += kThreads) xs[i] = x[(size_t)b * x_stride + i];
   __syncthreads();
-  norm_lds(xs, d, norm, w, nb, eps, red);
+  norm_lds(xs, d, norm, w, nb, eps);
+  __syncthreads();
   for (int i = threadIdx.x; i < d; i += kThreads) y[(size_t)b * y_stride + i] = xs[i];
 }
 
 hipError_t launch_norm(const float* x, int x_stride, float* y, int y_stride, int B, int d, int norm,
                        const float* w, const float* b, float eps, hipStream_t s) {
-  size_t smem = (size_t)d * 4 + 2 * kWaves * 4;
+  size_t smem = (size_t)d * 4 + 64;
   hipLaunchKernelGGL(norm_kernel, dim3(B), dim3(kThreads), smem, s, x, x_stride, y, y_stride, d, norm, w, b, eps);
   return hipGetLastError();
 }

@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -79,11 +80,17 @@ struct svl_model {
   int device = 0;
   std::vector<void*> allocs;
   std::vector<Layer> layers;
-  float* inv_freq = nullptr;
+  // RoPE cos/sin of every position below rope_len: [rope_len][head_dim / 2][2], computed on
+  // the host with the C library's cosf/sinf (SVL/nn/transformer.rs:114-118, 161-172) and
+  // grown on demand.  Superseded tables stay allocated until the model is destroyed, since
+  // kernels already enqueued may still read them.
+  mutable std::mutex rope_mu;
+  mutable float* rope = nullptr;
+  mutable int64_t rope_len = 0;
+  mutable std::vector<void*> rope_old;
   // STT
   void* text_emb = nullptr;
-  std::vector<void*> emb;
-  void** emb_dev = nullptr;
+  void* emb = nullptr;  // n_q tables back to back
   int tables_bf16 = 0;
   float* out_norm_w = nullptr;
   float* out_norm_b = nullptr;
@@ -96,6 +103,8 @@ struct svl_model {
   ~svl_model() {
     hipSetDevice(device);
     for (void* p : allocs) hipFree(p);
+    for (void* p : rope_old) hipFree(p);
+    if (rope) hipFree(rope);
     if (stream) hipStreamDestroy(stream);
   }
 
@@ -117,12 +126,10 @@ struct svl_state {
   std::vector<int64_t> pos_host;
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
-  float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  float* scores = nullptr;    // [B][H][slots]
   float* in = nullptr;        // TTS latent / forward input staging
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
   uint32_t* tok_out = nullptr;
-  int nsplit = 1;
-  int chunk = 32;
   size_t in_cap = 0;
 
   ~svl_state() {
@@ -242,22 +249,62 @@ int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string&
   return 0;
 }
 
-// Embedding tables: kept bf16 when every table is bf16, f32 otherwise.
-int load_table(svl_model* m, const svl_tensor* ts, size_t n, const std::string& name, size_t count, void** out) {
+// Embedding table `name` ([count] values) copied to `dst` on the device, kept bf16 when every
+// table is bf16 and converted to f32 otherwise.
+int load_table(svl_model* m, const svl_tensor* ts, size_t n, const std::string& name, size_t count, void* dst) {
   const svl_tensor* t = find_tensor(ts, n, name);
   if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", name.c_str());
   if (numel(t) != count)
     return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: %zu elements, expected %zu", name.c_str(), numel(t), count);
   if (m->tables_bf16) {
-    void* w;
-    TRY(m->alloc(&w, count * 2));
-    HIP_TRY(hipMemcpy(w, t->data, count * 2, hipMemcpyHostToDevice));
-    *out = w;
+    HIP_TRY(hipMemcpy(dst, t->data, count * 2, hipMemcpyHostToDevice));
     return 0;
   }
-  float* f;
-  TRY(upload_f32(m, t, count, &f));
-  *out = f;
+  if (t->dtype == SVL_F32) {
+    HIP_TRY(hipMemcpy(dst, t->data, count * 4, hipMemcpyHostToDevice));
+    return 0;
+  }
+  if (t->dtype != SVL_BF16 && t->dtype != SVL_F16)
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: dense dtype expected", name.c_str());
+  void* tmp;
+  HIP_TRY(hipMalloc(&tmp, count * 2));
+  hipError_t e = hipMemcpy(tmp, t->data, count * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = t->dtype == SVL_BF16 ? launch_bf16_to_f32((const uint16_t*)tmp, (float*)dst, count, m->stream)
+                             : launch_f16_to_f32((const uint16_t*)tmp, (float*)dst, count, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  hipFree(tmp);
+  HIP_TRY(e);
+  return 0;
+}
+
+// Makes the RoPE table cover positions [0, needed).  The same formula and C library as the
+// reference's f64 inv_freq / f32 angle / cos, sin (SVL/nn/transformer.rs:114-118, 161-172).
+int ensure_rope(const svl_model* m, int64_t needed) {
+  std::lock_guard<std::mutex> lock(m->rope_mu);
+  if (needed <= m->rope_len) return 0;
+  int64_t len = m->rope_len ? m->rope_len : 4096;
+  while (len < needed) len *= 2;
+  const int half = m->cfg.head_dim / 2;
+  std::vector<float> inv(half), tab((size_t)len * half * 2);
+  for (int i = 0; i < half; ++i)
+    inv[i] = (float)std::exp(-(std::log(m->cfg.max_period)) * 2.0 * (double)i / (double)m->cfg.head_dim);
+  for (int64_t p = 0; p < len; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float f = (float)p * inv[i];
+      tab[((size_t)p * half + i) * 2] = ::cosf(f);
+      tab[((size_t)p * half + i) * 2 + 1] = ::sinf(f);
+    }
+  void* d;
+  HIP_TRY(hipMalloc(&d, tab.size() * 4));
+  hipError_t e = hipMemcpy(d, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    hipFree(d);
+    HIP_TRY(e);
+  }
+  if (m->rope) m->rope_old.push_back(m->rope);
+  m->rope = (float*)d;
+  m->rope_len = len;
   return 0;
 }
 
@@ -270,8 +317,10 @@ int check_config(const svl_config* c) {
   if (c->ff_hidden <= 0 || c->ff_hidden % 32) return set_error(SVL_ERR_CONFIG, "ff_hidden must be a positive multiple of 32");
   if ((c->num_heads * c->head_dim) % 32) return set_error(SVL_ERR_CONFIG, "attention width must be a multiple of 32");
   // the GEMV prologue stages one input row in LDS (5 bytes per element, 64 KiB per workgroup)
-  if (c->d_model > 12288 || c->ff_hidden > 12288 || c->num_heads * c->head_dim > 12288)
-    return set_error(SVL_ERR_CONFIG, "d_model, ff_hidden and num_heads * head_dim must be <= 12288");
+  if (c->d_model > 8192 || c->ff_hidden > 8192 || c->num_heads * c->head_dim > 8192)
+    return set_error(SVL_ERR_CONFIG, "d_model, ff_hidden and num_heads * head_dim must be <= 8192");
+  // attention stages one head's weights over the window in LDS
+  if (c->context > 16000) return set_error(SVL_ERR_CONFIG, "context must be <= 16000");
   if (c->norm_kind != SVL_NORM_LAYER && c->norm_kind != SVL_NORM_RMS) return set_error(SVL_ERR_CONFIG, "unknown norm");
   if (c->ff_kind != SVL_FF_PLAIN_GELU && c->ff_kind != SVL_FF_GATED_SILU) return set_error(SVL_ERR_CONFIG, "unknown feed-forward");
   if (c->context < 0) return set_error(SVL_ERR_CONFIG, "context must be >= 0");
@@ -319,16 +368,7 @@ int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_mode
       TRY(load_linear(m, ts, n, p + "linear2.weight", d, c.ff_hidden, c.quantize, &L.ff2));
     }
   }
-  // inv_freq in f64 then f32 (SVL/nn/transformer.rs:114-118)
-  {
-    std::vector<float> inv(hd / 2);
-    for (int i = 0; i < hd / 2; ++i)
-      inv[i] = (float)std::exp(-(std::log(c.max_period)) * 2.0 * (double)i / (double)hd);
-    void* p;
-    TRY(m->alloc(&p, inv.size() * 4));
-    HIP_TRY(hipMemcpy(p, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
-    m->inv_freq = (float*)p;
-  }
+  TRY(ensure_rope(m, 4096));
   if (c.kind == SVL_MODEL_STT) {
     bool all_bf16 = true;
     const svl_tensor* te = find_tensor(ts, n, "text_emb.weight");
@@ -339,14 +379,13 @@ int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_mode
       all_bf16 = t && t->dtype == SVL_BF16;
     }
     m->tables_bf16 = all_bf16 ? 1 : 0;
-    TRY(load_table(m, ts, n, "text_emb.weight", (size_t)(c.text_card + 1) * d, &m->text_emb));
-    m->emb.resize(c.n_q);
+    const size_t esz = m->tables_bf16 ? 2 : 4;
+    const size_t rows = (size_t)(c.card + 1) * d;
+    TRY(m->alloc(&m->text_emb, (size_t)(c.text_card + 1) * d * esz));
+    TRY(load_table(m, ts, n, "text_emb.weight", (size_t)(c.text_card + 1) * d, m->text_emb));
+    TRY(m->alloc(&m->emb, rows * c.n_q * esz));
     for (int i = 0; i < c.n_q; ++i)
-      TRY(load_table(m, ts, n, "emb." + std::to_string(i) + ".weight", (size_t)(c.card + 1) * d, &m->emb[i]));
-    void* p;
-    TRY(m->alloc(&p, sizeof(void*) * c.n_q));
-    HIP_TRY(hipMemcpy(p, m->emb.data(), sizeof(void*) * c.n_q, hipMemcpyHostToDevice));
-    m->emb_dev = (void**)p;
+      TRY(load_table(m, ts, n, "emb." + std::to_string(i) + ".weight", rows, (char*)m->emb + rows * i * esz));
     TRY(load_vec(m, ts, n, "out_norm.alpha", d, &m->out_norm_w));
     TRY(load_linear(m, ts, n, "text_linear.weight", c.text_card, d, c.quantize, &m->text_linear));
   } else if (c.kind == SVL_MODEL_TTS) {
@@ -382,6 +421,11 @@ int norm_code(const svl_config& c) { return c.norm_kind == SVL_NORM_RMS ? NORM_R
 // transformer output).  Advances the positions at the end.
 int run_layers(const svl_model* m, svl_state* s) {
   const svl_config& c = m->cfg;
+  const float* rope;
+  {
+    std::lock_guard<std::mutex> lock(m->rope_mu);
+    rope = m->rope;
+  }
   const int d = c.d_model, hd = c.head_dim, H = c.num_heads, KVH = c.num_kv_heads;
   for (int i = 0; i < c.num_layers; ++i) {
     const Layer& L = m->layers[i];
@@ -397,7 +441,7 @@ int run_layers(const svl_model* m, svl_state* s) {
     g.eps = c.norm_eps;
     g.epi = EPI_QKV_ROPE;
     g.pos = s->pos;
-    g.inv_freq = m->inv_freq;
+    g.rope = rope;
     g.H = H;
     g.KVH = KVH;
     g.hd = hd;
@@ -420,12 +464,8 @@ int run_layers(const svl_model* m, svl_state* s) {
     a.cap = s->slots;
     a.window = c.context;
     a.kv_bf16 = c.kv_dtype == SVL_BF16;
-    a.scale = std::pow((float)hd, -0.5f);
-    a.chunk = s->chunk;
-    a.nsplit = s->nsplit;
-    a.pm = s->pm;
-    a.pl = s->pl;
-    a.po = s->po;
+    a.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
+    a.scores = s->scores;
     a.out = s->att;
     HIP_TRY(launch_attention(a, s->stream));
     // out_proj + residual
@@ -479,13 +519,18 @@ int run_layers(const svl_model* m, svl_state* s) {
   return 0;
 }
 
+// Validates that every stream has room for `steps` more positions and that the RoPE table
+// covers them.
 int check_room(const svl_state* s, int64_t steps) {
-  if (s->m->cfg.context > 0) return 0;
-  for (int64_t p : s->pos_host)
-    if (p + steps > s->slots)
+  int64_t top = 0;
+  for (int64_t p : s->pos_host) {
+    if (s->m->cfg.context == 0 && p + steps > s->slots)
       return set_error(SVL_ERR_INVALID_INPUT, "state capacity %d exceeded (position %lld + %lld steps)", s->slots,
                        (long long)p, (long long)steps);
-  return 0;
+    top = std::max(top, p + steps);
+  }
+  if (top >= ((int64_t)1 << 31)) return set_error(SVL_ERR_INVALID_INPUT, "position beyond 2^31");
+  return ensure_rope(s->m, top);
 }
 
 // text_linear over out_norm(x), then argmax into the feedback tokens (and `out` if given).
@@ -513,7 +558,7 @@ int stt_steps(const svl_model* m, svl_state* s, int64_t n, const uint32_t* d_aud
   for (int64_t i = 0; i < n; ++i) {
     EmbedArgs e{};
     e.text_emb = m->text_emb;
-    e.emb = m->emb_dev;
+    e.emb = m->emb;
     e.tables_bf16 = m->tables_bf16;
     e.d = c.d_model;
     e.n_q = c.n_q;
@@ -538,13 +583,12 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (batch <= 0) return set_error(SVL_ERR_INVALID_INPUT, "batch must be positive");
   int slots = c.context > 0 ? c.context : capacity;
   if (slots <= 0) return set_error(SVL_ERR_INVALID_INPUT, "an unlimited-context model needs a positive capacity");
+  if (slots > 16000) return set_error(SVL_ERR_INVALID_INPUT, "capacity must be <= 16000");
   HIP_TRY(hipSetDevice(m->device));
   svl_state* s = new svl_state();
   s->m = m;
   s->B = batch;
   s->slots = slots;
-  s->chunk = 32;
-  s->nsplit = (slots + s->chunk - 1) / s->chunk;
   auto fail = [&](int rc) {
     delete s;
     return rc;
@@ -572,10 +616,7 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * width * 4), s->h = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.text_card, 1) * 4), s->logits = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.d_model, c.z_dim) * 4), s->z = (float*)p;
-  const size_t np = (size_t)batch * c.num_heads * s->nsplit;
-  if (!rc) rc = s->alloc(&p, np * 4), s->pm = (float*)p;
-  if (!rc) rc = s->alloc(&p, np * 4), s->pl = (float*)p;
-  if (!rc) rc = s->alloc(&p, np * c.head_dim * 4), s->po = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * c.num_heads * slots * 4), s->scores = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;
   if (rc) return fail(rc);
@@ -843,7 +884,7 @@ int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, 
   HIP_TRY(hipMemcpyAsync(daudio, audio_tokens, (size_t)s->B * c.n_q * 4, hipMemcpyHostToDevice, s->stream));
   EmbedArgs e{};
   e.text_emb = m->text_emb;
-  e.emb = m->emb_dev;
+  e.emb = m->emb;
   e.tables_bf16 = m->tables_bf16;
   e.d = c.d_model;
   e.n_q = c.n_q;

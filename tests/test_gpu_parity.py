@@ -1,10 +1,11 @@
 """GPU parity: libsvl (HIP, through the C ABI) against the oracle on the same seeded inputs.
 
-Bars (from the step's contract):
+Bars:
   * quantization / dequantization of weights: bit-exact to the oracle's candle restatement
-  * logits: max-abs 1e-4 for f32 models; 2e-2 for bf16 and Q8_0 models (reduced-precision
-    weights: an activation re-quantization can round one Q8_0 step differently when inputs
-    differ in the last ulp)
+  * logits, attention, norms, hidden states: bit-exact to the oracle with an f32 KV cache (the
+    GPU kernels perform the oracle's f32 operations in the oracle's order), hence within the
+    step contract's max-abs 1e-4 (f32) / 2e-2 (bf16) with room to spare; a bf16 KV cache is
+    held to 2e-2
   * greedy tokens: identical over 256 steps
   * lockstep batches: bit-identical to the same streams run one by one
 Reduced shapes keep the structure (GQA/windows wrap, gated SiLU, RMSNorm / LayerNorm) and let
@@ -64,9 +65,9 @@ def test_q8_0_candle_blocks_round_trip():
     assert np.array_equal(blocks, blocked["transformer.layers.0.self_attn.in_proj_weight"][2])
 
 
-@pytest.mark.parametrize("dtype,tol", [("q8_0", LOWP_TOL), ("bf16", LOWP_TOL), ("f32", F32_TOL)])
-def test_stt_small_steps_match_oracle(dtype, tol):
-    """64 steps through a window of 24 (the ring wraps twice): logits within tolerance, tokens equal."""
+@pytest.mark.parametrize("dtype", ["q8_0", "bf16", "f32"])
+def test_stt_small_steps_match_oracle(dtype):
+    """64 steps through a window of 24 (the ring wraps twice): logits bit-exact, tokens equal."""
     s = W.S1_SMALL
     _, g, o = build(s, dtype, seed=3)
     gs, os_ = g.init_state(), o.new_state()
@@ -78,8 +79,8 @@ def test_stt_small_steps_match_oracle(dtype, tol):
         to, lo = os_.stt_step(text, audio[i], want_logits=True)
         worst = max(worst, float(np.max(np.abs(lg[0] - lo))))
         assert tg[0] == to, f"step {i}"
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), f"step {i}: max diff {worst}"
         text = int(tg[0])
-    assert worst < tol, worst
     print(f"{dtype}: max |logit diff| over 64 steps = {worst:.3g}")
 
 
@@ -127,7 +128,7 @@ def test_state_duplicate_reset_and_caches():
         ok, ov, ostart = os_.cache(layer)
         n = k.shape[1]
         assert first == 30 - n and n == s.context
-        assert np.max(np.abs(k - ok[0, :, -n:])) < 1e-4 and np.max(np.abs(v - ov[0, :, -n:])) < 1e-4
+        assert np.array_equal(k, ok[0, :, -n:]) and np.array_equal(v, ov[0, :, -n:])
     st.reset()
     assert np.array_equal(g.recognize(audio[:10, None], st), g.recognize(audio[:10, None], g.init_state()))
 
@@ -142,7 +143,7 @@ def test_tts_small_prefilled_matches_oracle():
     for i in range(12):
         z = g.backbone_step(None if i == 0 else lat[i][None], gs)[0]
         zo = os_.tts_step(None if i == 0 else lat[i])
-        assert np.max(np.abs(z - zo)) < F32_TOL, i
+        assert np.array_equal(z, zo), (i, float(np.max(np.abs(z - zo))))
 
 
 def test_transformer_forward_matches_oracle():
@@ -155,7 +156,7 @@ def test_transformer_forward_matches_oracle():
     y1 = g.forward(xs[:, :13], gs)
     y2 = g.forward(xs[:, 13:], gs)
     yo = os_.forward(xs)
-    assert np.max(np.abs(np.concatenate([y1, y2], axis=1) - yo)) < F32_TOL
+    assert np.array_equal(np.concatenate([y1, y2], axis=1), yo)
     assert gs.positions[0] == 20
 
 
@@ -242,4 +243,4 @@ def test_t1_f32_prefilled_256_within_f32_bar():
     for i in range(16):
         z = g.backbone_step(lat[i][None], gs)[0]
         zo = os_.tts_step(lat[i])
-        assert np.max(np.abs(z - zo)) < F32_TOL, i
+        assert np.array_equal(z, zo), (i, float(np.max(np.abs(z - zo))))
