@@ -11,7 +11,6 @@ MI355X HBM bandwidth with the algorithmic bytes of the steps actually timed; `cp
 the oracle (this repository's C restatement of the reference's CPU path) on the host cores.
 """
 import argparse
-import ctypes as C
 import json
 import os
 import sys
@@ -26,32 +25,6 @@ for p in (ROOT, PKG):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-
-
-class HipEvents:
-    """hipEvent timing on an arbitrary HIP stream (the library's own stream)."""
-
-    def __init__(self):
-        self.h = C.CDLL("libamdhip64.so")
-        self.h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
-        self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
-        self.h.hipEventSynchronize.argtypes = [C.c_void_p]
-        self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        self.h.hipEventDestroy.argtypes = [C.c_void_p]
-
-    def create(self):
-        e = C.c_void_p()
-        assert self.h.hipEventCreate(C.byref(e)) == 0
-        return e
-
-    def record(self, e, stream):
-        assert self.h.hipEventRecord(e, C.c_void_p(stream)) == 0
-
-    def elapsed_ms(self, a, b):
-        assert self.h.hipEventSynchronize(b) == 0
-        ms = C.c_float()
-        assert self.h.hipEventElapsedTime(C.byref(ms), a, b) == 0
-        return ms.value
 
 
 def step_bytes(shape, dtype, kv_bytes, positions, window):
@@ -99,37 +72,35 @@ def main():
               "(independent streams shard across GPUs with no communication).", file=sys.stderr)
         sys.exit(2)
 
-    import torch
-
     import svl
+    from svl import hip
     from svl import workloads as W
 
     shape, dtype = W.S1, "q8_0"
-    tensors = W.make_weights_fast(shape, dtype, seed=0)
+    t0 = time.perf_counter()
+    tensors = W.make_weights(shape, dtype, seed=0)
+    print(f"weights generated in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     model = svl.Model(shape.config(W.quantize_code(dtype)), tensors, kv_dtype=svl.F32)
     n_total = args.warmup + args.steps
     audio = W.audio_tokens(shape, max(n_total, args.cpu_steps), seed=1)[0]
-    d_audio = torch.from_numpy(audio.astype(np.int32)).cuda()
-    d_out = torch.zeros(n_total, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
+    d_audio = hip.DeviceBuffer.from_array(audio)
+    d_out = hip.DeviceBuffer(n_total * 4)
 
     st = model.init_state()
-    ev = HipEvents()
-    e0, e1 = ev.create(), ev.create()
+    e0, e1 = hip.Event(), hip.Event()
     # warm-up, then restart the stream from position 0
-    model.recognize_async(args.warmup, d_audio.data_ptr(), d_out.data_ptr(), st)
+    model.recognize_async(args.warmup, d_audio.address, d_out.address, st)
     st.synchronize()
     st.reset()
-    st.synchronize()
-    torch.cuda.synchronize()
+    hip.synchronize()
     t0 = time.perf_counter()
-    ev.record(e0, st.stream)
-    model.recognize_async(args.steps, d_audio.data_ptr(), d_out.data_ptr(), st)
-    ev.record(e1, st.stream)
+    e0.record(st.stream)
+    model.recognize_async(args.steps, d_audio.address, d_out.address, st)
+    e1.record(st.stream)
     st.synchronize()
-    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = ev.elapsed_ms(e0, e1)
+    gpu_ms = e0.elapsed_ms(e1)
+    print(f"timed {args.steps} steps: {gpu_ms:.2f} ms", file=sys.stderr, flush=True)
     steps_per_s = args.steps / (gpu_ms / 1e3)
 
     bytes_per_step = step_bytes(shape, dtype, 4, range(args.steps), shape.context)
@@ -164,7 +135,7 @@ def main():
                                 "kind": "port",
                                 "sample": f"{args.cpu_steps} greedy steps of the same workload from position 0 "
                                           f"(oracle, {args.cpu_threads} threads)"}
-        gpu_toks = d_out.cpu().numpy()[: min(args.cpu_steps, args.steps)].astype(np.uint32)
+        gpu_toks = d_out.to_array(np.uint32, args.steps)[: min(args.cpu_steps, args.steps)]
         line["cpu_baseline"]["tokens_match"] = bool(np.array_equal(gpu_toks, toks[: gpu_toks.size]))
     print(json.dumps(line), flush=True)
 

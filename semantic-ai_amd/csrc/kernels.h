@@ -13,7 +13,6 @@ enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 
 // One linear layer as held on the device.
 //   FMT_F32 / FMT_BF16: w = [out][in] row-major.
 //   FMT_Q8_0: w = int8 quants [out][in]; scale = f16 block scales [out][in/32].
-//   FMT_Q4K: w = 144-byte candle blocks [out][in/256] (kept as given).
 struct LinearDev {
   int fmt = FMT_F32;
   int out = 0, in = 0;
@@ -23,8 +22,10 @@ struct LinearDev {
 
 struct GemvArgs {
   LinearDev L;
-  int B;               // batch rows (grid.y)
-  int ipw;             // work items per workgroup (set by launch_gemv)
+  int B;               // batch rows
+  int ipw;             // work items per unit (rows, or gate/value pairs for the SiLU gate)
+  int parts;           // units per batch row = ceil(items / ipw)
+  int maxb;            // Q8_0: weight blocks per thread and unit (1, 2, 4, 8 or 16)
   const float* x;      // input [B][x_stride]
   int x_stride;
   int norm;            // NormKind applied to x in the prologue
@@ -54,7 +55,7 @@ struct AttnArgs {
   const float* q;      // [B][H*hd]
   const void* kc;
   const void* vc;
-  const int* pos;
+  int* pos;
   int B, H, KVH, hd, cap, window;  // window 0 = unlimited
   int kv_bf16;
   float scale;
@@ -67,22 +68,92 @@ struct EmbedArgs {
   const void* emb;          // n_q tables back to back, [n_q][card+1][d]
   int tables_bf16;
   int d, n_q, card, text_card, B;
-  const uint32_t* text_tok; // [B] or null: use fb_tok
-  const uint32_t* fb_tok;   // [B] feedback tokens (previous argmax)
+  const uint32_t* text_tok; // [B] explicit tokens, or null: use fb_tok
+  uint32_t* fb_tok;         // [B] feedback tokens (previous argmax)
   const uint32_t* audio;    // [B][n_q]
   int initial_at_zero;      // a stream at position 0 sees `card` audio tokens
-  const int* pos;
+  int* pos;
   float* x;                 // [B][d]
 };
 
-hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
-hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
-hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
-hipError_t launch_norm(const float* x, int x_stride, float* y, int y_stride, int B, int d, int norm,
-                       const float* w, const float* b, float eps, hipStream_t s);
-// argmax over logits [B][V]; writes fb_tok[b] and, when out is not null, out[b]; advances pos.
-hipError_t launch_argmax(const float* logits, int B, int V, uint32_t* fb_tok, uint32_t* out, int* pos,
-                         hipStream_t s);
+struct ArgmaxArgs {
+  const float* logits;      // [B][V]
+  int B, V;
+  uint32_t* fb_tok;         // [B]
+  uint32_t* out;            // [B] or null
+};
+
+struct NormArgs {           // y[b] = norm(x[b]) (TTS out_norm without z_proj)
+  const float* x;
+  int x_stride;
+  float* y;
+  int y_stride;
+  int B, d, norm;
+  const float* w;
+  const float* b;
+  float eps;
+};
+
+struct CopyArgs {           // y[b][0..n) = x[b][0..n)
+  const float* x;
+  int x_stride;
+  float* y;
+  int y_stride;
+  int B, n;
+  int advance;              // step-indexed source/destination (see StepParams)
+};
+
+// One phase of a step program: a unit function applied to `units` work units.
+enum PhaseKind { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN_SCORES = 2, PH_ATTN_SOFTMAX_V = 3, PH_ARGMAX = 4, PH_NORM = 5,
+                 PH_COPY_IN = 6, PH_COPY_OUT = 7 };
+
+struct Phase {
+  int kind;
+  int units;
+  GemvArgs g;
+  AttnArgs at;
+  EmbedArgs e;
+  ArgmaxArgs am;
+  NormArgs nm;
+  CopyArgs cp;
+};
+
+// Grid barrier counters (device memory, zeroed at creation): 8 group counters and a top
+// counter, each in its own 128-byte line, the release generation, and an abort flag.
+struct SyncState {
+  unsigned group[8][32];
+  unsigned top[32];
+  unsigned release[32];
+  unsigned abort_flag[32];
+};
+
+// Per-launch inputs of a step program run for n_steps steps.
+struct StepParams {
+  const Phase* prog;
+  int nphase;
+  int n_steps;
+  SyncState* sync;
+  unsigned gen0;                 // barriers completed by earlier launches on this state
+  const uint32_t* audio;         // step s: audio + s * audio_stride
+  size_t audio_stride;
+  const uint32_t* text;          // step s: text + s * text_stride, or null (feedback)
+  size_t text_stride;
+  uint32_t* out_tok;             // step s: out_tok + s * out_stride, or null
+  size_t out_stride;
+  const float* fwd_in;           // [B][T][d], step s reads column s
+  float* fwd_out;
+  int fwd_T;
+};
+
+constexpr int kStepThreads = 256;
+
+hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s);
+hipError_t launch_phase(const Phase* d_ph, int units, const StepParams& p, int step, size_t smem, hipStream_t s);
+int step_program_grid(int device);
+size_t phase_smem(const Phase& ph);
+// Fills the unit layout of a GEMV phase (ipw, parts, maxb, units) for `grid` workgroups.
+void plan_gemv(GemvArgs& g, int grid, int* units);
+
 hipError_t launch_q8_quantize(const float* w, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_from_blocks(const uint8_t* blocks, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_to_blocks(const int8_t* qs, const uint16_t* d, int rows, int K, uint8_t* blocks, hipStream_t s);

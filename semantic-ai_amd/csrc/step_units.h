@@ -1,0 +1,631 @@
+// Work units of the decode step, run by one 256-thread workgroup each.  The same functions
+// back the one-kernel-per-phase launches and the persistent step-program kernel.
+//
+// Numerics follow the reference's CPU path (crates/semantic-voice-local/src = SVL) operation
+// for operation, so results are bit-identical to the CPU restatement in oracle/:
+//   * Q8_0 matmul as candle's quantized CPU matmul: the activation row is quantized to Q8_0
+//     (d = amax / 127 kept as f16, q = round(x * (1 / d))); each weight block contributes
+//     (exact i32 dot as f32 * d_w) * d_x, added in block order.
+//   * dense matvec with the reference's 16-lane dot (SVL/nn/kernels/mod.rs:66-91).
+//   * attention with the reference's two passes (SVL/nn/kernels/attention.rs:139-168).
+//   * SiLU / GELU-tanh / exp as SVL/nn/kernels/{activation,mod}.rs (FMA variant).
+//   * RMSNorm / LayerNorm statistics in a 64-way blocked order (see blocked_sum).
+//
+// Data one workgroup writes and another reads within a launch (activations, KV ring, scores,
+// logits, tokens, positions) goes through agent-scope coherent loads and stores (the `sc1`
+// cache policy on gfx950), so no cache-wide fence is needed at phase boundaries.
+#pragma once
+
+#include "device_math.h"
+#include "kernels.h"
+
+namespace svl {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---- coherent accesses -------------------------------------------------------------------------
+
+__device__ __forceinline__ float ld_co(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_co(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_co(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_co(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_co(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_co(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint16_t ld_co(const uint16_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_co(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool BF16KV>
+__device__ __forceinline__ float kv_ld(const void* base, size_t idx) {
+  if (BF16KV) return bf16_to_f32(ld_co((const uint16_t*)base + idx));
+  return ld_co((const float*)base + idx);
+}
+
+// Copies x[0..n) into xs with coherent loads, eight per thread in flight.
+__device__ __forceinline__ void stage_row(const float* x, int n, float* xs) {
+  constexpr int kRound = 8;
+  for (int i0 = 0; i0 < n; i0 += kRound * kStepThreads) {
+    float v[kRound];
+#pragma unroll
+    for (int k = 0; k < kRound; ++k) {
+      const int i = i0 + threadIdx.x + k * kStepThreads;
+      if (i < n) v[k] = ld_co(x + i);
+    }
+#pragma unroll
+    for (int k = 0; k < kRound; ++k) {
+      const int i = i0 + threadIdx.x + k * kStepThreads;
+      if (i < n) xs[i] = v[k];
+    }
+  }
+}
+
+// ---- row statistics, norms, activation quantization ---------------------------------------------
+
+// Sum of x[i] (or x[i]^2) over a row in the order shared with the oracle: 64 strided partials
+// (lane l adds x[l], x[l+64], ... in order), then a butterfly over the partials (offsets
+// 32 .. 1).  Every lane of every wave computes the same value.
+__device__ __forceinline__ float blocked_sum(const float* xs, int K, bool squares) {
+  const int lane = threadIdx.x % kWave;
+  float acc = 0.0f;
+  for (int i = lane; i < K; i += kWave) {
+    float v = xs[i];
+    if (squares) v = v * v;
+    acc = acc + v;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, kWave);
+  return acc;
+}
+
+// candle-nn rms_norm (x / m * alpha, m = sqrt(sum(x^2) / K + eps)) or layer_norm
+// ((x - mean) * (1 / sqrt(var + eps)) * w + b, var = sum(x^2) / K - mean^2) of xs in place.
+__device__ void norm_lds(float* xs, int K, int norm, const float* nw, const float* nb, float eps) {
+  __syncthreads();
+  if (norm == NORM_RMS) {
+    const float s2 = blocked_sum(xs, K, true);
+    const float m = sqrtf(s2 / (float)K + eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K; i += kStepThreads) {
+      float t = xs[i] / m;
+      xs[i] = t * nw[i];
+    }
+  } else {
+    const float s = blocked_sum(xs, K, false);
+    const float s2 = blocked_sum(xs, K, true);
+    const float mean = s / (float)K;
+    const float mm = mean * mean;
+    const float var = s2 / (float)K - mm;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K; i += kStepThreads) {
+      float t = (xs[i] - mean) * inv_std;
+      t = t * nw[i];
+      xs[i] = t + nb[i];
+    }
+  }
+  __syncthreads();
+}
+
+// candle BlockQ8_0::from_float of xs[0..K) into xq (int8) and xdq (the f16-rounded scales as
+// f32).  A half-wave owns one block per iteration (lane = element).
+__device__ void quantize_lds(const float* xs, int K, int8_t* xq, float* xdq) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  constexpr int nwaves = kStepThreads / kWave;
+  const int nb = K / 32;
+  for (int blk = wave * 2 + lane / 32; blk < nb; blk += nwaves * 2) {
+    float v = xs[blk * 32 + (lane % 32)];
+    float amax = half_max(fabsf(v));
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    xq[blk * 32 + (lane % 32)] = (int8_t)sat_i8(roundf(v * id));
+    if ((lane % 32) == 0) xdq[blk] = f16_to_f32(f32_to_f16(d));
+  }
+  __syncthreads();
+}
+
+// ---- GEMV epilogues ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row, float y, float yp, float yv) {
+  switch (a.epi) {
+    case EPI_STORE:
+      st_co(a.y + (size_t)b * a.y_stride + row, y);
+      break;
+    case EPI_GELU:
+      st_co(a.y + (size_t)b * a.y_stride + row, ref_gelu_tanh(y));
+      break;
+    case EPI_SILU_GATE: {
+      // FeedForwardLayer::forward, gated (SVL/nn/transformer.rs:453-461): silu(gate) * value
+      float g = ref_silu(y);
+      st_co(a.y + (size_t)b * a.y_stride + row, g * yv);
+      break;
+    }
+    case EPI_RESID: {
+      float u = y;
+      if (a.lscale) u = u * a.lscale[row];
+      float* r = a.resid + (size_t)b * a.resid_stride + row;
+      st_co(r, ld_co(r) + u);
+      break;
+    }
+    case EPI_QKV_ROPE: {
+      // split q | k | v (transformer.rs:330-338); interleaved RoPE of q and k (rope_i); k and v
+      // into the ring slot of the current position.
+      const int qdim = a.H * a.hd, kvdim = a.KVH * a.hd;
+      const int p = ld_co(a.pos + b);
+      const int region = row < qdim ? 0 : (row < qdim + kvdim ? 1 : 2);
+      const int rr = region == 0 ? row : (region == 1 ? row - qdim : row - qdim - kvdim);
+      const int head = rr / a.hd, dim = rr % a.hd;
+      float out = y;
+      if (region < 2) {
+        const float* cs = a.rope + ((size_t)p * (a.hd / 2) + dim / 2) * 2;
+        const float c = cs[0], s = cs[1];
+        if ((dim & 1) == 0) {
+          float t0 = y * c, t1 = yp * s;
+          out = t0 - t1;
+        } else {
+          float t0 = yp * s, t1 = y * c;
+          out = t0 + t1;
+        }
+      }
+      if (region == 0) {
+        st_co(a.q_out + (size_t)b * qdim + rr, out);
+      } else {
+        const size_t idx = (((size_t)b * a.KVH + head) * a.cap + (size_t)(p % a.cap)) * a.hd + dim;
+        void* base = region == 1 ? a.kc : a.vc;
+        if (a.kv_bf16) st_co((uint16_t*)base + idx, f32_to_bf16(out));
+        else st_co((float*)base + idx, out);
+      }
+      break;
+    }
+  }
+}
+
+__device__ __forceinline__ int gemv_phys_row(const GemvArgs& a, int i0, int ni, int r) {
+  if (a.epi == EPI_SILU_GATE) return r < ni ? i0 + r : i0 + (r - ni) + a.ff_hidden;
+  return i0 + r;
+}
+
+__device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, int i0, int ni, const float* Y) {
+  const int t = threadIdx.x;
+  if (t < ni) {
+    const float y = Y[t];
+    const float yp = a.epi == EPI_QKV_ROPE ? Y[t ^ 1] : 0.0f;
+    const float yv = a.epi == EPI_SILU_GATE ? Y[ni + t] : 0.0f;
+    gemv_epilogue(a, b, i0 + t, y, yp, yv);
+  }
+  if (a.advance_pos && part == 0 && t == 0) st_co(a.pos + b, ld_co(a.pos + b) + 1);
+}
+
+__device__ __forceinline__ int gemv_items(const GemvArgs& a) {
+  return a.epi == EPI_SILU_GATE ? a.ff_hidden : a.L.out;
+}
+
+// ---- Q8_0 GEMV unit ---------------------------------------------------------------------------
+// Candle's quantized CPU matmul (SVL/nn/mod.rs:97; BlockQ8_0::vec_dot_unopt): terms
+// (exact i32 block dot as f32 * d_w) * d_x, each row adding its terms in block order.  The
+// unit's weight blocks (one 32-byte block per thread and round) are loaded before the input is
+// staged, since they do not depend on it.
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <int MAXB>
+__device__ void gemv_q8_unit(const GemvArgs& a, int unit, unsigned char* smem) {
+  const int K = a.L.in, nb = K / 32;
+  const int b = unit / a.parts, part = unit % a.parts;
+  const bool silu = a.epi == EPI_SILU_GATE;
+  const int i0 = part * a.ipw;
+  const int ni = min(a.ipw, gemv_items(a) - i0);
+  const int NR = silu ? 2 * ni : ni;
+  const int total = NR * nb;
+  const int ts = nb + 1;
+  float* xs = (float*)smem;             // K
+  int8_t* xq = (int8_t*)(xs + K);       // K
+  float* xdq = (float*)(xq + K);        // nb
+  float* T = xdq + nb;                  // 2 * ipw * ts
+  float* Y = T + 2 * a.ipw * ts;        // 2 * ipw
+
+  const int8_t* wq = (const int8_t*)a.L.w;
+  v4i wa[MAXB], wb[MAXB];
+  uint16_t wd[MAXB];
+#pragma unroll
+  for (int k = 0; k < MAXB; ++k) {
+    const int idx = threadIdx.x + k * kStepThreads;
+    if (idx < total) {
+      const int r = idx / nb, blk = idx - r * nb;
+      const size_t row = (size_t)gemv_phys_row(a, i0, ni, r);
+      const v4i* p = (const v4i*)(wq + row * K + (size_t)blk * 32);
+      wa[k] = __builtin_nontemporal_load(p);
+      wb[k] = __builtin_nontemporal_load(p + 1);
+      wd[k] = a.L.scale[row * nb + blk];
+    }
+  }
+  __syncthreads();
+  stage_row(a.x + (size_t)b * a.x_stride, K, xs);
+  if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
+  else __syncthreads();
+  quantize_lds(xs, K, xq, xdq);
+#pragma unroll
+  for (int k = 0; k < MAXB; ++k) {
+    const int idx = threadIdx.x + k * kStepThreads;
+    if (idx < total) {
+      const int r = idx / nb, blk = idx - r * nb;
+      const v4i xa = *(const v4i*)(xq + blk * 32);
+      const v4i xb = *(const v4i*)(xq + blk * 32 + 16);
+      int s = sdot4(wa[k].x, xa.x, 0);
+      s = sdot4(wa[k].y, xa.y, s);
+      s = sdot4(wa[k].z, xa.z, s);
+      s = sdot4(wa[k].w, xa.w, s);
+      s = sdot4(wb[k].x, xb.x, s);
+      s = sdot4(wb[k].y, xb.y, s);
+      s = sdot4(wb[k].z, xb.z, s);
+      s = sdot4(wb[k].w, xb.w, s);
+      float t = (float)s * f16_to_f32(wd[k]);
+      T[r * ts + blk] = t * xdq[blk];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < NR) {
+    const float* tr = T + threadIdx.x * ts;
+    float acc = 0.0f;
+    for (int blk = 0; blk < nb; ++blk) acc = acc + tr[blk];
+    Y[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  gemv_finish(a, b, part, i0, ni, Y);
+}
+
+// ---- dense GEMV unit ----------------------------------------------------------------------------
+// The reference's matvec (SVL/nn/kernels/matvec.rs:239-246) with its 16-lane dot
+// (kernels/mod.rs:66-91): 16 threads per row, thread i accumulating x[16c + i] * w[16c + i]
+// with FMA over c, then the pairwise lane sum and the scalar tail.  16 rows per unit
+// (8 gate/value pairs for the SiLU gate).
+
+template <bool BF16W>
+__device__ void gemv_dense_unit(const GemvArgs& a, int unit, unsigned char* smem) {
+  const int K = a.L.in;
+  const int b = unit / a.parts, part = unit % a.parts;
+  const bool silu = a.epi == EPI_SILU_GATE;
+  const int i0 = part * a.ipw;
+  const int ni = min(a.ipw, gemv_items(a) - i0);
+  const int NR = silu ? 2 * ni : ni;
+  float* xs = (float*)smem;   // K
+  float* Y = xs + K;          // 16
+  __syncthreads();
+  stage_row(a.x + (size_t)b * a.x_stride, K, xs);
+  if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
+  else __syncthreads();
+  const int g = threadIdx.x / 16, li = threadIdx.x % 16;
+  const int chunks = K / 16;
+  if (g < NR) {
+    const size_t row = (size_t)gemv_phys_row(a, i0, ni, g);
+    float acc = 0.0f;
+    int c = 0;
+    if (BF16W) {
+      const uint16_t* w = (const uint16_t*)a.L.w + row * K + li;
+      for (; c + 8 <= chunks; c += 8) {
+        uint16_t wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(xs[(c + u) * 16 + li], bf16_to_f32(wv[u]), acc);
+      }
+      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], bf16_to_f32(w[(size_t)c * 16]), acc);
+    } else {
+      const float* w = (const float*)a.L.w + row * K + li;
+      for (; c + 8 <= chunks; c += 8) {
+        float wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(xs[(c + u) * 16 + li], wv[u], acc);
+      }
+      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], w[(size_t)c * 16], acc);
+    }
+    // pairwise lane sum: acc[i] += acc[i + width] for width 8, 4, 2, 1
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
+    if (li == 0) {
+      float tail = 0.0f;
+      for (int i = chunks * 16; i < K; ++i) {
+        const float wv = BF16W ? bf16_to_f32(((const uint16_t*)a.L.w)[row * K + i]) : ((const float*)a.L.w)[row * K + i];
+        float p = xs[i] * wv;
+        tail = tail + p;
+      }
+      Y[g] = acc + tail;
+    }
+  }
+  __syncthreads();
+  gemv_finish(a, b, part, i0, ni, Y);
+}
+
+__device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, unsigned char* smem) {
+  if (a.L.fmt == FMT_Q8_0) {
+    switch (a.maxb) {
+      case 1: gemv_q8_unit<1>(a, unit, smem); break;
+      case 2: gemv_q8_unit<2>(a, unit, smem); break;
+      case 4: gemv_q8_unit<4>(a, unit, smem); break;
+      case 8: gemv_q8_unit<8>(a, unit, smem); break;
+      default: gemv_q8_unit<16>(a, unit, smem); break;
+    }
+  } else if (a.L.fmt == FMT_BF16) {
+    gemv_dense_unit<true>(a, unit, smem);
+  } else {
+    gemv_dense_unit<false>(a, unit, smem);
+  }
+}
+
+// ---- attention units ----------------------------------------------------------------------------
+// The query at position p attends to keys max(0, p - window + 1) ..= p (transformer.rs:385) in
+// the ring, in the reference's order (attention.rs:139-168):
+//   scores:    w_j = scale * dot(q, k_j) with the 16-lane dot; 16 keys per unit, one per
+//              16-thread group.  Units: B x H x ceil(cap / 16), the ones past a stream's keys idle.
+//   softmax_v: max, e_j = exp(w_j - max), sum of e_j in key order, then
+//              out = sum over keys in order of mul_add(e_j / sum, v_j, out).  One unit per
+//              (stream, head); wave w produces dims [32w, 32w + 32).
+
+constexpr int kKeysPerUnit = 16;
+
+template <int HD, bool BF16KV>
+__device__ void attn_scores_unit(const AttnArgs& a, int unit) {
+  const int chunks = (a.cap + kKeysPerUnit - 1) / kKeysPerUnit;
+  const int chunk = unit % chunks;
+  const int h = (unit / chunks) % a.H;
+  const int b = unit / (chunks * a.H);
+  const int p = ld_co(a.pos + b);
+  const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
+  const int jj = chunk * kKeysPerUnit + threadIdx.x / 16;
+  if (chunk * kKeysPerUnit >= L) return;
+  const int li = threadIdx.x % 16;
+  constexpr int C = HD / 16;
+  const int kvh = h / (a.H / a.KVH);
+  const float* qp = a.q + (size_t)b * a.H * HD + (size_t)h * HD + li;
+  float q[C], kv[C];
+  const bool live = jj < L;
+  const int j = p + 1 - L + jj;
+  const size_t base = ((((size_t)b * a.KVH + kvh) * (size_t)a.cap) + (size_t)(live ? j % a.cap : 0)) * HD + li;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    q[c] = ld_co(qp + c * 16);
+    kv[c] = kv_ld<BF16KV>(a.kc, base + c * 16);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) acc = fmaf(q[c], kv[c], acc);
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
+  if (live && li == 0) st_co(a.scores + ((size_t)b * a.H + h) * a.cap + jj, a.scale * (acc + 0.0f));
+}
+
+template <int HD, bool BF16KV>
+__device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, unsigned char* smem) {
+  float* w = (float*)smem;           // L weights
+  float* sum_slot = w + a.cap;       // 1
+  const int h = unit % a.H, b = unit / a.H;
+  const int p = ld_co(a.pos + b);
+  const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
+  const int first = p + 1 - L;
+  const float* sc = a.scores + ((size_t)b * a.H + h) * a.cap;
+  __syncthreads();
+  for (int j0 = 0; j0 < L; j0 += 8 * kStepThreads) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + threadIdx.x + u * kStepThreads;
+      if (j < L) v[u] = ld_co(sc + j);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + threadIdx.x + u * kStepThreads;
+      if (j < L) w[j] = v[u];
+    }
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (wave == 0) {
+    float mx = -__builtin_huge_valf();
+    for (int j = lane; j < L; j += kWave) mx = fmaxf(mx, w[j]);
+    mx = wave_max(mx);
+    for (int j = lane; j < L; j += kWave) w[j] = ref_exp(w[j] - mx);
+    if (lane == 0) {
+      float sum = 0.0f;
+      for (int j = 0; j < L; ++j) sum = sum + w[j];
+      sum_slot[0] = sum;
+    }
+  }
+  __syncthreads();
+  const float sum = sum_slot[0];
+  for (int j = threadIdx.x; j < L; j += kStepThreads) w[j] = w[j] / sum;
+  __syncthreads();
+  if (wave < HD / 32 && lane < 32) {
+    const int d = wave * 32 + lane;
+    const int kvh = h / (a.H / a.KVH);
+    const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
+    float acc = 0.0f;
+    int j = 0;
+    for (; j + 16 <= L; j += 16) {
+      float vv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) vv[u] = kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + j + u) % a.cap)) * HD + d);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc = fmaf(w[j + u], vv[u], acc);
+    }
+    for (; j < L; ++j) acc = fmaf(w[j], kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + j) % a.cap)) * HD + d), acc);
+    st_co(a.out + (size_t)b * a.H * HD + (size_t)h * HD + d, acc);
+  }
+}
+
+__device__ __forceinline__ void attn_scores_dispatch(const AttnArgs& a, int unit) {
+  if (a.hd == 128) {
+    if (a.kv_bf16) attn_scores_unit<128, true>(a, unit);
+    else attn_scores_unit<128, false>(a, unit);
+  } else {
+    if (a.kv_bf16) attn_scores_unit<64, true>(a, unit);
+    else attn_scores_unit<64, false>(a, unit);
+  }
+}
+
+__device__ __forceinline__ void attn_softmax_v_dispatch(const AttnArgs& a, int unit, unsigned char* smem) {
+  if (a.hd == 128) {
+    if (a.kv_bf16) attn_softmax_v_unit<128, true>(a, unit, smem);
+    else attn_softmax_v_unit<128, false>(a, unit, smem);
+  } else {
+    if (a.kv_bf16) attn_softmax_v_unit<64, true>(a, unit, smem);
+    else attn_softmax_v_unit<64, false>(a, unit, smem);
+  }
+}
+
+// ---- embedding, argmax, norm, copies ----------------------------------------------------------
+
+// SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
+// ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 256.
+__device__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit) {
+  const int chunks = (a.d + kStepThreads - 1) / kStepThreads;
+  const int b = unit / chunks;
+  const int i = (unit % chunks) * kStepThreads + threadIdx.x;
+  if (i >= a.d) return;
+  uint32_t t = text ? text[b] : ld_co(a.fb_tok + b);
+  t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
+  const bool initial = a.initial_at_zero && ld_co(a.pos + b) == 0;
+  const size_t rows = (size_t)a.card + 1;
+  const uint32_t* au = audio + (size_t)b * a.n_q;
+  float x = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.text_emb)[(size_t)t * a.d + i])
+                          : ((const float*)a.text_emb)[(size_t)t * a.d + i];
+  for (int c0 = 0; c0 < a.n_q; c0 += 8) {
+    float e[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = c0 + u;
+      e[u] = 0.0f;
+      if (c < a.n_q) {
+        uint32_t tok = initial ? (uint32_t)a.card : au[c];
+        tok = tok > (uint32_t)a.card ? (uint32_t)a.card : tok;
+        const size_t idx = ((size_t)c * rows + tok) * a.d + i;
+        e[u] = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.emb)[idx]) : ((const float*)a.emb)[idx];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (c0 + u < a.n_q) x = x + e[u];
+  }
+  st_co(a.x + (size_t)b * a.d + i, x);
+}
+
+// argmax over logits[b] (first index of the maximum); unit = stream.
+__device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsigned char* smem) {
+  float* sv = (float*)smem;
+  int* si = (int*)(sv + 16);
+  const int b = unit;
+  const float* lg = a.logits + (size_t)b * a.V;
+  float best = -__builtin_huge_valf();
+  int idx = 0x7fffffff;
+  for (int i0 = 0; i0 < a.V; i0 += 8 * kStepThreads) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + threadIdx.x + u * kStepThreads;
+      if (i < a.V) v[u] = ld_co(lg + i);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + threadIdx.x + u * kStepThreads;
+      if (i < a.V && (idx == 0x7fffffff || v[u] > best)) {
+        best = v[u];
+        idx = i;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(best, o, kWave);
+    const int oi = __shfl_xor(idx, o, kWave);
+    if (oi != 0x7fffffff && (idx == 0x7fffffff || ov > best || (ov == best && oi < idx))) {
+      best = ov;
+      idx = oi;
+    }
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bv = sv[0];
+    int bi = si[0];
+    for (int w = 1; w < kStepThreads / kWave; ++w) {
+      if (si[w] != 0x7fffffff && (bi == 0x7fffffff || sv[w] > bv || (sv[w] == bv && si[w] < bi))) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    }
+    if (bi == 0x7fffffff) bi = 0;
+    st_co(a.fb_tok + b, (uint32_t)bi);
+    if (out) st_co(out + b, (uint32_t)bi);
+  }
+}
+
+// y[b] = norm(x[b]); unit = stream.
+__device__ void norm_unit(const NormArgs& a, int unit, unsigned char* smem) {
+  float* xs = (float*)smem;
+  __syncthreads();
+  stage_row(a.x + (size_t)unit * a.x_stride, a.d, xs);
+  norm_lds(xs, a.d, a.norm, a.w, a.b, a.eps);
+  for (int i = threadIdx.x; i < a.d; i += kStepThreads) st_co(a.y + (size_t)unit * a.y_stride + i, xs[i]);
+}
+
+// y[b][0..n) = x[b][0..n); unit = (stream, 256-element chunk).
+__device__ void copy_unit(const float* x, int x_stride, float* y, int y_stride, int n, int unit) {
+  const int chunks = (n + kStepThreads - 1) / kStepThreads;
+  const int b = unit / chunks;
+  const int i = (unit % chunks) * kStepThreads + threadIdx.x;
+  if (i < n) st_co(y + (size_t)b * y_stride + i, ld_co(x + (size_t)b * x_stride + i));
+}
+
+// Runs work unit `unit` of phase `ph` for step `step` of a launch.
+__device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, unsigned char* smem) {
+  switch (ph.kind) {
+    case PH_EMBED: {
+      const uint32_t* text = P.text ? P.text + (size_t)step * P.text_stride : nullptr;
+      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit);
+      break;
+    }
+    case PH_GEMV:
+      gemv_unit(ph.g, unit, smem);
+      break;
+    case PH_ATTN_SCORES:
+      attn_scores_dispatch(ph.at, unit);
+      break;
+    case PH_ATTN_SOFTMAX_V:
+      attn_softmax_v_dispatch(ph.at, unit, smem);
+      break;
+    case PH_ARGMAX:
+      argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem);
+      break;
+    case PH_NORM:
+      norm_unit(ph.nm, unit, smem);
+      break;
+    case PH_COPY_IN:
+      copy_unit(P.fwd_in + (size_t)step * ph.cp.n, ph.cp.x_stride, ph.cp.y, ph.cp.y_stride, ph.cp.n, unit);
+      break;
+    case PH_COPY_OUT:
+      copy_unit(ph.cp.x, ph.cp.x_stride, P.fwd_out + (size_t)step * ph.cp.n, ph.cp.y_stride, ph.cp.n, unit);
+      break;
+  }
+}
+
+}  // namespace svl

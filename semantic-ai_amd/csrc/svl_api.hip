@@ -115,6 +115,12 @@ struct svl_model {
   }
 };
 
+struct Program {
+  std::vector<Phase> phases;
+  Phase* dev = nullptr;  // device copy
+  size_t smem = 0;       // dynamic LDS of the largest phase
+};
+
 struct svl_state {
   const svl_model* m = nullptr;
   int B = 1;
@@ -127,10 +133,17 @@ struct svl_state {
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
   float* scores = nullptr;    // [B][H][slots]
-  float* in = nullptr;        // TTS latent / forward input staging
+  float* in = nullptr;        // TTS latent staging [B][latent_dim]
+  float* fwd = nullptr;       // transformer forward staging (input then output)
+  size_t fwd_cap = 0;
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
   uint32_t* tok_out = nullptr;
-  size_t in_cap = 0;
+  // step programs and the grid barrier of the persistent kernel
+  Program stt, tts, fwd_prog;
+  SyncState* sync = nullptr;
+  unsigned gen = 0;
+  int grid = 0;
+  bool persistent = true;
 
   ~svl_state() {
     hipSetDevice(m->device);
@@ -417,105 +430,241 @@ const LinearDev* find_linear(const svl_model* m, const char* name) {
 
 int norm_code(const svl_config& c) { return c.norm_kind == SVL_NORM_RMS ? NORM_RMS : NORM_LAYER; }
 
-// One step of every stream through all layers, from s->x (the embedded input) to s->x (the
-// transformer output).  Advances the positions at the end.
-int run_layers(const svl_model* m, svl_state* s) {
+Phase gemv_phase(const svl_state* s, const LinearDev& L) {
+  Phase ph{};
+  ph.kind = PH_GEMV;
+  ph.g.L = L;
+  ph.g.B = s->B;
+  return ph;
+}
+
+void add_gemv(const svl_state* s, std::vector<Phase>& out, Phase ph) {
+  plan_gemv(ph.g, s->grid, &ph.units);
+  out.push_back(ph);
+}
+
+// The layers of one step (Layer::forward, SVL/nn/transformer.rs:222-250): s->x in, s->x out.
+// The last layer's feed-forward output advances the positions: no later phase of the step
+// reads them.
+void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& out) {
   const svl_config& c = m->cfg;
-  const float* rope;
-  {
-    std::lock_guard<std::mutex> lock(m->rope_mu);
-    rope = m->rope;
-  }
   const int d = c.d_model, hd = c.head_dim, H = c.num_heads, KVH = c.num_kv_heads;
+  const int kv_bf16 = c.kv_dtype == SVL_BF16;
   for (int i = 0; i < c.num_layers; ++i) {
     const Layer& L = m->layers[i];
-    GemvArgs g{};
-    g.B = s->B;
-    // norm1 -> in_proj -> RoPE(q, k) -> q buffer, KV ring
-    g.L = L.in_proj;
-    g.x = s->x;
-    g.x_stride = d;
-    g.norm = norm_code(c);
-    g.nw = L.n1w;
-    g.nb = L.n1b;
-    g.eps = c.norm_eps;
-    g.epi = EPI_QKV_ROPE;
-    g.pos = s->pos;
-    g.rope = rope;
-    g.H = H;
-    g.KVH = KVH;
-    g.hd = hd;
-    g.q_out = s->q;
-    g.kc = s->kc[i];
-    g.vc = s->vc[i];
-    g.cap = s->slots;
-    g.kv_bf16 = c.kv_dtype == SVL_BF16;
-    HIP_TRY(launch_gemv(g, s->stream));
+    // norm1 -> in_proj -> RoPE(q, k) -> q buffer and KV ring
+    Phase g = gemv_phase(s, L.in_proj);
+    g.g.x = s->x;
+    g.g.x_stride = d;
+    g.g.norm = norm_code(c);
+    g.g.nw = L.n1w;
+    g.g.nb = L.n1b;
+    g.g.eps = c.norm_eps;
+    g.g.epi = EPI_QKV_ROPE;
+    g.g.pos = s->pos;
+    g.g.rope = nullptr;  // set per launch (the table grows)
+    g.g.H = H;
+    g.g.KVH = KVH;
+    g.g.hd = hd;
+    g.g.q_out = s->q;
+    g.g.kc = s->kc[i];
+    g.g.vc = s->vc[i];
+    g.g.cap = s->slots;
+    g.g.kv_bf16 = kv_bf16;
+    add_gemv(s, out, g);
     // attention over the ring
-    AttnArgs a{};
-    a.q = s->q;
-    a.kc = s->kc[i];
-    a.vc = s->vc[i];
-    a.pos = s->pos;
-    a.B = s->B;
-    a.H = H;
-    a.KVH = KVH;
-    a.hd = hd;
-    a.cap = s->slots;
-    a.window = c.context;
-    a.kv_bf16 = c.kv_dtype == SVL_BF16;
-    a.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
-    a.scores = s->scores;
-    a.out = s->att;
-    HIP_TRY(launch_attention(a, s->stream));
-    // out_proj + residual
-    GemvArgs o{};
-    o.B = s->B;
-    o.L = L.out_proj;
-    o.x = s->att;
-    o.x_stride = H * hd;
-    o.norm = NORM_NONE;
-    o.epi = EPI_RESID;
-    o.resid = s->x;
-    o.resid_stride = d;
-    o.lscale = L.ls1;
-    HIP_TRY(launch_gemv(o, s->stream));
-    // norm2 -> feed-forward in
-    GemvArgs f{};
-    f.B = s->B;
-    f.L = L.ff1;
-    f.x = s->x;
-    f.x_stride = d;
-    f.norm = norm_code(c);
-    f.nw = L.n2w;
-    f.nb = L.n2b;
-    f.eps = c.norm_eps;
-    f.y = s->h;
-    f.y_stride = c.ff_hidden;
+    Phase a{};
+    a.at.q = s->q;
+    a.at.kc = s->kc[i];
+    a.at.vc = s->vc[i];
+    a.at.pos = s->pos;
+    a.at.B = s->B;
+    a.at.H = H;
+    a.at.KVH = KVH;
+    a.at.hd = hd;
+    a.at.cap = s->slots;
+    a.at.window = c.context;
+    a.at.kv_bf16 = kv_bf16;
+    a.at.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
+    a.at.scores = s->scores;
+    a.at.out = s->att;
+    a.kind = PH_ATTN_SCORES;
+    a.units = s->B * H * ((s->slots + 15) / 16);
+    out.push_back(a);
+    a.kind = PH_ATTN_SOFTMAX_V;
+    a.units = s->B * H;
+    out.push_back(a);
+    // out_proj + residual (layer scale if any)
+    Phase o = gemv_phase(s, L.out_proj);
+    o.g.x = s->att;
+    o.g.x_stride = H * hd;
+    o.g.norm = NORM_NONE;
+    o.g.epi = EPI_RESID;
+    o.g.resid = s->x;
+    o.g.resid_stride = d;
+    o.g.lscale = L.ls1;
+    add_gemv(s, out, o);
+    // norm2 -> feed-forward in (SiLU gate or GELU)
+    Phase f = gemv_phase(s, L.ff1);
+    f.g.x = s->x;
+    f.g.x_stride = d;
+    f.g.norm = norm_code(c);
+    f.g.nw = L.n2w;
+    f.g.nb = L.n2b;
+    f.g.eps = c.norm_eps;
+    f.g.y = s->h;
+    f.g.y_stride = c.ff_hidden;
     if (c.ff_kind == SVL_FF_GATED_SILU) {
-      f.epi = EPI_SILU_GATE;
-      f.ff_hidden = c.ff_hidden;
+      f.g.epi = EPI_SILU_GATE;
+      f.g.ff_hidden = c.ff_hidden;
     } else {
-      f.epi = EPI_GELU;
+      f.g.epi = EPI_GELU;
     }
-    HIP_TRY(launch_gemv(f, s->stream));
-    // feed-forward out + residual (the last layer advances the positions: no later kernel of
-    // the step reads them)
-    GemvArgs f2{};
-    f2.B = s->B;
-    f2.L = L.ff2;
-    f2.x = s->h;
-    f2.x_stride = c.ff_hidden;
-    f2.norm = NORM_NONE;
-    f2.epi = EPI_RESID;
-    f2.resid = s->x;
-    f2.resid_stride = d;
-    f2.lscale = L.ls2;
-    f2.pos = s->pos;
-    f2.advance_pos = i == c.num_layers - 1;
-    HIP_TRY(launch_gemv(f2, s->stream));
+    add_gemv(s, out, f);
+    // feed-forward out + residual
+    Phase f2 = gemv_phase(s, L.ff2);
+    f2.g.x = s->h;
+    f2.g.x_stride = c.ff_hidden;
+    f2.g.norm = NORM_NONE;
+    f2.g.epi = EPI_RESID;
+    f2.g.resid = s->x;
+    f2.g.resid_stride = d;
+    f2.g.lscale = L.ls2;
+    f2.g.pos = s->pos;
+    f2.g.advance_pos = i == c.num_layers - 1;
+    add_gemv(s, out, f2);
   }
-  for (auto& p : s->pos_host) p += 1;
+}
+
+int upload_program(svl_state* s, Program& p) {
+  p.smem = 0;
+  for (const Phase& ph : p.phases) p.smem = std::max(p.smem, phase_smem(ph));
+  void* d;
+  TRY(s->alloc(&d, p.phases.size() * sizeof(Phase)));
+  HIP_TRY(hipMemcpy(d, p.phases.data(), p.phases.size() * sizeof(Phase), hipMemcpyHostToDevice));
+  p.dev = (Phase*)d;
+  return 0;
+}
+
+// Writes the current RoPE table pointer into the program's in_proj phases (host and device
+// copies) when it changed.
+int refresh_rope(svl_state* s, Program& p, const float* rope) {
+  bool changed = false;
+  for (Phase& ph : p.phases)
+    if (ph.kind == PH_GEMV && ph.g.epi == EPI_QKV_ROPE && ph.g.rope != rope) {
+      ph.g.rope = rope;
+      changed = true;
+    }
+  if (changed)
+    HIP_TRY(hipMemcpyAsync(p.dev, p.phases.data(), p.phases.size() * sizeof(Phase), hipMemcpyHostToDevice, s->stream));
+  return 0;
+}
+
+// Builds the STT, TTS and forward programs of a state (SVL/stt/model.rs:239-276,
+// SVL/tts/flow_lm.rs:169-180, SVL/nn/transformer.rs:139-186).
+int build_programs(const svl_model* m, svl_state* s) {
+  const svl_config& c = m->cfg;
+  const int d = c.d_model;
+  if (c.kind == SVL_MODEL_STT) {
+    std::vector<Phase>& P = s->stt.phases;
+    Phase e{};
+    e.kind = PH_EMBED;
+    e.e.text_emb = m->text_emb;
+    e.e.emb = m->emb;
+    e.e.tables_bf16 = m->tables_bf16;
+    e.e.d = d;
+    e.e.n_q = c.n_q;
+    e.e.card = c.card;
+    e.e.text_card = c.text_card;
+    e.e.B = s->B;
+    e.e.fb_tok = s->fb_tok;
+    e.e.initial_at_zero = 1;
+    e.e.pos = s->pos;
+    e.e.x = s->x;
+    e.units = s->B * ((d + kStepThreads - 1) / kStepThreads);
+    P.push_back(e);
+    build_layers(m, s, P);
+    Phase t = gemv_phase(s, m->text_linear);
+    t.g.x = s->x;
+    t.g.x_stride = d;
+    t.g.norm = NORM_RMS;
+    t.g.nw = m->out_norm_w;
+    t.g.eps = 1e-8f;  // SVL/stt/model.rs:252
+    t.g.epi = EPI_STORE;
+    t.g.y = s->logits;
+    t.g.y_stride = c.text_card;
+    add_gemv(s, P, t);
+    Phase am{};
+    am.kind = PH_ARGMAX;
+    am.am.logits = s->logits;
+    am.am.B = s->B;
+    am.am.V = c.text_card;
+    am.am.fb_tok = s->fb_tok;
+    am.units = s->B;
+    P.push_back(am);
+    TRY(upload_program(s, s->stt));
+  }
+  if (c.kind == SVL_MODEL_TTS) {
+    std::vector<Phase>& P = s->tts.phases;
+    Phase in = gemv_phase(s, m->input_linear);
+    in.g.x = s->in;
+    in.g.x_stride = c.latent_dim;
+    in.g.norm = NORM_NONE;
+    in.g.epi = EPI_STORE;
+    in.g.y = s->x;
+    in.g.y_stride = d;
+    add_gemv(s, P, in);
+    build_layers(m, s, P);
+    if (c.z_dim > 0) {
+      Phase z = gemv_phase(s, m->z_proj);
+      z.g.x = s->x;
+      z.g.x_stride = d;
+      z.g.norm = NORM_LAYER;
+      z.g.nw = m->out_norm_w;
+      z.g.nb = m->out_norm_b;
+      z.g.eps = 1e-5f;  // SVL/tts/flow_lm.rs:176
+      z.g.epi = EPI_STORE;
+      z.g.y = s->z;
+      z.g.y_stride = c.z_dim;
+      add_gemv(s, P, z);
+    } else {
+      Phase n{};
+      n.kind = PH_NORM;
+      n.nm.x = s->x;
+      n.nm.x_stride = d;
+      n.nm.y = s->z;
+      n.nm.y_stride = d;
+      n.nm.B = s->B;
+      n.nm.d = d;
+      n.nm.norm = NORM_LAYER;
+      n.nm.w = m->out_norm_w;
+      n.nm.b = m->out_norm_b;
+      n.nm.eps = 1e-5f;
+      n.units = s->B;
+      P.push_back(n);
+    }
+    TRY(upload_program(s, s->tts));
+  }
+  {
+    // Transformer::forward one position at a time (causal attention makes this the reference's
+    // block forward, transformer.rs:139-186): x[b] = in[b][t]; layers; out[b][t] = x[b].
+    std::vector<Phase>& P = s->fwd_prog.phases;
+    Phase ci{};
+    ci.kind = PH_COPY_IN;
+    ci.cp.y = s->x;
+    ci.cp.y_stride = d;
+    ci.cp.B = s->B;
+    ci.cp.n = d;
+    ci.units = s->B * ((d + kStepThreads - 1) / kStepThreads);
+    P.push_back(ci);
+    build_layers(m, s, P);
+    Phase co = ci;
+    co.kind = PH_COPY_OUT;
+    co.cp.x = s->x;
+    co.cp.x_stride = d;
+    P.push_back(co);
+    TRY(upload_program(s, s->fwd_prog));
+  }
   return 0;
 }
 
@@ -533,47 +682,47 @@ int check_room(const svl_state* s, int64_t steps) {
   return ensure_rope(s->m, top);
 }
 
-// text_linear over out_norm(x), then argmax into the feedback tokens (and `out` if given).
-int run_stt_head(const svl_model* m, svl_state* s, uint32_t* out) {
-  const svl_config& c = m->cfg;
-  GemvArgs g{};
-  g.B = s->B;
-  g.L = m->text_linear;
-  g.x = s->x;
-  g.x_stride = c.d_model;
-  g.norm = NORM_RMS;
-  g.nw = m->out_norm_w;
-  g.eps = 1e-8f;  // SVL/stt/model.rs:252
-  g.epi = EPI_STORE;
-  g.y = s->logits;
-  g.y_stride = c.text_card;
-  HIP_TRY(launch_gemv(g, s->stream));
-  HIP_TRY(launch_argmax(s->logits, s->B, c.text_card, s->fb_tok, out, nullptr, s->stream));
+// Runs `n_steps` steps of program `p` on the state's stream: one persistent launch, or one
+// launch per phase.
+int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
+  const float* rope;
+  {
+    std::lock_guard<std::mutex> lock(s->m->rope_mu);
+    rope = s->m->rope;
+  }
+  TRY(refresh_rope(s, p, rope));
+  P.prog = p.dev;
+  P.nphase = (int)p.phases.size();
+  P.sync = s->sync;
+  if (s->persistent) {
+    const unsigned need = (unsigned)(P.nphase * n_steps);
+    if ((uint64_t)s->gen + need >= (1u << 31)) {
+      HIP_TRY(hipMemsetAsync(s->sync, 0, sizeof(SyncState), s->stream));
+      s->gen = 0;
+    }
+    P.n_steps = (int)n_steps;
+    P.gen0 = s->gen;
+    HIP_TRY(launch_step_program(P, s->grid, p.smem, s->stream));
+    s->gen += need;
+  } else {
+    P.n_steps = 1;
+    for (int64_t step = 0; step < n_steps; ++step)
+      for (int i = 0; i < P.nphase; ++i)
+        HIP_TRY(launch_phase(p.dev + i, p.phases[i].units, P, (int)step, p.smem, s->stream));
+  }
+  for (auto& q : s->pos_host) q += n_steps;
   return 0;
 }
 
-int stt_steps(const svl_model* m, svl_state* s, int64_t n, const uint32_t* d_audio, uint32_t* d_out) {
-  const svl_config& c = m->cfg;
-  TRY(check_room(s, n));
-  for (int64_t i = 0; i < n; ++i) {
-    EmbedArgs e{};
-    e.text_emb = m->text_emb;
-    e.emb = m->emb;
-    e.tables_bf16 = m->tables_bf16;
-    e.d = c.d_model;
-    e.n_q = c.n_q;
-    e.card = c.card;
-    e.text_card = c.text_card;
-    e.B = s->B;
-    e.text_tok = nullptr;
-    e.fb_tok = s->fb_tok;
-    e.audio = d_audio + (size_t)i * s->B * c.n_q;
-    e.initial_at_zero = 1;
-    e.pos = s->pos;
-    e.x = s->x;
-    HIP_TRY(launch_embed(e, s->stream));
-    TRY(run_layers(m, s));
-    TRY(run_stt_head(m, s, d_out + (size_t)i * s->B));
+// After a synchronization: reports (and clears) a grid barrier that gave up waiting.
+int check_abort(svl_state* s) {
+  if (!s->persistent) return 0;
+  unsigned flag = 0;
+  HIP_TRY(hipMemcpy(&flag, &s->sync->abort_flag[0], sizeof(flag), hipMemcpyDeviceToHost));
+  if (flag) {
+    HIP_TRY(hipMemset(s->sync, 0, sizeof(SyncState)));
+    s->gen = 0;
+    return set_error(SVL_ERR_DEVICE, "a grid barrier of the step kernel timed out; the state is undefined");
   }
   return 0;
 }
@@ -583,16 +732,20 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (batch <= 0) return set_error(SVL_ERR_INVALID_INPUT, "batch must be positive");
   int slots = c.context > 0 ? c.context : capacity;
   if (slots <= 0) return set_error(SVL_ERR_INVALID_INPUT, "an unlimited-context model needs a positive capacity");
-  if (slots > 16000) return set_error(SVL_ERR_INVALID_INPUT, "capacity must be <= 16000");
+  if (slots > 12000) return set_error(SVL_ERR_INVALID_INPUT, "capacity must be <= 12000");
   HIP_TRY(hipSetDevice(m->device));
   svl_state* s = new svl_state();
   s->m = m;
   s->B = batch;
   s->slots = slots;
+  s->grid = step_program_grid(m->device);
+  const char* mode = getenv("SVL_STEP_LAUNCH");
+  s->persistent = !(mode && !strcmp(mode, "phases"));
   auto fail = [&](int rc) {
     delete s;
     return rc;
   };
+  if (s->grid <= 0) return fail(set_error(SVL_ERR_DEVICE, "cannot query the compute unit count"));
   if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
     return fail(set_error(SVL_ERR_DEVICE, "hipStreamCreate failed"));
   const size_t kvb = (size_t)batch * c.num_kv_heads * slots * c.head_dim * (c.kv_dtype == SVL_BF16 ? 2 : 4);
@@ -617,8 +770,12 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.text_card, 1) * 4), s->logits = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.d_model, c.z_dim) * 4), s->z = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * c.num_heads * slots * 4), s->scores = (float*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.latent_dim, 1) * 4), s->in = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;
+  if (!rc) rc = s->alloc(&p, sizeof(SyncState)), s->sync = (SyncState*)p;
+  if (!rc && hipMemsetAsync(s->sync, 0, sizeof(SyncState), s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
+  if (!rc) rc = build_programs(m, s);
   if (rc) return fail(rc);
   s->pos_host.assign(batch, 0);
   if (launch_fill_i32(s->pos, 0, batch, s->stream) != hipSuccess ||
@@ -629,13 +786,15 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   return 0;
 }
 
-int ensure_in(svl_state* s, size_t bytes) {
-  if (s->in_cap >= bytes) return 0;
-  void* p;
-  TRY(s->alloc(&p, bytes));
-  s->in = (float*)p;
-  s->in_cap = bytes;
-  return 0;
+StepParams stt_params(const svl_state* s, const uint32_t* d_audio, const uint32_t* d_text, uint32_t* d_out) {
+  StepParams P{};
+  P.audio = d_audio;
+  P.audio_stride = (size_t)s->B * s->m->cfg.n_q;
+  P.text = d_text;
+  P.text_stride = (size_t)s->B;
+  P.out_tok = d_out;
+  P.out_stride = (size_t)s->B;
+  return P;
 }
 
 }  // namespace
@@ -831,7 +990,7 @@ int svl_state_synchronize(svl_state* s) {
   if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   HIP_TRY(hipSetDevice(s->m->device));
   HIP_TRY(hipStreamSynchronize(s->stream));
-  return 0;
+  return check_abort(s);
 }
 
 void* svl_state_stream(const svl_state* s) { return s ? (void*)s->stream : nullptr; }
@@ -845,22 +1004,31 @@ int svl_transformer_forward(const svl_model* m, svl_state* s, const float* xs, i
   HIP_TRY(hipSetDevice(m->device));
   const int d = m->cfg.d_model;
   const size_t bytes = (size_t)s->B * t * d * 4;
-  TRY(ensure_in(s, 2 * bytes));
-  float* din = s->in;
-  float* dout = s->in + (size_t)s->B * t * d;
-  HIP_TRY(hipMemcpyAsync(din, xs, bytes, hipMemcpyHostToDevice, s->stream));
-  // One position at a time: causal attention makes this the same computation as the
-  // reference's block forward (transformer.rs:139-186).
-  for (int64_t i = 0; i < t; ++i) {
-    HIP_TRY(hipMemcpy2DAsync(s->x, (size_t)d * 4, din + (size_t)i * d, (size_t)t * d * 4, (size_t)d * 4, s->B,
-                             hipMemcpyDeviceToDevice, s->stream));
-    TRY(run_layers(m, s));
-    HIP_TRY(hipMemcpy2DAsync(dout + (size_t)i * d, (size_t)t * d * 4, s->x, (size_t)d * 4, (size_t)d * 4, s->B,
-                             hipMemcpyDeviceToDevice, s->stream));
+  if (s->fwd_cap < 2 * bytes) {
+    void* p;
+    TRY(s->alloc(&p, 2 * bytes));
+    s->fwd = (float*)p;
+    s->fwd_cap = 2 * bytes;
   }
+  float* din = s->fwd;
+  float* dout = s->fwd + (size_t)s->B * t * d;
+  // the copy phases read column `step` of [B][T][d]
+  for (Phase& ph : s->fwd_prog.phases)
+    if (ph.kind == PH_COPY_IN || ph.kind == PH_COPY_OUT) {
+      ph.cp.x_stride = (int)(t * d);
+      ph.cp.y_stride = ph.kind == PH_COPY_IN ? d : (int)(t * d);
+    }
+  HIP_TRY(hipMemcpyAsync(s->fwd_prog.dev, s->fwd_prog.phases.data(), s->fwd_prog.phases.size() * sizeof(Phase),
+                         hipMemcpyHostToDevice, s->stream));
+  HIP_TRY(hipMemcpyAsync(din, xs, bytes, hipMemcpyHostToDevice, s->stream));
+  StepParams P{};
+  P.fwd_in = din;
+  P.fwd_out = dout;
+  P.fwd_T = (int)t;
+  TRY(run_program(s, s->fwd_prog, P, t));
   HIP_TRY(hipMemcpyAsync(ys, dout, bytes, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
-  return 0;
+  return check_abort(s);
 }
 
 int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
@@ -882,29 +1050,18 @@ int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, 
   uint32_t* daudio = s->tok_in + s->B;
   HIP_TRY(hipMemcpyAsync(dtext, text_tokens, (size_t)s->B * 4, hipMemcpyHostToDevice, s->stream));
   HIP_TRY(hipMemcpyAsync(daudio, audio_tokens, (size_t)s->B * c.n_q * 4, hipMemcpyHostToDevice, s->stream));
-  EmbedArgs e{};
-  e.text_emb = m->text_emb;
-  e.emb = m->emb;
-  e.tables_bf16 = m->tables_bf16;
-  e.d = c.d_model;
-  e.n_q = c.n_q;
-  e.card = c.card;
-  e.text_card = c.text_card;
-  e.B = s->B;
-  e.text_tok = dtext;
-  e.fb_tok = s->fb_tok;
-  e.audio = daudio;
-  e.initial_at_zero = 0;
-  e.pos = s->pos;
-  e.x = s->x;
-  HIP_TRY(launch_embed(e, s->stream));
-  TRY(run_layers(m, s));
-  TRY(run_stt_head(m, s, s->tok_out));
+  // LanguageModel::step takes the caller's tokens as they are (no first-step rule).
+  s->stt.phases[0].e.initial_at_zero = 0;
+  HIP_TRY(hipMemcpyAsync(s->stt.dev, s->stt.phases.data(), sizeof(Phase), hipMemcpyHostToDevice, s->stream));
+  int rc = run_program(s, s->stt, stt_params(s, daudio, dtext, s->tok_out), 1);
+  s->stt.phases[0].e.initial_at_zero = 1;
+  HIP_TRY(hipMemcpyAsync(s->stt.dev, s->stt.phases.data(), sizeof(Phase), hipMemcpyHostToDevice, s->stream));
+  if (rc) return rc;
   HIP_TRY(hipMemcpyAsync(out_tokens, s->tok_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
   if (out_logits)
     HIP_TRY(hipMemcpyAsync(out_logits, s->logits, (size_t)s->B * c.text_card * 4, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
-  return 0;
+  return check_abort(s);
 }
 
 int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
@@ -914,8 +1071,10 @@ int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, c
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
   if (m->cfg.kind != SVL_MODEL_STT) return set_error(SVL_ERR_CONFIG, "not an STT model");
   if (n_steps < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative step count");
+  if (n_steps == 0) return 0;
+  TRY(check_room(s, n_steps));
   HIP_TRY(hipSetDevice(m->device));
-  return stt_steps(m, s, n_steps, d_audio_tokens, d_out_tokens);
+  return run_program(s, s->stt, stt_params(s, d_audio_tokens, nullptr, d_out_tokens), n_steps);
 }
 
 int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
@@ -929,6 +1088,7 @@ int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const u
   const size_t na = (size_t)n_steps * s->B * c.n_q;
   for (size_t i = 0; i < na; ++i)
     if (audio_tokens[i] > (uint32_t)c.card) return set_error(SVL_ERR_INVALID_INPUT, "audio token %u out of range", audio_tokens[i]);
+  TRY(check_room(s, n_steps));
   HIP_TRY(hipSetDevice(m->device));
   uint32_t *da, *dout;
   HIP_TRY(hipMalloc(&da, na * 4));
@@ -939,7 +1099,7 @@ int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const u
   }
   int rc = 0;
   e = hipMemcpyAsync(da, audio_tokens, na * 4, hipMemcpyHostToDevice, s->stream);
-  if (e == hipSuccess) rc = stt_steps(m, s, n_steps, da, dout);
+  if (e == hipSuccess) rc = run_program(s, s->stt, stt_params(s, da, nullptr, dout), n_steps);
   if (e == hipSuccess && rc == 0)
     e = hipMemcpyAsync(out_tokens, dout, (size_t)n_steps * s->B * 4, hipMemcpyDeviceToHost, s->stream);
   hipError_t e2 = hipStreamSynchronize(s->stream);
@@ -948,7 +1108,7 @@ int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const u
   if (rc) return rc;
   HIP_TRY(e);
   HIP_TRY(e2);
-  return 0;
+  return check_abort(s);
 }
 
 int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
@@ -959,48 +1119,17 @@ int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent,
   TRY(check_room(s, 1));
   HIP_TRY(hipSetDevice(m->device));
   const int d = c.d_model, ld = c.latent_dim;
-  TRY(ensure_in(s, (size_t)s->B * ld * 4));
-  const float* in;
   if (latent) {
     HIP_TRY(hipMemcpyAsync(s->in, latent, (size_t)s->B * ld * 4, hipMemcpyHostToDevice, s->stream));
-    in = s->in;
   } else {
     for (int b = 0; b < s->B; ++b)
       HIP_TRY(hipMemcpyAsync(s->in + (size_t)b * ld, m->bos, (size_t)ld * 4, hipMemcpyDeviceToDevice, s->stream));
-    in = s->in;
   }
-  GemvArgs g{};
-  g.B = s->B;
-  g.L = m->input_linear;
-  g.x = in;
-  g.x_stride = ld;
-  g.norm = NORM_NONE;
-  g.epi = EPI_STORE;
-  g.y = s->x;
-  g.y_stride = d;
-  HIP_TRY(launch_gemv(g, s->stream));
-  TRY(run_layers(m, s));
+  TRY(run_program(s, s->tts, StepParams{}, 1));
   const int zd = c.z_dim > 0 ? c.z_dim : d;
-  if (c.z_dim > 0) {
-    GemvArgs z{};
-    z.B = s->B;
-    z.L = m->z_proj;
-    z.x = s->x;
-    z.x_stride = d;
-    z.norm = NORM_LAYER;
-    z.nw = m->out_norm_w;
-    z.nb = m->out_norm_b;
-    z.eps = 1e-5f;  // SVL/tts/flow_lm.rs:176
-    z.epi = EPI_STORE;
-    z.y = s->z;
-    z.y_stride = zd;
-    HIP_TRY(launch_gemv(z, s->stream));
-  } else {
-    HIP_TRY(launch_norm(s->x, d, s->z, d, s->B, d, NORM_LAYER, m->out_norm_w, m->out_norm_b, 1e-5f, s->stream));
-  }
   HIP_TRY(hipMemcpyAsync(out_z, s->z, (size_t)s->B * zd * 4, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
-  return 0;
+  return check_abort(s);
 }
 
 }  // extern "C"

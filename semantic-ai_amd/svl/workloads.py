@@ -152,13 +152,18 @@ def tensor_names(s: Shape):
     return out
 
 
-def make_weights(s: Shape, dtype: str, seed: int = 0) -> dict:
+def make_weights(s: Shape, dtype: str, seed: int = 0, threads: int | None = None) -> dict:
     """name -> (dtype code, shape, ndarray) for the oracle and for libsvl.
 
     dtype "f32": everything f32.  "bf16": everything bf16 (stored as bf16 bits).
-    "q8_0"/"q4k": linear weights f32 (quantized by the model), the rest bf16."""
-    tensors = {}
-    for name, shape, role in tensor_names(s):
+    "q8_0"/"q4k": linear weights f32 (quantized by the model), the rest bf16.
+    Tensors are drawn in parallel threads (each has its own generator, so the result does not
+    depend on the thread count)."""
+    from concurrent.futures import ThreadPoolExecutor
+    import os
+
+    def one(item):
+        name, shape, role = item
         if role == "norm_w":
             x = normal(seed, name, shape, 0.02, 1.0)
         elif role == "vec":
@@ -166,10 +171,13 @@ def make_weights(s: Shape, dtype: str, seed: int = 0) -> dict:
         else:
             x = normal(seed, name, shape, 0.02)
         if dtype == "f32" or (dtype in ("q8_0", "q4k") and role in ("linear", "dense_linear")):
-            tensors[name] = (F32, shape, x)
-        else:
-            tensors[name] = (BF16, shape, to_bf16_bits(x))
-    return tensors
+            return name, (F32, shape, x)
+        return name, (BF16, shape, to_bf16_bits(x))
+
+    items = tensor_names(s)
+    n = threads or min(16, os.cpu_count() or 4)
+    with ThreadPoolExecutor(n) as ex:
+        return dict(ex.map(one, items))
 
 
 def quantize_code(dtype: str) -> int:
@@ -215,28 +223,3 @@ def linear_bytes(s: Shape, dtype: str) -> int:
         else:
             total += n * 4
     return total
-
-
-def make_weights_fast(s: Shape, dtype: str, seed: int = 0, device: str = "cuda") -> dict:
-    """Same layout and distributions as ``make_weights``, drawn with torch's generator on
-    `device` (seconds instead of minutes for the 1B-parameter shapes).  The values differ from
-    ``make_weights``'s but are reproducible for a given seed, device type and torch version;
-    they come back as host numpy arrays so both the GPU library and the oracle read the same
-    bytes."""
-    import torch
-
-    tensors = {}
-    for name, shape, role in tensor_names(s):
-        g = torch.Generator(device=device)
-        g.manual_seed((seed << 32) ^ zlib.crc32(name.encode()))
-        x = torch.randn(int(np.prod(shape)), generator=g, device=device, dtype=torch.float32)
-        x.mul_(0.02)
-        if role == "norm_w" or (role == "vec" and "layer_scale" in name):
-            x.add_(1.0)
-        if dtype == "f32" or (dtype in ("q8_0", "q4k") and role in ("linear", "dense_linear")):
-            tensors[name] = (F32, shape, x.cpu().numpy().reshape(shape))
-        else:
-            bits = x.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
-            tensors[name] = (BF16, shape, bits.reshape(shape))
-        del x
-    return tensors

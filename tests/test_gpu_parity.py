@@ -27,8 +27,8 @@ F32_TOL = 1e-4
 LOWP_TOL = 2e-2
 
 
-def build(shape, dtype, seed=0, fast=False, kv_dtype=svl.F32):
-    t = (W.make_weights_fast if fast else W.make_weights)(shape, dtype, seed=seed)
+def build(shape, dtype, seed=0, kv_dtype=svl.F32):
+    t = W.make_weights(shape, dtype, seed=seed)
     q = W.quantize_code(dtype)
     return t, svl.Model(shape.config(q), t, kv_dtype=kv_dtype), oracle.Model(shape.config(q), t)
 
@@ -206,7 +206,7 @@ def test_input_errors():
 @pytest.fixture(scope="module")
 def s1_q8():
     oracle.set_threads(min(16, os.cpu_count() or 4))
-    t, g, o = build(W.S1, "q8_0", seed=0, fast=True)
+    t, g, o = build(W.S1, "q8_0", seed=0)
     del t
     return g, o
 
@@ -235,7 +235,7 @@ def test_s1_q8_0_logits_within_bar(s1_q8):
 def test_t1_f32_prefilled_256_within_f32_bar():
     """Pocket-TTS shape, f32, 256 prefilled positions, 16 steps: z within 1e-4."""
     s = W.T1
-    t, g, o = build(s, "f32", seed=0, fast=True)
+    t, g, o = build(s, "f32", seed=0)
     ks, vs = W.prefill_caches(s, 256, seed=3)
     gs = g.state_from_layer_caches(ks, vs, capacity=512)
     os_ = o.state_from_layer_caches(ks, vs)
@@ -244,3 +244,16 @@ def test_t1_f32_prefilled_256_within_f32_bar():
         z = g.backbone_step(lat[i][None], gs)[0]
         zo = os_.tts_step(lat[i])
         assert np.array_equal(z, zo), (i, float(np.max(np.abs(z - zo))))
+
+
+def test_persistent_and_per_phase_launches_agree(monkeypatch):
+    """The persistent step kernel and one launch per phase run the same units: same bits."""
+    s = W.S1_SMALL
+    t = W.make_weights(s, "q8_0", seed=19)
+    g = svl.Model(s.config(W.Q8_0), t)
+    audio = W.audio_tokens(s, 30, seed=20)[0][:, None, :]
+    a = g.recognize(audio, g.init_state())
+    monkeypatch.setenv("SVL_STEP_LAUNCH", "phases")
+    st = g.init_state()
+    b = g.recognize(audio, st)
+    assert np.array_equal(a, b)
