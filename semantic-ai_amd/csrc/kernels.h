@@ -132,6 +132,8 @@ struct StepParams {
   const Phase* prog;
   int nphase;
   int n_steps;
+  int* pos;                      // [B] stream positions (cached per step in LDS)
+  int B;
   SyncState* sync;
   unsigned gen0;                 // barriers completed by earlier launches on this state
   const uint32_t* audio;         // step s: audio + s * audio_stride
@@ -146,6 +148,7 @@ struct StepParams {
 };
 
 constexpr int kStepThreads = 256;
+constexpr int kMaxBatch = 1024;
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s);
 hipError_t launch_phase(const Phase* d_ph, int units, const StepParams& p, int step, size_t smem, hipStream_t s);

@@ -54,15 +54,24 @@ __device__ __forceinline__ bool grid_barrier(SyncState* s, unsigned gen) {
   return s_ok != 0;
 }
 
+// Positions of the streams at the start of the step, cached in LDS (the last layer advances
+// them; no later phase of the step reads them).
+__device__ __forceinline__ void load_positions(const StepParams& P, int* spos) {
+  for (int b = threadIdx.x; b < P.B; b += kStepThreads) spos[b] = ld_co(P.pos + b);
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int spos[kMaxBatch];
   unsigned gen = P.gen0;
   for (int step = 0; step < P.n_steps; ++step) {
+    load_positions(P, spos);
     for (int p = 0; p < P.nphase; ++p) {
       const Phase& ph = P.prog[p];
       for (int u = blockIdx.x; u < ph.units; u += gridDim.x) {
         __syncthreads();
-        run_unit(ph, P, step, u, smem);
+        if (!run_unit(ph, P, step, u, spos, smem)) break;
       }
       if (!grid_barrier(P.sync, ++gen)) return;
     }
@@ -71,7 +80,9 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
 
 __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* ph, StepParams P, int step) {
   extern __shared__ __align__(16) unsigned char smem[];
-  run_unit(*ph, P, step, blockIdx.x, smem);
+  __shared__ int spos[kMaxBatch];
+  load_positions(P, spos);
+  run_unit(*ph, P, step, blockIdx.x, spos, smem);
 }
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s) {
@@ -129,13 +140,13 @@ size_t phase_smem(const Phase& ph) {
       const GemvArgs& g = ph.g;
       const int K = g.L.in;
       if (g.L.fmt == FMT_Q8_0) {
-        const int nb = K / 32;
-        return (size_t)K * 4 + K + (size_t)nb * 4 + (size_t)2 * g.ipw * (nb + 1) * 4 + (size_t)2 * g.ipw * 4 + 64;
+        const int nb = K / 32, nb4 = (nb + 3) & ~3, ts = nb4 + 4;
+        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
       return (size_t)K * 4 + 16 * 4 + 64;
     }
     case PH_ATTN_SOFTMAX_V:
-      return (size_t)(ph.at.cap + 1) * 4 + 64;
+      return (size_t)(((ph.at.cap + 3) & ~3) + 4) * 4 + 64;
     case PH_ARGMAX:
       return 32 * 4 + 64;
     case PH_NORM:

@@ -82,7 +82,19 @@ __device__ __forceinline__ void stage_row(const float* x, int n, float* xs) {
 __device__ __forceinline__ float blocked_sum(const float* xs, int K, bool squares) {
   const int lane = threadIdx.x % kWave;
   float acc = 0.0f;
-  for (int i = lane; i < K; i += kWave) {
+  int i = lane;
+  for (; i + 7 * kWave < K; i += 8 * kWave) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = xs[i + u * kWave];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      float t = v[u];
+      if (squares) t = t * t;
+      acc = acc + t;
+    }
+  }
+  for (; i < K; i += kWave) {
     float v = xs[i];
     if (squares) v = v * v;
     acc = acc + v;
@@ -138,9 +150,63 @@ __device__ void quantize_lds(const float* xs, int K, int8_t* xq, float* xdq) {
   __syncthreads();
 }
 
-// ---- GEMV epilogues ---------------------------------------------------------------------------
+// acc = 0; acc += t[i] for i = 0 .. n-1 in order, reading t (16-byte aligned, in LDS) 16 values
+// ahead of the additions.
+__device__ __forceinline__ float ordered_sum(const float* t, int n) {
+  typedef float v4f_t __attribute__((ext_vector_type(4)));
+  const v4f_t* t4 = (const v4f_t*)t;
+  const int n16 = n / 16;
+  float acc = 0.0f;
+  v4f_t cur[4], nxt[4];
+  if (n16 > 0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cur[u] = t4[u];
+  }
+  for (int c = 0; c < n16; ++c) {
+    if (c + 1 < n16) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) nxt[u] = t4[(c + 1) * 4 + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc = acc + cur[u].x;
+      acc = acc + cur[u].y;
+      acc = acc + cur[u].z;
+      acc = acc + cur[u].w;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+  }
+  for (int i = n16 * 16; i < n; ++i) acc = acc + t[i];
+  return acc;
+}
 
-__device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row, float y, float yp, float yv) {
+// ---- GEMV epilogues ---------------------------------------------------------------------------
+// Inputs of an item's epilogue that live in global memory (RoPE cos/sin, the old residual) are
+// loaded when the unit starts, so they arrive with the weights.
+
+struct EpiIn {
+  float a = 0.0f, b = 0.0f;  // QKV_ROPE: cos, sin; RESID: old residual
+};
+
+__device__ __forceinline__ EpiIn gemv_epi_prefetch(const GemvArgs& a, int b, int row, int p) {
+  EpiIn e;
+  if (a.epi == EPI_QKV_ROPE) {
+    const int qdim = a.H * a.hd, kvdim = a.KVH * a.hd;
+    if (row < qdim + kvdim) {
+      const int rr = row < qdim ? row : row - qdim;
+      const float* cs = a.rope + ((size_t)p * (a.hd / 2) + (rr % a.hd) / 2) * 2;
+      e.a = cs[0];
+      e.b = cs[1];
+    }
+  } else if (a.epi == EPI_RESID) {
+    e.a = ld_co(a.resid + (size_t)b * a.resid_stride + row);
+  }
+  return e;
+}
+
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row, int p, const EpiIn& in, float y,
+                                              float yp, float yv) {
   switch (a.epi) {
     case EPI_STORE:
       st_co(a.y + (size_t)b * a.y_stride + row, y);
@@ -157,22 +223,19 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row,
     case EPI_RESID: {
       float u = y;
       if (a.lscale) u = u * a.lscale[row];
-      float* r = a.resid + (size_t)b * a.resid_stride + row;
-      st_co(r, ld_co(r) + u);
+      st_co(a.resid + (size_t)b * a.resid_stride + row, in.a + u);
       break;
     }
     case EPI_QKV_ROPE: {
       // split q | k | v (transformer.rs:330-338); interleaved RoPE of q and k (rope_i); k and v
       // into the ring slot of the current position.
       const int qdim = a.H * a.hd, kvdim = a.KVH * a.hd;
-      const int p = ld_co(a.pos + b);
       const int region = row < qdim ? 0 : (row < qdim + kvdim ? 1 : 2);
       const int rr = region == 0 ? row : (region == 1 ? row - qdim : row - qdim - kvdim);
       const int head = rr / a.hd, dim = rr % a.hd;
       float out = y;
       if (region < 2) {
-        const float* cs = a.rope + ((size_t)p * (a.hd / 2) + dim / 2) * 2;
-        const float c = cs[0], s = cs[1];
+        const float c = in.a, s = in.b;
         if ((dim & 1) == 0) {
           float t0 = y * c, t1 = yp * s;
           out = t0 - t1;
@@ -199,20 +262,24 @@ __device__ __forceinline__ int gemv_phys_row(const GemvArgs& a, int i0, int ni, 
   return i0 + r;
 }
 
-__device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, int i0, int ni, const float* Y) {
+__device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, int i0, int ni, int p, const EpiIn& in,
+                                            const float* Y) {
   const int t = threadIdx.x;
   if (t < ni) {
     const float y = Y[t];
     const float yp = a.epi == EPI_QKV_ROPE ? Y[t ^ 1] : 0.0f;
     const float yv = a.epi == EPI_SILU_GATE ? Y[ni + t] : 0.0f;
-    gemv_epilogue(a, b, i0 + t, y, yp, yv);
+    gemv_epilogue(a, b, i0 + t, p, in, y, yp, yv);
   }
-  if (a.advance_pos && part == 0 && t == 0) st_co(a.pos + b, ld_co(a.pos + b) + 1);
+  if (a.advance_pos && part == 0 && t == 0) st_co(a.pos + b, p + 1);
 }
 
 __device__ __forceinline__ int gemv_items(const GemvArgs& a) {
   return a.epi == EPI_SILU_GATE ? a.ff_hidden : a.L.out;
 }
+
+// Row stride of the per-block terms in LDS: 16-byte aligned, padded.
+__device__ __forceinline__ int term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
 
 // ---- Q8_0 GEMV unit ---------------------------------------------------------------------------
 // Candle's quantized CPU matmul (SVL/nn/mod.rs:97; BlockQ8_0::vec_dot_unopt): terms
@@ -223,7 +290,7 @@ __device__ __forceinline__ int gemv_items(const GemvArgs& a) {
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 template <int MAXB>
-__device__ void gemv_q8_unit(const GemvArgs& a, int unit, unsigned char* smem) {
+__device__ void gemv_q8_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
   const int K = a.L.in, nb = K / 32;
   const int b = unit / a.parts, part = unit % a.parts;
   const bool silu = a.epi == EPI_SILU_GATE;
@@ -231,13 +298,16 @@ __device__ void gemv_q8_unit(const GemvArgs& a, int unit, unsigned char* smem) {
   const int ni = min(a.ipw, gemv_items(a) - i0);
   const int NR = silu ? 2 * ni : ni;
   const int total = NR * nb;
-  const int ts = nb + 1;
+  const int ts = term_stride(nb);
+  const int p = spos[b];
   float* xs = (float*)smem;             // K
   int8_t* xq = (int8_t*)(xs + K);       // K
-  float* xdq = (float*)(xq + K);        // nb
-  float* T = xdq + nb;                  // 2 * ipw * ts
+  float* xdq = (float*)(xq + K);        // nb (+ pad to 16 bytes)
+  float* T = xdq + ((nb + 3) & ~3);     // 2 * ipw * ts
   float* Y = T + 2 * a.ipw * ts;        // 2 * ipw
 
+  EpiIn in;
+  if ((int)threadIdx.x < ni) in = gemv_epi_prefetch(a, b, i0 + threadIdx.x, p);
   const int8_t* wq = (const int8_t*)a.L.w;
   v4i wa[MAXB], wb[MAXB];
   uint16_t wd[MAXB];
@@ -247,13 +317,12 @@ __device__ void gemv_q8_unit(const GemvArgs& a, int unit, unsigned char* smem) {
     if (idx < total) {
       const int r = idx / nb, blk = idx - r * nb;
       const size_t row = (size_t)gemv_phys_row(a, i0, ni, r);
-      const v4i* p = (const v4i*)(wq + row * K + (size_t)blk * 32);
-      wa[k] = __builtin_nontemporal_load(p);
-      wb[k] = __builtin_nontemporal_load(p + 1);
+      const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
+      wa[k] = __builtin_nontemporal_load(wp);
+      wb[k] = __builtin_nontemporal_load(wp + 1);
       wd[k] = a.L.scale[row * nb + blk];
     }
   }
-  __syncthreads();
   stage_row(a.x + (size_t)b * a.x_stride, K, xs);
   if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
   else __syncthreads();
@@ -278,14 +347,9 @@ __device__ void gemv_q8_unit(const GemvArgs& a, int unit, unsigned char* smem) {
     }
   }
   __syncthreads();
-  if (threadIdx.x < NR) {
-    const float* tr = T + threadIdx.x * ts;
-    float acc = 0.0f;
-    for (int blk = 0; blk < nb; ++blk) acc = acc + tr[blk];
-    Y[threadIdx.x] = acc;
-  }
+  if ((int)threadIdx.x < NR) Y[threadIdx.x] = ordered_sum(T + threadIdx.x * ts, nb);
   __syncthreads();
-  gemv_finish(a, b, part, i0, ni, Y);
+  gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
 // ---- dense GEMV unit ----------------------------------------------------------------------------
@@ -295,16 +359,18 @@ __device__ void gemv_q8_unit(const GemvArgs& a, int unit, unsigned char* smem) {
 // (8 gate/value pairs for the SiLU gate).
 
 template <bool BF16W>
-__device__ void gemv_dense_unit(const GemvArgs& a, int unit, unsigned char* smem) {
+__device__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
   const int K = a.L.in;
   const int b = unit / a.parts, part = unit % a.parts;
   const bool silu = a.epi == EPI_SILU_GATE;
   const int i0 = part * a.ipw;
   const int ni = min(a.ipw, gemv_items(a) - i0);
   const int NR = silu ? 2 * ni : ni;
+  const int p = spos[b];
   float* xs = (float*)smem;   // K
   float* Y = xs + K;          // 16
-  __syncthreads();
+  EpiIn in;
+  if ((int)threadIdx.x < ni) in = gemv_epi_prefetch(a, b, i0 + threadIdx.x, p);
   stage_row(a.x + (size_t)b * a.x_stride, K, xs);
   if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
   else __syncthreads();
@@ -316,22 +382,22 @@ __device__ void gemv_dense_unit(const GemvArgs& a, int unit, unsigned char* smem
     int c = 0;
     if (BF16W) {
       const uint16_t* w = (const uint16_t*)a.L.w + row * K + li;
-      for (; c + 8 <= chunks; c += 8) {
-        uint16_t wv[8];
+      for (; c + 16 <= chunks; c += 16) {
+        uint16_t wv[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+        for (int u = 0; u < 16; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = fmaf(xs[(c + u) * 16 + li], bf16_to_f32(wv[u]), acc);
+        for (int u = 0; u < 16; ++u) acc = fmaf(xs[(c + u) * 16 + li], bf16_to_f32(wv[u]), acc);
       }
       for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], bf16_to_f32(w[(size_t)c * 16]), acc);
     } else {
       const float* w = (const float*)a.L.w + row * K + li;
-      for (; c + 8 <= chunks; c += 8) {
-        float wv[8];
+      for (; c + 16 <= chunks; c += 16) {
+        float wv[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+        for (int u = 0; u < 16; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = fmaf(xs[(c + u) * 16 + li], wv[u], acc);
+        for (int u = 0; u < 16; ++u) acc = fmaf(xs[(c + u) * 16 + li], wv[u], acc);
       }
       for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], w[(size_t)c * 16], acc);
     }
@@ -342,29 +408,29 @@ __device__ void gemv_dense_unit(const GemvArgs& a, int unit, unsigned char* smem
       float tail = 0.0f;
       for (int i = chunks * 16; i < K; ++i) {
         const float wv = BF16W ? bf16_to_f32(((const uint16_t*)a.L.w)[row * K + i]) : ((const float*)a.L.w)[row * K + i];
-        float p = xs[i] * wv;
-        tail = tail + p;
+        float pr = xs[i] * wv;
+        tail = tail + pr;
       }
       Y[g] = acc + tail;
     }
   }
   __syncthreads();
-  gemv_finish(a, b, part, i0, ni, Y);
+  gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
-__device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, unsigned char* smem) {
+__device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
   if (a.L.fmt == FMT_Q8_0) {
     switch (a.maxb) {
-      case 1: gemv_q8_unit<1>(a, unit, smem); break;
-      case 2: gemv_q8_unit<2>(a, unit, smem); break;
-      case 4: gemv_q8_unit<4>(a, unit, smem); break;
-      case 8: gemv_q8_unit<8>(a, unit, smem); break;
-      default: gemv_q8_unit<16>(a, unit, smem); break;
+      case 1: gemv_q8_unit<1>(a, unit, spos, smem); break;
+      case 2: gemv_q8_unit<2>(a, unit, spos, smem); break;
+      case 4: gemv_q8_unit<4>(a, unit, spos, smem); break;
+      case 8: gemv_q8_unit<8>(a, unit, spos, smem); break;
+      default: gemv_q8_unit<16>(a, unit, spos, smem); break;
     }
   } else if (a.L.fmt == FMT_BF16) {
-    gemv_dense_unit<true>(a, unit, smem);
+    gemv_dense_unit<true>(a, unit, spos, smem);
   } else {
-    gemv_dense_unit<false>(a, unit, smem);
+    gemv_dense_unit<false>(a, unit, spos, smem);
   }
 }
 
@@ -372,23 +438,32 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, unsigned 
 // The query at position p attends to keys max(0, p - window + 1) ..= p (transformer.rs:385) in
 // the ring, in the reference's order (attention.rs:139-168):
 //   scores:    w_j = scale * dot(q, k_j) with the 16-lane dot; 16 keys per unit, one per
-//              16-thread group.  Units: B x H x ceil(cap / 16), the ones past a stream's keys idle.
+//              16-thread group.  Units are chunk-major (chunk = unit / (B * H)), so once a
+//              chunk is past every stream's keys the workgroup has no more work in the phase.
 //   softmax_v: max, e_j = exp(w_j - max), sum of e_j in key order, then
 //              out = sum over keys in order of mul_add(e_j / sum, v_j, out).  One unit per
 //              (stream, head); wave w produces dims [32w, 32w + 32).
 
 constexpr int kKeysPerUnit = 16;
 
+__device__ __forceinline__ int visible_keys(const AttnArgs& a, int p) {
+  return a.window > 0 ? min(p + 1, a.window) : p + 1;
+}
+
+// Returns false when no later unit of this phase has keys to score.
 template <int HD, bool BF16KV>
-__device__ void attn_scores_unit(const AttnArgs& a, int unit) {
-  const int chunks = (a.cap + kKeysPerUnit - 1) / kKeysPerUnit;
-  const int chunk = unit % chunks;
-  const int h = (unit / chunks) % a.H;
-  const int b = unit / (chunks * a.H);
-  const int p = ld_co(a.pos + b);
-  const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
+__device__ bool attn_scores_unit(const AttnArgs& a, int unit, const int* spos) {
+  const int chunk = unit / (a.B * a.H);
+  const int bh = unit % (a.B * a.H);
+  const int b = bh / a.H, h = bh % a.H;
+  const int p = spos[b];
+  const int L = visible_keys(a, p);
+  if (chunk * kKeysPerUnit >= L) {
+    int lmax = 0;
+    for (int i = 0; i < a.B; ++i) lmax = max(lmax, visible_keys(a, spos[i]));
+    return chunk * kKeysPerUnit < lmax;
+  }
   const int jj = chunk * kKeysPerUnit + threadIdx.x / 16;
-  if (chunk * kKeysPerUnit >= L) return;
   const int li = threadIdx.x % 16;
   constexpr int C = HD / 16;
   const int kvh = h / (a.H / a.KVH);
@@ -408,18 +483,18 @@ __device__ void attn_scores_unit(const AttnArgs& a, int unit) {
 #pragma unroll
   for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
   if (live && li == 0) st_co(a.scores + ((size_t)b * a.H + h) * a.cap + jj, a.scale * (acc + 0.0f));
+  return true;
 }
 
 template <int HD, bool BF16KV>
-__device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, unsigned char* smem) {
-  float* w = (float*)smem;           // L weights
-  float* sum_slot = w + a.cap;       // 1
+__device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem) {
+  float* w = (float*)smem;                     // L weights (16-byte aligned)
+  float* sum_slot = w + ((a.cap + 3) & ~3);    // 1
   const int h = unit % a.H, b = unit / a.H;
-  const int p = ld_co(a.pos + b);
-  const int L = a.window > 0 ? min(p + 1, a.window) : p + 1;
+  const int p = spos[b];
+  const int L = visible_keys(a, p);
   const int first = p + 1 - L;
   const float* sc = a.scores + ((size_t)b * a.H + h) * a.cap;
-  __syncthreads();
   for (int j0 = 0; j0 < L; j0 += 8 * kStepThreads) {
     float v[8];
 #pragma unroll
@@ -440,11 +515,9 @@ __device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, unsigned char* 
     for (int j = lane; j < L; j += kWave) mx = fmaxf(mx, w[j]);
     mx = wave_max(mx);
     for (int j = lane; j < L; j += kWave) w[j] = ref_exp(w[j] - mx);
-    if (lane == 0) {
-      float sum = 0.0f;
-      for (int j = 0; j < L; ++j) sum = sum + w[j];
-      sum_slot[0] = sum;
-    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done before lane 0 reads them
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) sum_slot[0] = ordered_sum(w, L);
   }
   __syncthreads();
   const float sum = sum_slot[0];
@@ -454,37 +527,44 @@ __device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, unsigned char* 
     const int d = wave * 32 + lane;
     const int kvh = h / (a.H / a.KVH);
     const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
+    constexpr int CH = 32;
     float acc = 0.0f;
-    int j = 0;
-    for (; j + 16 <= L; j += 16) {
-      float vv[16];
+    float cur[CH], nxt[CH];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) vv[u] = kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + j + u) % a.cap)) * HD + d);
+    for (int u = 0; u < CH; ++u)
+      cur[u] = u < L ? kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + u) % a.cap)) * HD + d) : 0.0f;
+    for (int j = 0; j < L; j += CH) {
 #pragma unroll
-      for (int u = 0; u < 16; ++u) acc = fmaf(w[j + u], vv[u], acc);
+      for (int u = 0; u < CH; ++u) {
+        const int jn = j + CH + u;
+        nxt[u] = jn < L ? kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + jn) % a.cap)) * HD + d) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        if (j + u < L) acc = fmaf(w[j + u], cur[u], acc);
+#pragma unroll
+      for (int u = 0; u < CH; ++u) cur[u] = nxt[u];
     }
-    for (; j < L; ++j) acc = fmaf(w[j], kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + j) % a.cap)) * HD + d), acc);
     st_co(a.out + (size_t)b * a.H * HD + (size_t)h * HD + d, acc);
   }
 }
 
-__device__ __forceinline__ void attn_scores_dispatch(const AttnArgs& a, int unit) {
+__device__ __forceinline__ bool attn_scores_dispatch(const AttnArgs& a, int unit, const int* spos) {
   if (a.hd == 128) {
-    if (a.kv_bf16) attn_scores_unit<128, true>(a, unit);
-    else attn_scores_unit<128, false>(a, unit);
-  } else {
-    if (a.kv_bf16) attn_scores_unit<64, true>(a, unit);
-    else attn_scores_unit<64, false>(a, unit);
+    if (a.kv_bf16) return attn_scores_unit<128, true>(a, unit, spos);
+    return attn_scores_unit<128, false>(a, unit, spos);
   }
+  if (a.kv_bf16) return attn_scores_unit<64, true>(a, unit, spos);
+  return attn_scores_unit<64, false>(a, unit, spos);
 }
 
-__device__ __forceinline__ void attn_softmax_v_dispatch(const AttnArgs& a, int unit, unsigned char* smem) {
+__device__ __forceinline__ void attn_softmax_v_dispatch(const AttnArgs& a, int unit, const int* spos, unsigned char* smem) {
   if (a.hd == 128) {
-    if (a.kv_bf16) attn_softmax_v_unit<128, true>(a, unit, smem);
-    else attn_softmax_v_unit<128, false>(a, unit, smem);
+    if (a.kv_bf16) attn_softmax_v_unit<128, true>(a, unit, spos, smem);
+    else attn_softmax_v_unit<128, false>(a, unit, spos, smem);
   } else {
-    if (a.kv_bf16) attn_softmax_v_unit<64, true>(a, unit, smem);
-    else attn_softmax_v_unit<64, false>(a, unit, smem);
+    if (a.kv_bf16) attn_softmax_v_unit<64, true>(a, unit, spos, smem);
+    else attn_softmax_v_unit<64, false>(a, unit, spos, smem);
   }
 }
 
@@ -492,33 +572,34 @@ __device__ __forceinline__ void attn_softmax_v_dispatch(const AttnArgs& a, int u
 
 // SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
 // ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 256.
-__device__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit) {
+__device__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit, const int* spos) {
   const int chunks = (a.d + kStepThreads - 1) / kStepThreads;
   const int b = unit / chunks;
   const int i = (unit % chunks) * kStepThreads + threadIdx.x;
   if (i >= a.d) return;
+  const bool initial = a.initial_at_zero && spos[b] == 0;
+  const uint32_t* au = audio + (size_t)b * a.n_q;
   uint32_t t = text ? text[b] : ld_co(a.fb_tok + b);
   t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
-  const bool initial = a.initial_at_zero && ld_co(a.pos + b) == 0;
   const size_t rows = (size_t)a.card + 1;
-  const uint32_t* au = audio + (size_t)b * a.n_q;
   float x = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.text_emb)[(size_t)t * a.d + i])
                           : ((const float*)a.text_emb)[(size_t)t * a.d + i];
-  for (int c0 = 0; c0 < a.n_q; c0 += 8) {
-    float e[8];
+  constexpr int G = 32;  // codebooks per round: tokens, then rows, then the adds in order
+  for (int c0 = 0; c0 < a.n_q; c0 += G) {
+    uint32_t tok[G];
+    float e[G];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int c = c0 + u;
-      e[u] = 0.0f;
-      if (c < a.n_q) {
-        uint32_t tok = initial ? (uint32_t)a.card : au[c];
-        tok = tok > (uint32_t)a.card ? (uint32_t)a.card : tok;
-        const size_t idx = ((size_t)c * rows + tok) * a.d + i;
+    for (int u = 0; u < G; ++u) tok[u] = c0 + u < a.n_q ? (initial ? (uint32_t)a.card : au[c0 + u]) : 0u;
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      if (c0 + u < a.n_q) {
+        const uint32_t tk = tok[u] > (uint32_t)a.card ? (uint32_t)a.card : tok[u];
+        const size_t idx = ((size_t)(c0 + u) * rows + tk) * a.d + i;
         e[u] = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.emb)[idx]) : ((const float*)a.emb)[idx];
       }
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < G; ++u)
       if (c0 + u < a.n_q) x = x + e[u];
   }
   st_co(a.x + (size_t)b * a.d + i, x);
@@ -532,15 +613,16 @@ __device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsign
   const float* lg = a.logits + (size_t)b * a.V;
   float best = -__builtin_huge_valf();
   int idx = 0x7fffffff;
-  for (int i0 = 0; i0 < a.V; i0 += 8 * kStepThreads) {
-    float v[8];
+  constexpr int R = 32;
+  for (int i0 = 0; i0 < a.V; i0 += R * kStepThreads) {
+    float v[R];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < R; ++u) {
       const int i = i0 + threadIdx.x + u * kStepThreads;
       if (i < a.V) v[u] = ld_co(lg + i);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < R; ++u) {
       const int i = i0 + threadIdx.x + u * kStepThreads;
       if (i < a.V && (idx == 0x7fffffff || v[u] > best)) {
         best = v[u];
@@ -557,7 +639,6 @@ __device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsign
       idx = oi;
     }
   }
-  __syncthreads();
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (lane == 0) {
     sv[wave] = best;
@@ -582,7 +663,6 @@ __device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsign
 // y[b] = norm(x[b]); unit = stream.
 __device__ void norm_unit(const NormArgs& a, int unit, unsigned char* smem) {
   float* xs = (float*)smem;
-  __syncthreads();
   stage_row(a.x + (size_t)unit * a.x_stride, a.d, xs);
   norm_lds(xs, a.d, a.norm, a.w, a.b, a.eps);
   for (int i = threadIdx.x; i < a.d; i += kStepThreads) st_co(a.y + (size_t)unit * a.y_stride + i, xs[i]);
@@ -596,22 +676,24 @@ __device__ void copy_unit(const float* x, int x_stride, float* y, int y_stride, 
   if (i < n) st_co(y + (size_t)b * y_stride + i, ld_co(x + (size_t)b * x_stride + i));
 }
 
-// Runs work unit `unit` of phase `ph` for step `step` of a launch.
-__device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, unsigned char* smem) {
+// Runs work unit `unit` of phase `ph` for step `step` of a launch; `spos` holds the streams'
+// positions at the start of the step.  Returns false when the workgroup has no later unit in
+// this phase.
+__device__ __forceinline__ bool run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
+                                         unsigned char* smem) {
   switch (ph.kind) {
     case PH_EMBED: {
       const uint32_t* text = P.text ? P.text + (size_t)step * P.text_stride : nullptr;
-      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit);
+      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit, spos);
       break;
     }
     case PH_GEMV:
-      gemv_unit(ph.g, unit, smem);
+      gemv_unit(ph.g, unit, spos, smem);
       break;
     case PH_ATTN_SCORES:
-      attn_scores_dispatch(ph.at, unit);
-      break;
+      return attn_scores_dispatch(ph.at, unit, spos);
     case PH_ATTN_SOFTMAX_V:
-      attn_softmax_v_dispatch(ph.at, unit, smem);
+      attn_softmax_v_dispatch(ph.at, unit, spos, smem);
       break;
     case PH_ARGMAX:
       argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem);
@@ -626,6 +708,7 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       copy_unit(ph.cp.x, ph.cp.x_stride, P.fwd_out + (size_t)step * ph.cp.n, ph.cp.y_stride, ph.cp.n, unit);
       break;
   }
+  return true;
 }
 
 }  // namespace svl

@@ -340,6 +340,7 @@ int check_config(const svl_config* c) {
   if (c->kv_dtype != SVL_F32 && c->kv_dtype != SVL_BF16) return set_error(SVL_ERR_CONFIG, "kv_dtype must be F32 or BF16");
   if (c->kind == SVL_MODEL_STT && (c->n_q <= 0 || c->card <= 0 || c->text_card <= 0))
     return set_error(SVL_ERR_CONFIG, "invalid STT heads");
+  if (c->kind == SVL_MODEL_STT && c->n_q > 64) return set_error(SVL_ERR_CONFIG, "n_q must be <= 64");
   if (c->kind == SVL_MODEL_TTS && c->latent_dim <= 0) return set_error(SVL_ERR_CONFIG, "invalid TTS latent_dim");
   if (c->kind == SVL_MODEL_TTS && c->latent_dim % 4) return set_error(SVL_ERR_CONFIG, "latent_dim must be a multiple of 4");
   return 0;
@@ -694,6 +695,8 @@ int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
   P.prog = p.dev;
   P.nphase = (int)p.phases.size();
   P.sync = s->sync;
+  P.pos = s->pos;
+  P.B = s->B;
   if (s->persistent) {
     const unsigned need = (unsigned)(P.nphase * n_steps);
     if ((uint64_t)s->gen + need >= (1u << 31)) {
@@ -729,7 +732,7 @@ int check_abort(svl_state* s) {
 
 int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** out) {
   const svl_config& c = m->cfg;
-  if (batch <= 0) return set_error(SVL_ERR_INVALID_INPUT, "batch must be positive");
+  if (batch <= 0 || batch > kMaxBatch) return set_error(SVL_ERR_INVALID_INPUT, "batch must be in [1, %d]", kMaxBatch);
   int slots = c.context > 0 ? c.context : capacity;
   if (slots <= 0) return set_error(SVL_ERR_INVALID_INPUT, "an unlimited-context model needs a positive capacity");
   if (slots > 12000) return set_error(SVL_ERR_INVALID_INPUT, "capacity must be <= 12000");
