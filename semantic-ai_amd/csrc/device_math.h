@@ -112,16 +112,46 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
   return v;
 }
-// Sum over the 32-lane half of the wave that the calling lane belongs to.
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+// Lane moves inside a wave.  DPP controls: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] =
+// 0x4E, row_half_mirror (lane i of 8 <- 7 - i) = 0x141, row_mirror (lane i of 16 <- 15 - i) =
+// 0x140.  ds_swizzle bitmask mode (offset bit 15 clear): source lane within the 32-lane group =
+// ((lane & and) | or) ^ xor, with and = offset[4:0], or = offset[9:5], xor = offset[14:10].
+template <int OFFSET>
+__device__ __forceinline__ float swizzle(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), OFFSET));
+}
+
+// Maximum over the 32-lane half of the wave that the calling lane belongs to, in every lane, of
+// non-negative floats given by their bit patterns (whose unsigned order is the float order).
+__device__ __forceinline__ uint32_t half_max_bits(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));  // lane ^ 16
   return v;
 }
-__device__ __forceinline__ float half_max(float v) {
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+
+// x of lane u (u < 8, known after unrolling) of the calling lane's 32-lane half.
+__device__ __forceinline__ float half_lane(float x, int u) {
+  switch (u) {
+    case 0: return swizzle<0 << 5>(x);
+    case 1: return swizzle<1 << 5>(x);
+    case 2: return swizzle<2 << 5>(x);
+    case 3: return swizzle<3 << 5>(x);
+    case 4: return swizzle<4 << 5>(x);
+    case 5: return swizzle<5 << 5>(x);
+    case 6: return swizzle<6 << 5>(x);
+    default: return swizzle<7 << 5>(x);
+  }
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its
+// outstanding global loads (which __syncthreads would wait for).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 }  // namespace svl

@@ -25,7 +25,7 @@ struct GemvArgs {
   int B;               // batch rows
   int ipw;             // work items per unit (rows, or gate/value pairs for the SiLU gate)
   int parts;           // units per batch row = ceil(items / ipw)
-  int maxb;            // Q8_0: weight blocks per thread and unit (1, 2, 4, 8 or 16)
+  int maxb;            // Q8_0: weight blocks per thread and unit (1 .. 4)
   const float* x;      // input [B][x_stride]
   int x_stride;
   int norm;            // NormKind applied to x in the prologue
@@ -147,7 +147,7 @@ struct StepParams {
   int fwd_T;
 };
 
-constexpr int kStepThreads = 256;
+constexpr int kStepThreads = 1024;
 constexpr int kMaxBatch = 1024;
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s);

@@ -30,20 +30,20 @@ __device__ __forceinline__ bool grid_barrier(SyncState* s, unsigned gen) {
     const unsigned g = blockIdx.x & 7u;
     const unsigned members = gridDim.x / 8u + (g < (gridDim.x & 7u) ? 1u : 0u);
     const unsigned ngroups = gridDim.x < 8u ? gridDim.x : 8u;
-    const unsigned old = __hip_atomic_fetch_add(&s->group[g][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old = __hip_atomic_fetch_add(gbl(&s->group[g][0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old + 1u == members * gen) {
-      const unsigned t = __hip_atomic_fetch_add(&s->top[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t + 1u == ngroups * gen) __hip_atomic_store(&s->release[0], gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned t = __hip_atomic_fetch_add(gbl(&s->top[0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t + 1u == ngroups * gen) __hip_atomic_store(gbl(&s->release[0]), gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     int ok = 1;
     unsigned spins = 0;
-    while (__hip_atomic_load(&s->release[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen) {
-      if (__hip_atomic_load(&s->abort_flag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    while (__hip_atomic_load(gbl(&s->release[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen) {
+      if (__hip_atomic_load(gbl(&s->abort_flag[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
         ok = 0;
         break;
       }
       if (++spins > kSpinLimit) {
-        __hip_atomic_store(&s->abort_flag[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gbl(&s->abort_flag[0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ok = 0;
         break;
       }
@@ -58,19 +58,32 @@ __device__ __forceinline__ bool grid_barrier(SyncState* s, unsigned gen) {
 // them; no later phase of the step reads them).
 __device__ __forceinline__ void load_positions(const StepParams& P, int* spos) {
   for (int b = threadIdx.x; b < P.B; b += kStepThreads) spos[b] = ld_co(P.pos + b);
-  __syncthreads();
+  lds_barrier();
+}
+
+// The program's phase descriptors are copied into LDS once per phase, so the units read their
+// arguments from LDS.
+constexpr int kPhaseWords = sizeof(Phase) / 4;
+static_assert(sizeof(Phase) % 4 == 0 && kPhaseWords <= kStepThreads, "phase descriptor size");
+
+__device__ __forceinline__ void load_phase(const Phase* src, uint32_t* dst) {
+  lds_barrier();
+  if (threadIdx.x < kPhaseWords) dst[threadIdx.x] = ldg((const uint32_t*)src + threadIdx.x);
+  lds_barrier();
 }
 
 __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int spos[kMaxBatch];
+  __shared__ __align__(16) uint32_t ph_words[kPhaseWords];
+  const Phase& ph = *(const Phase*)ph_words;
   unsigned gen = P.gen0;
   for (int step = 0; step < P.n_steps; ++step) {
     load_positions(P, spos);
     for (int p = 0; p < P.nphase; ++p) {
-      const Phase& ph = P.prog[p];
+      load_phase(P.prog + p, ph_words);
       for (int u = blockIdx.x; u < ph.units; u += gridDim.x) {
-        __syncthreads();
+        lds_barrier();
         if (!run_unit(ph, P, step, u, spos, smem)) break;
       }
       if (!grid_barrier(P.sync, ++gen)) return;
@@ -78,11 +91,14 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
   }
 }
 
-__global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* ph, StepParams P, int step) {
+__global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, StepParams P, int step) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int spos[kMaxBatch];
+  __shared__ __align__(16) uint32_t ph_words[kPhaseWords];
+  const Phase& ph = *(const Phase*)ph_words;
+  load_phase(d_ph, ph_words);
   load_positions(P, spos);
-  run_unit(*ph, P, step, blockIdx.x, spos, smem);
+  run_unit(ph, P, step, blockIdx.x, spos, smem);
 }
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s) {
@@ -117,17 +133,18 @@ void plan_gemv(GemvArgs& g, int grid, int* units) {
   const int items = silu ? g.ff_hidden : g.L.out;
   if (g.L.fmt == FMT_Q8_0) {
     const int nb = g.L.in / 32;
-    // About one unit per workgroup and batch row, at most 16 weight blocks per thread.
+    // About one unit per workgroup and batch row, at most 4 weight blocks per thread.
     int ipw = (items + grid - 1) / grid;
     if (g.epi == EPI_QKV_ROPE && (ipw & 1)) ++ipw;
     const int per_row = silu ? 2 : 1;
-    while (ipw > 1 && per_row * ipw * nb > 16 * kStepThreads) ipw = (g.epi == EPI_QKV_ROPE) ? ((ipw / 2 + 1) & ~1) : ipw / 2;
+    if (ipw > kStepThreads / per_row) ipw = kStepThreads / per_row;  // one thread per row in the sums
+    while (ipw > 1 && per_row * ipw * nb > 4 * kStepThreads) ipw = (g.epi == EPI_QKV_ROPE) ? ((ipw / 2 + 1) & ~1) : ipw / 2;
     if (g.epi == EPI_QKV_ROPE && ipw < 2) ipw = 2;
     g.ipw = ipw;
-    g.maxb = pow2_at_least((per_row * ipw * nb + kStepThreads - 1) / kStepThreads);
-    if (g.maxb > 16) g.maxb = 16;
+    g.maxb = (per_row * ipw * nb + kStepThreads - 1) / kStepThreads;
+    if (g.maxb > 4) g.maxb = 4;
   } else {
-    g.ipw = silu ? 8 : 16;
+    g.ipw = silu ? kStepThreads / 32 : kStepThreads / 16;
     g.maxb = 0;
   }
   g.parts = (items + g.ipw - 1) / g.ipw;
@@ -143,7 +160,7 @@ size_t phase_smem(const Phase& ph) {
         const int nb = K / 32, nb4 = (nb + 3) & ~3, ts = nb4 + 4;
         return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
-      return (size_t)K * 4 + 16 * 4 + 64;
+      return (size_t)K * 4 + (kStepThreads / 16) * 4 + 64;
     }
     case PH_ATTN_SOFTMAX_V:
       return (size_t)(((ph.at.cap + 3) & ~3) + 4) * 4 + 64;

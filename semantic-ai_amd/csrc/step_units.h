@@ -1,4 +1,4 @@
-// Work units of the decode step, run by one 256-thread workgroup each.  The same functions
+// Work units of the decode step, run by one 1024-thread workgroup each.  The same functions
 // back the one-kernel-per-phase launches and the persistent step-program kernel.
 //
 // Numerics follow the reference's CPU path (crates/semantic-voice-local/src = SVL) operation
@@ -23,31 +23,38 @@ namespace svl {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// ---- coherent accesses -------------------------------------------------------------------------
+// ---- global memory accesses ----------------------------------------------------------------------
+// Every device pointer the units receive is global memory; it is addressed as such (global_load /
+// global_store rather than flat accesses, whose completion the compiler has to wait for
+// conservatively).
 
-__device__ __forceinline__ float ld_co(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#define SVL_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+__device__ __forceinline__ const SVL_GLOBAL T* gbl(const T* p) {
+  return (const SVL_GLOBAL T*)p;
 }
-__device__ __forceinline__ void st_co(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T>
+__device__ __forceinline__ SVL_GLOBAL T* gbl(T* p) {
+  return (SVL_GLOBAL T*)p;
 }
-__device__ __forceinline__ uint32_t ld_co(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  return *gbl(p);
 }
-__device__ __forceinline__ void st_co(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T>
+__device__ __forceinline__ T ldg_stream(const T* p) {  // read once: non-temporal
+  return __builtin_nontemporal_load(gbl(p));
 }
-__device__ __forceinline__ int ld_co(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+// Coherent accesses: data one workgroup writes and another reads within a launch.
+template <typename T>
+__device__ __forceinline__ T ld_co(const T* p) {
+  return __hip_atomic_load(gbl(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_co(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint16_t ld_co(const uint16_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_co(uint16_t* p, uint16_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T>
+__device__ __forceinline__ void st_co(T* p, T v) {
+  __hip_atomic_store(gbl(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool BF16KV>
@@ -56,98 +63,157 @@ __device__ __forceinline__ float kv_ld(const void* base, size_t idx) {
   return ld_co((const float*)base + idx);
 }
 
-// Copies x[0..n) into xs with coherent loads, eight per thread in flight.
-__device__ __forceinline__ void stage_row(const float* x, int n, float* xs) {
-  constexpr int kRound = 8;
-  for (int i0 = 0; i0 < n; i0 += kRound * kStepThreads) {
-    float v[kRound];
+// ---- rows, norms, activation quantization ---------------------------------------------------------
+// A row of K <= 8192 activations is held in registers, thread t owning elements t + 1024 u.
+
+constexpr int kPerThread = 8192 / kStepThreads;
+
+// v[u] = x[t + 1024 u] (coherent loads, all in flight together); 0 past K.  Every load is
+// issued (past K at the clamped address x[K - 1]) so that the number of loads in flight is
+// known at compile time and waiting for the row never waits for loads issued after it.
+__device__ __forceinline__ void load_row(const float* x, int K, float (&v)[kPerThread]) {
 #pragma unroll
-    for (int k = 0; k < kRound; ++k) {
-      const int i = i0 + threadIdx.x + k * kStepThreads;
-      if (i < n) v[k] = ld_co(x + i);
-    }
+  for (int u = 0; u < kPerThread; ++u) {
+    const int i = threadIdx.x + u * kStepThreads;
+    v[u] = ld_co(x + min(i, K - 1));
+  }
 #pragma unroll
-    for (int k = 0; k < kRound; ++k) {
-      const int i = i0 + threadIdx.x + k * kStepThreads;
-      if (i < n) xs[i] = v[k];
-    }
+  for (int u = 0; u < kPerThread; ++u) {
+    const int i = threadIdx.x + u * kStepThreads;
+    if (i >= K) v[u] = 0.0f;
   }
 }
 
-// ---- row statistics, norms, activation quantization ---------------------------------------------
+__device__ __forceinline__ void store_row(const float (&v)[kPerThread], int K, float* xs) {
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    if (u * kStepThreads >= K) break;  // uniform
+    const int i = threadIdx.x + u * kStepThreads;
+    if (i < K) xs[i] = v[u];
+  }
+}
 
-// Sum of x[i] (or x[i]^2) over a row in the order shared with the oracle: 64 strided partials
-// (lane l adds x[l], x[l+64], ... in order), then a butterfly over the partials (offsets
-// 32 .. 1).  Every lane of every wave computes the same value.
-__device__ __forceinline__ float blocked_sum(const float* xs, int K, bool squares) {
+// Lane 0 ends with the oracle's butterfly over 64 partials: for o = 32, 16, ..., 1, lane l < o
+// adds lane l + o (the lanes whose results reach lane 0).
+__device__ __forceinline__ float lane0_tree_sum(float v) {
+  v = v + __shfl_down(v, 32, kWave);
+  v = v + swizzle<0x401F>(v);  // lane ^ 16
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));  // row_shl:8
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xf, 0xf, false));  // row_shl:4
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xf, 0xf, false));  // row_shl:2
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xf, 0xf, false));  // row_shl:1
+  return v;
+}
+
+// Sums of x[i] and of x[i]^2 over a row in the order shared with the oracle: 64 strided partials
+// (lane l adds x[l], x[l+64], ... in order), then the butterfly over the partials (offsets
+// 32 .. 1).  Run by one wave; the totals are valid in lane 0.
+template <bool PLAIN>
+__device__ __forceinline__ void blocked_sums(const float* xs, int K, float& s, float& s2) {
   const int lane = threadIdx.x % kWave;
-  float acc = 0.0f;
+  constexpr int U = 16;
+  float a = 0.0f, a2 = 0.0f;
   int i = lane;
-  for (; i + 7 * kWave < K; i += 8 * kWave) {
-    float v[8];
+  for (; i + (U - 1) * kWave < K; i += U * kWave) {
+    float v[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = xs[i + u * kWave];
+    for (int u = 0; u < U; ++u) v[u] = xs[i + u * kWave];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      float t = v[u];
-      if (squares) t = t * t;
-      acc = acc + t;
+    for (int u = 0; u < U; ++u) {
+      if (PLAIN) a = a + v[u];
+      const float t = v[u] * v[u];
+      a2 = a2 + t;
     }
   }
   for (; i < K; i += kWave) {
-    float v = xs[i];
-    if (squares) v = v * v;
-    acc = acc + v;
+    const float v = xs[i];
+    if (PLAIN) a = a + v;
+    const float t = v * v;
+    a2 = a2 + t;
   }
+  s = PLAIN ? lane0_tree_sum(a) : 0.0f;
+  s2 = lane0_tree_sum(a2);
+}
+
+// Norm weights of the elements a thread owns, loaded ahead of the row statistics.
+struct NormW {
+  float w[kPerThread], b[kPerThread];
+};
+
+__device__ __forceinline__ void load_norm_weights(int norm, const float* nw, const float* nb, int K, NormW& o) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, kWave);
-  return acc;
+  for (int u = 0; u < kPerThread; ++u) o.w[u] = ldg(nw + min((int)threadIdx.x + u * kStepThreads, K - 1));
+  if (norm == NORM_LAYER) {
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) o.b[u] = ldg(nb + min((int)threadIdx.x + u * kStepThreads, K - 1));
+  }
 }
 
 // candle-nn rms_norm (x / m * alpha, m = sqrt(sum(x^2) / K + eps)) or layer_norm
-// ((x - mean) * (1 / sqrt(var + eps)) * w + b, var = sum(x^2) / K - mean^2) of xs in place.
-__device__ void norm_lds(float* xs, int K, int norm, const float* nw, const float* nb, float eps) {
-  __syncthreads();
-  if (norm == NORM_RMS) {
-    const float s2 = blocked_sum(xs, K, true);
-    const float m = sqrtf(s2 / (float)K + eps);
-    __syncthreads();
-    for (int i = threadIdx.x; i < K; i += kStepThreads) {
-      float t = xs[i] / m;
-      xs[i] = t * nw[i];
-    }
-  } else {
-    const float s = blocked_sum(xs, K, false);
-    const float s2 = blocked_sum(xs, K, true);
-    const float mean = s / (float)K;
-    const float mm = mean * mean;
-    const float var = s2 / (float)K - mm;
-    const float inv_std = 1.0f / sqrtf(var + eps);
-    __syncthreads();
-    for (int i = threadIdx.x; i < K; i += kStepThreads) {
-      float t = (xs[i] - mean) * inv_std;
-      t = t * nw[i];
-      xs[i] = t + nb[i];
+// ((x - mean) * (1 / sqrt(var + eps)) * w + b, var = sum(x^2) / K - mean^2) of the row in v,
+// in place.  xs (K floats) and stats (2 floats) are LDS scratch; wave 0 computes the
+// statistics.
+__device__ __forceinline__ void norm_regs(float (&v)[kPerThread], int K, int norm, const NormW& nw, float eps, float* xs,
+                                          float* stats) {
+  store_row(v, K, xs);
+  lds_barrier();
+  if (threadIdx.x < kWave) {
+    float s, s2;
+    if (norm == NORM_LAYER) blocked_sums<true>(xs, K, s, s2);
+    else blocked_sums<false>(xs, K, s, s2);
+    if (threadIdx.x == 0) {
+      if (norm == NORM_RMS) {
+        stats[0] = sqrtf(s2 / (float)K + eps);
+      } else {
+        const float mean = s / (float)K;
+        const float mm = mean * mean;
+        const float var = s2 / (float)K - mm;
+        stats[0] = mean;
+        stats[1] = 1.0f / sqrtf(var + eps);
+      }
     }
   }
-  __syncthreads();
+  lds_barrier();
+  const float s0 = stats[0], s1 = stats[1];
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    if (u * kStepThreads >= K) break;  // uniform
+    if (norm == NORM_RMS) {
+      const float t = v[u] / s0;
+      v[u] = t * nw.w[u];
+    } else {
+      float t = (v[u] - s0) * s1;
+      t = t * nw.w[u];
+      v[u] = t + nw.b[u];
+    }
+  }
 }
 
-// candle BlockQ8_0::from_float of xs[0..K) into xq (int8) and xdq (the f16-rounded scales as
-// f32).  A half-wave owns one block per iteration (lane = element).
-__device__ void quantize_lds(const float* xs, int K, int8_t* xq, float* xdq) {
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  constexpr int nwaves = kStepThreads / kWave;
-  const int nb = K / 32;
-  for (int blk = wave * 2 + lane / 32; blk < nb; blk += nwaves * 2) {
-    float v = xs[blk * 32 + (lane % 32)];
-    float amax = half_max(fabsf(v));
-    float d = amax / 127.0f;
-    float id = d != 0.0f ? 1.0f / d : 0.0f;
-    xq[blk * 32 + (lane % 32)] = (int8_t)sat_i8(roundf(v * id));
-    if ((lane % 32) == 0) xdq[blk] = f16_to_f32(f32_to_f16(d));
+// candle BlockQ8_0::from_float of the row in v into xq (int8, LDS) and xdq (the f16-rounded
+// block scales as f32, LDS): amax = max(0, |x_i|...), d = amax / 127, id = 1 / d (0 if d = 0),
+// q_i = round(x_i * id).  The 32 elements of a block are held by the 32 lanes of a half-wave;
+// after the half-wave maximum, lane u of each half computes d and id of the block of element
+// group u, and every lane takes id back from that lane.
+__device__ __forceinline__ void quantize_regs(const float (&v)[kPerThread], int K, int8_t* xq, float* xdq) {
+  const int hl = threadIdx.x & 31;
+  float mine = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    if (u * kStepThreads >= K) break;  // uniform
+    const float m = __uint_as_float(half_max_bits(__float_as_uint(fmaxf(fabsf(v[u]), 0.0f))));
+    if (hl == u) mine = m;
   }
-  __syncthreads();
+  const float dm = mine / 127.0f;
+  const float idm = dm != 0.0f ? 1.0f / dm : 0.0f;
+  const int own = (threadIdx.x & ~31) + hl * kStepThreads;  // first element of lane hl's block
+  if (hl < kPerThread && own < K) xdq[own / 32] = f16_to_f32(f32_to_f16(dm));
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    if (u * kStepThreads >= K) break;  // uniform
+    const float id = half_lane(idm, u);
+    const int i = threadIdx.x + u * kStepThreads;
+    if (i < K) xq[i] = (int8_t)sat_i8(roundf(v[u] * id));
+  }
 }
 
 // acc = 0; acc += t[i] for i = 0 .. n-1 in order, reading t (16-byte aligned, in LDS) 16 values
@@ -190,15 +256,15 @@ struct EpiIn {
 };
 
 __device__ __forceinline__ EpiIn gemv_epi_prefetch(const GemvArgs& a, int b, int row, int p) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
   EpiIn e;
   if (a.epi == EPI_QKV_ROPE) {
-    const int qdim = a.H * a.hd, kvdim = a.KVH * a.hd;
-    if (row < qdim + kvdim) {
-      const int rr = row < qdim ? row : row - qdim;
-      const float* cs = a.rope + ((size_t)p * (a.hd / 2) + (rr % a.hd) / 2) * 2;
-      e.a = cs[0];
-      e.b = cs[1];
-    }
+    // q rows, then k rows; v rows (no rotation) read an unused but valid entry
+    const int qdim = a.H * a.hd;
+    const int rr = row < qdim ? row : row - qdim;
+    const v2f cs = ldg((const v2f*)(a.rope + ((size_t)p * (a.hd / 2) + (rr % a.hd) / 2) * 2));
+    e.a = cs.x;
+    e.b = cs.y;
   } else if (a.epi == EPI_RESID) {
     e.a = ld_co(a.resid + (size_t)b * a.resid_stride + row);
   }
@@ -222,7 +288,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row,
     }
     case EPI_RESID: {
       float u = y;
-      if (a.lscale) u = u * a.lscale[row];
+      if (a.lscale) u = u * ldg(a.lscale + row);
       st_co(a.resid + (size_t)b * a.resid_stride + row, in.a + u);
       break;
     }
@@ -290,7 +356,7 @@ __device__ __forceinline__ int term_stride(int nb) { return ((nb + 3) & ~3) + 4;
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 template <int MAXB>
-__device__ void gemv_q8_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
+__device__ __forceinline__ void gemv_q8_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
   const int K = a.L.in, nb = K / 32;
   const int b = unit / a.parts, part = unit % a.parts;
   const bool silu = a.epi == EPI_SILU_GATE;
@@ -304,34 +370,57 @@ __device__ void gemv_q8_unit(const GemvArgs& a, int unit, const int* spos, unsig
   int8_t* xq = (int8_t*)(xs + K);       // K
   float* xdq = (float*)(xq + K);        // nb (+ pad to 16 bytes)
   float* T = xdq + ((nb + 3) & ~3);     // 2 * ipw * ts
-  float* Y = T + 2 * a.ipw * ts;        // 2 * ipw
+  float* Y = T + 2 * a.ipw * ts;        // 2 * ipw (first 2 floats: norm statistics)
 
-  EpiIn in;
-  if ((int)threadIdx.x < ni) in = gemv_epi_prefetch(a, b, i0 + threadIdx.x, p);
+  // The epilogue inputs, the row and its norm weights are requested before the weight blocks:
+  // loads complete in order, so the norm and the quantization run while the weights stream in.
+  const EpiIn in = gemv_epi_prefetch(a, b, i0 + min((int)threadIdx.x, ni - 1), p);
+  NormW nwt;
+  if (a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
+  float v[kPerThread];
+  load_row(a.x + (size_t)b * a.x_stride, K, v);
+  __builtin_amdgcn_sched_barrier(0);
   const int8_t* wq = (const int8_t*)a.L.w;
   v4i wa[MAXB], wb[MAXB];
-  uint16_t wd[MAXB];
+  uint32_t wd[MAXB];
+  // block k of this thread: index threadIdx.x + 1024 k = r * nb + blk, stepped without division
+  int rk[MAXB], bk[MAXB];
+  {
+    int r = threadIdx.x / nb, blk = threadIdx.x - (threadIdx.x / nb) * nb;
+    const int dr = kStepThreads / nb, db = kStepThreads - dr * nb;
 #pragma unroll
-  for (int k = 0; k < MAXB; ++k) {
-    const int idx = threadIdx.x + k * kStepThreads;
-    if (idx < total) {
-      const int r = idx / nb, blk = idx - r * nb;
-      const size_t row = (size_t)gemv_phys_row(a, i0, ni, r);
-      const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
-      wa[k] = __builtin_nontemporal_load(wp);
-      wb[k] = __builtin_nontemporal_load(wp + 1);
-      wd[k] = a.L.scale[row * nb + blk];
+    for (int k = 0; k < MAXB; ++k) {
+      rk[k] = r;
+      bk[k] = blk;
+      r += dr;
+      blk += db;
+      if (blk >= nb) {
+        blk -= nb;
+        ++r;
+      }
     }
   }
-  stage_row(a.x + (size_t)b * a.x_stride, K, xs);
-  if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
-  else __syncthreads();
-  quantize_lds(xs, K, xq, xdq);
+  // Every thread issues MAXB block loads (past the unit's blocks: the unit's first block again),
+  // so their number is known at compile time.
+#pragma unroll
+  for (int k = 0; k < MAXB; ++k) {
+    const bool live = (int)threadIdx.x + k * kStepThreads < total;
+    const int r = live ? rk[k] : 0, blk = live ? bk[k] : 0;
+    const size_t row = (size_t)gemv_phys_row(a, i0, ni, r);
+    const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
+    wa[k] = ldg_stream(wp);
+    wb[k] = ldg_stream(wp + 1);
+    wd[k] = ldg(a.L.scale + row * nb + blk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (a.norm != NORM_NONE) norm_regs(v, K, a.norm, nwt, a.eps, xs, Y);
+  quantize_regs(v, K, xq, xdq);
+  lds_barrier();
 #pragma unroll
   for (int k = 0; k < MAXB; ++k) {
     const int idx = threadIdx.x + k * kStepThreads;
     if (idx < total) {
-      const int r = idx / nb, blk = idx - r * nb;
+      const int r = rk[k], blk = bk[k];
       const v4i xa = *(const v4i*)(xq + blk * 32);
       const v4i xb = *(const v4i*)(xq + blk * 32 + 16);
       int s = sdot4(wa[k].x, xa.x, 0);
@@ -342,24 +431,24 @@ __device__ void gemv_q8_unit(const GemvArgs& a, int unit, const int* spos, unsig
       s = sdot4(wb[k].y, xb.y, s);
       s = sdot4(wb[k].z, xb.z, s);
       s = sdot4(wb[k].w, xb.w, s);
-      float t = (float)s * f16_to_f32(wd[k]);
+      float t = (float)s * f16_to_f32((uint16_t)wd[k]);
       T[r * ts + blk] = t * xdq[blk];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if ((int)threadIdx.x < NR) Y[threadIdx.x] = ordered_sum(T + threadIdx.x * ts, nb);
-  __syncthreads();
+  lds_barrier();
   gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
 // ---- dense GEMV unit ----------------------------------------------------------------------------
 // The reference's matvec (SVL/nn/kernels/matvec.rs:239-246) with its 16-lane dot
 // (kernels/mod.rs:66-91): 16 threads per row, thread i accumulating x[16c + i] * w[16c + i]
-// with FMA over c, then the pairwise lane sum and the scalar tail.  16 rows per unit
-// (8 gate/value pairs for the SiLU gate).
+// with FMA over c, then the pairwise lane sum and the scalar tail.  Up to 64 rows per unit
+// (32 gate/value pairs for the SiLU gate).
 
 template <bool BF16W>
-__device__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
+__device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
   const int K = a.L.in;
   const int b = unit / a.parts, part = unit % a.parts;
   const bool silu = a.epi == EPI_SILU_GATE;
@@ -368,12 +457,19 @@ __device__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, un
   const int NR = silu ? 2 * ni : ni;
   const int p = spos[b];
   float* xs = (float*)smem;   // K
-  float* Y = xs + K;          // 16
+  float* Y = xs + K;          // kStepThreads / 16 (first 2 floats: norm statistics)
   EpiIn in;
   if ((int)threadIdx.x < ni) in = gemv_epi_prefetch(a, b, i0 + threadIdx.x, p);
-  stage_row(a.x + (size_t)b * a.x_stride, K, xs);
-  if (a.norm != NORM_NONE) norm_lds(xs, K, a.norm, a.nw, a.nb, a.eps);
-  else __syncthreads();
+  NormW nwt;
+  if (a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
+  float v[kPerThread];
+  load_row(a.x + (size_t)b * a.x_stride, K, v);
+  if (a.norm != NORM_NONE) {
+    norm_regs(v, K, a.norm, nwt, a.eps, xs, Y);
+    lds_barrier();  // every read of xs by the statistics is done
+  }
+  store_row(v, K, xs);
+  lds_barrier();
   const int g = threadIdx.x / 16, li = threadIdx.x % 16;
   const int chunks = K / 16;
   if (g < NR) {
@@ -385,21 +481,21 @@ __device__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, un
       for (; c + 16 <= chunks; c += 16) {
         uint16_t wv[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+        for (int u = 0; u < 16; ++u) wv[u] = ldg_stream(w + (size_t)(c + u) * 16);
 #pragma unroll
         for (int u = 0; u < 16; ++u) acc = fmaf(xs[(c + u) * 16 + li], bf16_to_f32(wv[u]), acc);
       }
-      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], bf16_to_f32(w[(size_t)c * 16]), acc);
+      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], bf16_to_f32(ldg(w + (size_t)c * 16)), acc);
     } else {
       const float* w = (const float*)a.L.w + row * K + li;
       for (; c + 16 <= chunks; c += 16) {
         float wv[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) wv[u] = __builtin_nontemporal_load(w + (size_t)(c + u) * 16);
+        for (int u = 0; u < 16; ++u) wv[u] = ldg_stream(w + (size_t)(c + u) * 16);
 #pragma unroll
         for (int u = 0; u < 16; ++u) acc = fmaf(xs[(c + u) * 16 + li], wv[u], acc);
       }
-      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], w[(size_t)c * 16], acc);
+      for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], ldg(w + (size_t)c * 16), acc);
     }
     // pairwise lane sum: acc[i] += acc[i + width] for width 8, 4, 2, 1
 #pragma unroll
@@ -407,14 +503,14 @@ __device__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, un
     if (li == 0) {
       float tail = 0.0f;
       for (int i = chunks * 16; i < K; ++i) {
-        const float wv = BF16W ? bf16_to_f32(((const uint16_t*)a.L.w)[row * K + i]) : ((const float*)a.L.w)[row * K + i];
+        const float wv = BF16W ? bf16_to_f32(ldg((const uint16_t*)a.L.w + row * K + i)) : ldg((const float*)a.L.w + row * K + i);
         float pr = xs[i] * wv;
         tail = tail + pr;
       }
       Y[g] = acc + tail;
     }
   }
-  __syncthreads();
+  lds_barrier();
   gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
@@ -423,9 +519,8 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, const int
     switch (a.maxb) {
       case 1: gemv_q8_unit<1>(a, unit, spos, smem); break;
       case 2: gemv_q8_unit<2>(a, unit, spos, smem); break;
-      case 4: gemv_q8_unit<4>(a, unit, spos, smem); break;
-      case 8: gemv_q8_unit<8>(a, unit, spos, smem); break;
-      default: gemv_q8_unit<16>(a, unit, spos, smem); break;
+      case 3: gemv_q8_unit<3>(a, unit, spos, smem); break;
+      default: gemv_q8_unit<4>(a, unit, spos, smem); break;
     }
   } else if (a.L.fmt == FMT_BF16) {
     gemv_dense_unit<true>(a, unit, spos, smem);
@@ -437,14 +532,14 @@ __device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, const int
 // ---- attention units ----------------------------------------------------------------------------
 // The query at position p attends to keys max(0, p - window + 1) ..= p (transformer.rs:385) in
 // the ring, in the reference's order (attention.rs:139-168):
-//   scores:    w_j = scale * dot(q, k_j) with the 16-lane dot; 16 keys per unit, one per
+//   scores:    w_j = scale * dot(q, k_j) with the 16-lane dot; 64 keys per unit, one per
 //              16-thread group.  Units are chunk-major (chunk = unit / (B * H)), so once a
 //              chunk is past every stream's keys the workgroup has no more work in the phase.
 //   softmax_v: max, e_j = exp(w_j - max), sum of e_j in key order, then
 //              out = sum over keys in order of mul_add(e_j / sum, v_j, out).  One unit per
 //              (stream, head); wave w produces dims [32w, 32w + 32).
 
-constexpr int kKeysPerUnit = 16;
+constexpr int kKeysPerUnit = kStepThreads / 16;
 
 __device__ __forceinline__ int visible_keys(const AttnArgs& a, int p) {
   return a.window > 0 ? min(p + 1, a.window) : p + 1;
@@ -452,7 +547,7 @@ __device__ __forceinline__ int visible_keys(const AttnArgs& a, int p) {
 
 // Returns false when no later unit of this phase has keys to score.
 template <int HD, bool BF16KV>
-__device__ bool attn_scores_unit(const AttnArgs& a, int unit, const int* spos) {
+__device__ __forceinline__ bool attn_scores_unit(const AttnArgs& a, int unit, const int* spos) {
   const int chunk = unit / (a.B * a.H);
   const int bh = unit % (a.B * a.H);
   const int b = bh / a.H, h = bh % a.H;
@@ -487,7 +582,7 @@ __device__ bool attn_scores_unit(const AttnArgs& a, int unit, const int* spos) {
 }
 
 template <int HD, bool BF16KV>
-__device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem) {
+__device__ __forceinline__ void attn_softmax_v_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem) {
   float* w = (float*)smem;                     // L weights (16-byte aligned)
   float* sum_slot = w + ((a.cap + 3) & ~3);    // 1
   const int h = unit % a.H, b = unit / a.H;
@@ -508,7 +603,7 @@ __device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, const int* spos
       if (j < L) w[j] = v[u];
     }
   }
-  __syncthreads();
+  lds_barrier();
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (wave == 0) {
     float mx = -__builtin_huge_valf();
@@ -519,15 +614,15 @@ __device__ void attn_softmax_v_unit(const AttnArgs& a, int unit, const int* spos
     __builtin_amdgcn_wave_barrier();
     if (lane == 0) sum_slot[0] = ordered_sum(w, L);
   }
-  __syncthreads();
+  lds_barrier();
   const float sum = sum_slot[0];
   for (int j = threadIdx.x; j < L; j += kStepThreads) w[j] = w[j] / sum;
-  __syncthreads();
+  lds_barrier();
   if (wave < HD / 32 && lane < 32) {
     const int d = wave * 32 + lane;
     const int kvh = h / (a.H / a.KVH);
     const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
-    constexpr int CH = 32;
+    constexpr int CH = 16;
     float acc = 0.0f;
     float cur[CH], nxt[CH];
 #pragma unroll
@@ -571,31 +666,31 @@ __device__ __forceinline__ void attn_softmax_v_dispatch(const AttnArgs& a, int u
 // ---- embedding, argmax, norm, copies ----------------------------------------------------------
 
 // SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
-// ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 256.
-__device__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit, const int* spos) {
+// ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 1024.
+__device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit, const int* spos) {
   const int chunks = (a.d + kStepThreads - 1) / kStepThreads;
   const int b = unit / chunks;
   const int i = (unit % chunks) * kStepThreads + threadIdx.x;
   if (i >= a.d) return;
   const bool initial = a.initial_at_zero && spos[b] == 0;
   const uint32_t* au = audio + (size_t)b * a.n_q;
-  uint32_t t = text ? text[b] : ld_co(a.fb_tok + b);
+  uint32_t t = text ? ldg(text + b) : ld_co(a.fb_tok + b);
   t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
   const size_t rows = (size_t)a.card + 1;
-  float x = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.text_emb)[(size_t)t * a.d + i])
-                          : ((const float*)a.text_emb)[(size_t)t * a.d + i];
-  constexpr int G = 32;  // codebooks per round: tokens, then rows, then the adds in order
+  float x = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.text_emb + (size_t)t * a.d + i))
+                          : ldg((const float*)a.text_emb + (size_t)t * a.d + i);
+  constexpr int G = 16;  // codebooks per round: tokens, then rows, then the adds in order
   for (int c0 = 0; c0 < a.n_q; c0 += G) {
     uint32_t tok[G];
     float e[G];
 #pragma unroll
-    for (int u = 0; u < G; ++u) tok[u] = c0 + u < a.n_q ? (initial ? (uint32_t)a.card : au[c0 + u]) : 0u;
+    for (int u = 0; u < G; ++u) tok[u] = c0 + u < a.n_q ? (initial ? (uint32_t)a.card : ldg(au + c0 + u)) : 0u;
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       if (c0 + u < a.n_q) {
         const uint32_t tk = tok[u] > (uint32_t)a.card ? (uint32_t)a.card : tok[u];
         const size_t idx = ((size_t)(c0 + u) * rows + tk) * a.d + i;
-        e[u] = a.tables_bf16 ? bf16_to_f32(((const uint16_t*)a.emb)[idx]) : ((const float*)a.emb)[idx];
+        e[u] = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.emb + idx)) : ldg((const float*)a.emb + idx);
       }
     }
 #pragma unroll
@@ -606,14 +701,14 @@ __device__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint3
 }
 
 // argmax over logits[b] (first index of the maximum); unit = stream.
-__device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsigned char* smem) {
+__device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsigned char* smem) {
   float* sv = (float*)smem;
   int* si = (int*)(sv + 16);
   const int b = unit;
   const float* lg = a.logits + (size_t)b * a.V;
   float best = -__builtin_huge_valf();
   int idx = 0x7fffffff;
-  constexpr int R = 32;
+  constexpr int R = 8;
   for (int i0 = 0; i0 < a.V; i0 += R * kStepThreads) {
     float v[R];
 #pragma unroll
@@ -644,7 +739,7 @@ __device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsign
     sv[wave] = best;
     si[wave] = idx;
   }
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x == 0) {
     float bv = sv[0];
     int bi = si[0];
@@ -661,15 +756,22 @@ __device__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsign
 }
 
 // y[b] = norm(x[b]); unit = stream.
-__device__ void norm_unit(const NormArgs& a, int unit, unsigned char* smem) {
+__device__ __forceinline__ void norm_unit(const NormArgs& a, int unit, unsigned char* smem) {
   float* xs = (float*)smem;
-  stage_row(a.x + (size_t)unit * a.x_stride, a.d, xs);
-  norm_lds(xs, a.d, a.norm, a.w, a.b, a.eps);
-  for (int i = threadIdx.x; i < a.d; i += kStepThreads) st_co(a.y + (size_t)unit * a.y_stride + i, xs[i]);
+  NormW nwt;
+  load_norm_weights(a.norm, a.w, a.b, a.d, nwt);
+  float v[kPerThread];
+  load_row(a.x + (size_t)unit * a.x_stride, a.d, v);
+  norm_regs(v, a.d, a.norm, nwt, a.eps, xs, xs + a.d);
+#pragma unroll
+  for (int u = 0; u < kPerThread; ++u) {
+    const int i = threadIdx.x + u * kStepThreads;
+    if (i < a.d) st_co(a.y + (size_t)unit * a.y_stride + i, v[u]);
+  }
 }
 
-// y[b][0..n) = x[b][0..n); unit = (stream, 256-element chunk).
-__device__ void copy_unit(const float* x, int x_stride, float* y, int y_stride, int n, int unit) {
+// y[b][0..n) = x[b][0..n); unit = (stream, 1024-element chunk).
+__device__ __forceinline__ void copy_unit(const float* x, int x_stride, float* y, int y_stride, int n, int unit) {
   const int chunks = (n + kStepThreads - 1) / kStepThreads;
   const int b = unit / chunks;
   const int i = (unit % chunks) * kStepThreads + threadIdx.x;

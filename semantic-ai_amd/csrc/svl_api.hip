@@ -490,7 +490,7 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     a.at.scores = s->scores;
     a.at.out = s->att;
     a.kind = PH_ATTN_SCORES;
-    a.units = s->B * H * ((s->slots + 15) / 16);
+    a.units = s->B * H * ((s->slots + kStepThreads / 16 - 1) / (kStepThreads / 16));
     out.push_back(a);
     a.kind = PH_ATTN_SOFTMAX_V;
     a.units = s->B * H;

@@ -25,7 +25,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-LIB_PATH = os.path.join(PKG, "lib", "libsvl.so")
+LIB_PATH = os.environ.get("SVL_LIBRARY") or os.path.join(PKG, "lib", "libsvl.so")
 
 F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
 NORM_LAYER, NORM_RMS = 0, 1
