@@ -6,9 +6,15 @@ Q8_0, batch 1, greedy decoding from an empty state.  A step is one decode step: 
 gather-sum, 16 layers, output norm, text_linear, argmax, with the argmax fed back as the next
 text token on the device.  Inputs (weights, audio tokens) are resident in HBM before timing.
 
-Prints ONE JSON line (rank 0).  `value` is decode steps/s; `roofline` prices the step against
-MI355X HBM bandwidth with the algorithmic bytes of the steps actually timed; `cpu_baseline` is
-the oracle (this repository's C restatement of the reference's CPU path) on the host cores.
+Prints ONE JSON line (rank 0).  `value` is decode steps/s; `roofline` prices the dominant
+kernel -- the persistent step-program kernel, one launch of which runs all the timed steps --
+against MI355X HBM bandwidth with the algorithmic bytes of the steps it ran; its `traffic` is the
+HBM bytes of that launch as measured by rocprofv3 counters (profiles/), when the profiled launch
+had the same number of steps; `cpu_baseline` is the oracle (this repository's C restatement of
+the reference's CPU path) on the host cores.
+
+`--calibrate-copy BYTES` instead runs the plain copy kernel of libsvl three times over BYTES
+(the known-size reference that scales the traffic counters) and prints one JSON line.
 """
 import argparse
 import json
@@ -25,6 +31,45 @@ for p in (ROOT, PKG):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "step_program_kernel.stt1b_q8_0_b1.traffic.txt")
+
+
+def read_traffic(steps):
+    """HBM bytes of one step-program launch of `steps` steps, from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel calibration), or
+    None when no summary for that launch size exists."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    kv = {}
+    for line in open(TRAFFIC_FILE):
+        if ":" in line and not line.lstrip().startswith("#"):
+            k, v = line.split(":", 1)
+            kv[k.strip()] = v.strip()
+    try:
+        if int(kv["steps_per_dispatch"]) != steps:
+            return None
+        return int(float(kv["hbm_bytes_per_dispatch"]))
+    except (KeyError, ValueError):
+        return None
+
+
+def calibrate_copy(nbytes):
+    import svl
+    from svl import hip
+
+    L = svl.load_library()
+    src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    e0, e1 = hip.Event(), hip.Event()
+    times = []
+    for _ in range(3):
+        e0.record(None)
+        svl._check(L.svl_bench_copy(0, src.address, dst.address, nbytes, None))
+        e1.record(None)
+        hip.synchronize()
+        times.append(e0.elapsed_ms(e1))
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "dispatches": 3,
+                      "ms": [round(t, 4) for t in times],
+                      "GBps_read_plus_write": round(2 * nbytes / (min(times) / 1e3) / 1e9, 1)}), flush=True)
 
 
 def step_bytes(shape, dtype, kv_bytes, positions, window):
@@ -62,15 +107,19 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--warmup", type=int, default=256)
     ap.add_argument("--cpu-steps", type=int, default=64)
     ap.add_argument("--cpu-threads", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step has no multi-GPU path "
               "(independent streams shard across GPUs with no communication).", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     import svl
     from svl import hip
@@ -81,17 +130,17 @@ def main():
     tensors = W.make_weights(shape, dtype, seed=0)
     print(f"weights generated in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     model = svl.Model(shape.config(W.quantize_code(dtype)), tensors, kv_dtype=svl.F32)
-    n_total = args.warmup + args.steps
-    audio = W.audio_tokens(shape, max(n_total, args.cpu_steps), seed=1)[0]
+    audio = W.audio_tokens(shape, max(args.steps, args.cpu_steps), seed=1)[0]
     d_audio = hip.DeviceBuffer.from_array(audio)
-    d_out = hip.DeviceBuffer(n_total * 4)
+    d_out = hip.DeviceBuffer(args.steps * 4)
 
     st = model.init_state()
     e0, e1 = hip.Event(), hip.Event()
-    # warm-up, then restart the stream from position 0
-    model.recognize_async(args.warmup, d_audio.address, d_out.address, st)
-    st.synchronize()
-    st.reset()
+    # warm-up: launches of the same size as the timed one, each from position 0
+    for _ in range(max(1, -(-args.warmup // args.steps)) if args.warmup > 0 else 0):
+        model.recognize_async(args.steps, d_audio.address, d_out.address, st)
+        st.synchronize()
+        st.reset()
     hip.synchronize()
     t0 = time.perf_counter()
     e0.record(st.stream)
@@ -104,7 +153,8 @@ def main():
     steps_per_s = args.steps / (gpu_ms / 1e3)
 
     bytes_per_step = step_bytes(shape, dtype, 4, range(args.steps), shape.context)
-    achieved = float(bytes_per_step.mean()) / (gpu_ms / 1e3 / args.steps) / 1e9
+    launch_bytes = float(bytes_per_step.sum())
+    achieved = launch_bytes / (gpu_ms / 1e3) / 1e9
 
     line = {
         "metric": "decode steps/s at B=1 (STT-1B-shape, Q8_0); % of HBM roofline",
@@ -124,10 +174,11 @@ def main():
                    "head_dim": shape.head_dim, "ff_hidden": shape.ff_hidden, "window": shape.context,
                    "text_vocab": shape.text_card, "codebooks": shape.n_q, "batch": 1,
                    "kv_dtype": "f32", "wall_s": round(wall, 4)},
-        "roofline": {"bound": "hbm", "kernel": "decode step (all kernels of one step)",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "bytes_per_step": int(bytes_per_step.mean()), "traffic": None},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(args.steps),
+                     "kernel": "step_program_kernel (one launch = all timed steps)",
+                     "algorithmic_bytes_per_launch": int(launch_bytes),
+                     "launch_ms": round(gpu_ms, 4)},
     }
     if not args.no_cpu_baseline:
         cps, toks = cpu_baseline(shape, dtype, tensors, audio, args.cpu_steps, args.cpu_threads)

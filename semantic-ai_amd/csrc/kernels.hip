@@ -7,6 +7,8 @@
 //     at a grid barrier between phases (all workgroups are co-resident: cooperative launch of
 //     one workgroup per CU), or
 //   * as one kernel launch per phase (the same units, one workgroup per unit).
+#include <algorithm>
+
 #include "kernels.h"
 #include "step_units.h"
 
@@ -293,6 +295,20 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s) {
 }
 hipError_t launch_fill_i32(int* p, int v, size_t n, hipStream_t s) {
   hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, n);
+  return hipGetLastError();
+}
+
+// Plain streaming copy (calibration of the HBM traffic counters): grid-stride 16-byte moves.
+__global__ __launch_bounds__(256) void copy_kernel(const v4i* src, v4i* dst, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    __builtin_nontemporal_store(ldg_stream(src + i), gbl(dst + i));
+}
+
+hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s) {
+  const size_t n = bytes / 16;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, s, (const v4i*)src, (v4i*)dst, n);
   return hipGetLastError();
 }
 

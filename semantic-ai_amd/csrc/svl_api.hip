@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "../../include/svl.h"
+#include "../../include/svl_bench.h"
 #include "kernels.h"
 
 using namespace svl;
@@ -808,6 +809,15 @@ const char* svl_last_error(void) { return g_error.c_str(); }
 
 int svl_device_count(int* count) {
   HIP_TRY(hipGetDeviceCount(count));
+  return 0;
+}
+
+int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* stream) {
+  if ((bytes % 16) || ((uintptr_t)src % 16) || ((uintptr_t)dst % 16))
+    return set_error(SVL_ERR_INVALID_INPUT, "copy needs 16-byte multiples and alignment");
+  if (bytes && (!src || !dst)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  HIP_TRY(hipSetDevice(device));
+  HIP_TRY(launch_copy(src, dst, bytes, (hipStream_t)stream));
   return 0;
 }
 

@@ -40,6 +40,7 @@ EXPORTS = [
     "svl_state_layer_cache", "svl_state_positions", "svl_state_reset", "svl_state_destroy",
     "svl_state_synchronize", "svl_state_stream", "svl_transformer_forward", "svl_stt_step",
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_tts_backbone_step",
+    "svl_bench_copy",
 ]
 
 
@@ -105,6 +106,7 @@ def load_library(path: str = LIB_PATH):
     L.svl_stt_recognize.argtypes = [vp, vp, i64, vp, vp]
     L.svl_stt_recognize_async.argtypes = [vp, vp, i64, vp, vp]
     L.svl_tts_backbone_step.argtypes = [vp, vp, vp, vp]
+    L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
     for name in EXPORTS:
         if name not in ("svl_last_error", "svl_model_destroy", "svl_state_destroy", "svl_state_stream"):
             getattr(L, name).restype = C.c_int
