@@ -15,43 +15,11 @@ constexpr int kWave = 64;
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
-// IEEE binary16 -> f32 (exact).
-__device__ __forceinline__ float f16_to_f32(uint16_t h) {
-  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
-  uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
-  uint32_t man = (uint32_t)h & 0x3ffu;
-  if (exp == 0x1fu) return u2f(sign | 0x7f800000u | (man << 13));
-  if (exp == 0) {
-    if (man == 0) return u2f(sign);
-    return u2f(sign | f2u((float)man * 0x1p-24f));
-  }
-  return u2f(sign | ((exp + 112u) << 23) | (man << 13));
-}
-
-// f32 -> binary16, round to nearest even (the `half` crate's f16::from_f32 semantics).
-__device__ __forceinline__ uint16_t f32_to_f16(float f) {
-  uint32_t x = f2u(f);
-  uint32_t sign = (x >> 16) & 0x8000u;
-  uint32_t exp = (x >> 23) & 0xffu;
-  uint32_t man = x & 0x7fffffu;
-  if (exp == 0xffu) return (uint16_t)(man ? (sign | 0x7e00u | (man >> 13)) : (sign | 0x7c00u));
-  int e = (int)exp - 112;
-  if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u);
-  if (e <= 0) {
-    if (e < -10) return (uint16_t)sign;
-    uint32_t m = man | 0x800000u;
-    int shift = 14 - e;
-    uint32_t hm = m >> shift;
-    uint32_t half = 1u << (shift - 1);
-    uint32_t rem = m & ((1u << shift) - 1u);
-    if (rem > half || (rem == half && (hm & 1u))) hm++;
-    return (uint16_t)(sign | hm);
-  }
-  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
-  uint32_t rem = man & 0x1fffu;
-  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
-  return (uint16_t)h;
-}
+// IEEE binary16 <-> f32 with the hardware conversions (v_cvt_f32_f16 / v_cvt_f16_f32: exact
+// widening and round-to-nearest-even narrowing, f16 subnormals kept -- the `half` crate's
+// f16::to_f32 / from_f32 for every non-NaN value).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 
@@ -132,7 +100,7 @@ __device__ __forceinline__ uint32_t half_max_bits(uint32_t v) {
   return v;
 }
 
-// x of lane u (u < 8, known after unrolling) of the calling lane's 32-lane half.
+// x of lane u (u < 16, known after unrolling) of the calling lane's 32-lane half.
 __device__ __forceinline__ float half_lane(float x, int u) {
   switch (u) {
     case 0: return swizzle<0 << 5>(x);
@@ -142,7 +110,15 @@ __device__ __forceinline__ float half_lane(float x, int u) {
     case 4: return swizzle<4 << 5>(x);
     case 5: return swizzle<5 << 5>(x);
     case 6: return swizzle<6 << 5>(x);
-    default: return swizzle<7 << 5>(x);
+    case 7: return swizzle<7 << 5>(x);
+    case 8: return swizzle<8 << 5>(x);
+    case 9: return swizzle<9 << 5>(x);
+    case 10: return swizzle<10 << 5>(x);
+    case 11: return swizzle<11 << 5>(x);
+    case 12: return swizzle<12 << 5>(x);
+    case 13: return swizzle<13 << 5>(x);
+    case 14: return swizzle<14 << 5>(x);
+    default: return swizzle<15 << 5>(x);
   }
 }
 

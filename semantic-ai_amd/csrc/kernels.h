@@ -25,7 +25,7 @@ struct GemvArgs {
   int B;               // batch rows
   int ipw;             // work items per unit (rows, or gate/value pairs for the SiLU gate)
   int parts;           // units per batch row = ceil(items / ipw)
-  int maxb;            // Q8_0: weight blocks per thread and unit (1 .. 4)
+  int maxb;            // Q8_0: weight blocks per weight-wave thread and unit (1 .. kWBlocks)
   const float* x;      // input [B][x_stride]
   int x_stride;
   int norm;            // NormKind applied to x in the prologue
@@ -59,7 +59,6 @@ struct AttnArgs {
   int B, H, KVH, hd, cap, window;  // window 0 = unlimited
   int kv_bf16;
   float scale;
-  float* scores;       // [B][H][cap] scratch: scaled q.k of the visible keys
   float* out;          // [B][H*hd]
 };
 
@@ -104,8 +103,7 @@ struct CopyArgs {           // y[b][0..n) = x[b][0..n)
 };
 
 // One phase of a step program: a unit function applied to `units` work units.
-enum PhaseKind { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN_SCORES = 2, PH_ATTN_SOFTMAX_V = 3, PH_ARGMAX = 4, PH_NORM = 5,
-                 PH_COPY_IN = 6, PH_COPY_OUT = 7 };
+enum PhaseKind { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN = 2, PH_ARGMAX = 4, PH_NORM = 5, PH_COPY_IN = 6, PH_COPY_OUT = 7 };
 
 struct Phase {
   int kind;
@@ -147,7 +145,10 @@ struct StepParams {
   int fwd_T;
 };
 
-constexpr int kStepThreads = 1024;
+constexpr int kStepThreads = 1024;                       // workgroup of the step kernels
+constexpr int kRowThreads = 512;                         // row waves: threads [0, 512)
+constexpr int kWeightThreads = kStepThreads - kRowThreads;  // weight waves: threads [512, 1024)
+constexpr int kWBlocks = 6;                              // Q8_0 blocks per weight-wave thread and unit
 constexpr int kMaxBatch = 1024;
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s);

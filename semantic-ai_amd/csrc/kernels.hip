@@ -14,81 +14,101 @@
 
 namespace svl {
 
-// ---- grid barrier -------------------------------------------------------------------------------
-// Hierarchical arrive: each workgroup adds to the counter of its group (blockIdx % 8), the last
-// arriver of a group adds to the top counter, the last group publishes the generation.  Counters
-// only grow (generation g completes when group counters reach g * members), so nothing is reset
-// between barriers or launches.  All data a workgroup wrote in the phase was stored with
-// agent-scope stores, and waited for before arriving.  A bounded spin sets the abort flag instead
-// of hanging; every workgroup then leaves the kernel.
+// ---- grid barrier (row waves) ----------------------------------------------------------------------
+// Each row wave waits for its own stores of the phase and counts itself in LDS; the first row
+// wave then adds one to the counter of the workgroup's group (blockIdx % 8) without waiting for
+// the result, polls the group counters until each has reached generation x members, and
+// releases the other row waves through LDS.  Counters only grow, so nothing is reset between
+// barriers or launches (the host clears them long before 32-bit wrap).  A bounded spin sets the
+// abort flag instead of hanging; every workgroup then leaves the kernel.
 
 constexpr unsigned kSpinLimit = 1u << 22;
 
-__device__ __forceinline__ bool grid_barrier(SyncState* s, unsigned gen) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  __shared__ int s_ok;
-  if (threadIdx.x == 0) {
-    const unsigned g = blockIdx.x & 7u;
-    const unsigned members = gridDim.x / 8u + (g < (gridDim.x & 7u) ? 1u : 0u);
-    const unsigned ngroups = gridDim.x < 8u ? gridDim.x : 8u;
-    const unsigned old = __hip_atomic_fetch_add(gbl(&s->group[g][0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old + 1u == members * gen) {
-      const unsigned t = __hip_atomic_fetch_add(gbl(&s->top[0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t + 1u == ngroups * gen) __hip_atomic_store(gbl(&s->release[0]), gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ unsigned group_members(unsigned g) {
+  return gridDim.x / 8u + (g < (gridDim.x & 7u) ? 1u : 0u);
+}
+
+// Row waves only; `n` counts the grid barriers of this launch (1, 2, ...).  False when the
+// launch is aborting.
+__device__ __forceinline__ bool grid_barrier(SyncState* s, unsigned gen, unsigned n, WgSync* ws) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are complete
+  lds_signal(&ws->g_arrive);
+  if (threadIdx.x >= kWave) return lds_wait<true>(&ws->g_release, n, &ws->stop);
+  const int lane = threadIdx.x;
+  if (!lds_wait(&ws->g_arrive, n * kRowWaves, &ws->stop)) return false;
+  if (lane == 0) __hip_atomic_fetch_add(gbl(&s->group[blockIdx.x & 7u][0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned ngroups = gridDim.x < 8u ? gridDim.x : 8u;
+  const unsigned target = lane < (int)ngroups ? group_members(lane) * gen : 0u;
+  const unsigned* ctr = lane < (int)ngroups ? &s->group[lane][0] : &s->abort_flag[0];
+  bool ok = true;
+  unsigned spins = 0;
+  for (;;) {
+    const unsigned v = __hip_atomic_load(gbl(ctr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned ab = __hip_atomic_load(gbl(&s->abort_flag[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool waiting = lane < (int)ngroups && (int)(v - target) < 0;
+    if (ab || lds_ld(&ws->stop)) {
+      ok = false;
+      break;
     }
-    int ok = 1;
-    unsigned spins = 0;
-    while (__hip_atomic_load(gbl(&s->release[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen) {
-      if (__hip_atomic_load(gbl(&s->abort_flag[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-        ok = 0;
-        break;
-      }
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(gbl(&s->abort_flag[0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = 0;
-        break;
-      }
+    if (!__any(waiting)) break;
+    if (++spins > kSpinLimit) {
+      if (lane == 0) __hip_atomic_store(gbl(&s->abort_flag[0]), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = false;
+      break;
     }
-    s_ok = ok;
   }
-  __syncthreads();
-  return s_ok != 0;
+  if (lane == 0) {
+    if (ok) __hip_atomic_store(&ws->g_release, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else __hip_atomic_store(&ws->stop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  return ok;
 }
 
 // Positions of the streams at the start of the step, cached in LDS (the last layer advances
-// them; no later phase of the step reads them).
+// them; no later phase of the step reads them).  Row waves.
 __device__ __forceinline__ void load_positions(const StepParams& P, int* spos) {
-  for (int b = threadIdx.x; b < P.B; b += kStepThreads) spos[b] = ld_co(P.pos + b);
-  lds_barrier();
+  for (int b = threadIdx.x; b < P.B; b += kRowThreads) spos[b] = ld_co(P.pos + b);
 }
 
-// The program's phase descriptors are copied into LDS once per phase, so the units read their
-// arguments from LDS.
-constexpr int kPhaseWords = sizeof(Phase) / 4;
-static_assert(sizeof(Phase) % 4 == 0 && kPhaseWords <= kStepThreads, "phase descriptor size");
+// The phase descriptors are read with scalar loads from the program (read-only during a launch),
+// so the compiler may read a field again instead of keeping it in registers.
+__device__ __forceinline__ const Phase& phase_at(const Phase* prog, int p) {
+  return *(const Phase*)(const SVL_CONST Phase*)(prog + p);
+}
 
-__device__ __forceinline__ void load_phase(const Phase* src, uint32_t* dst) {
-  lds_barrier();
-  if (threadIdx.x < kPhaseWords) dst[threadIdx.x] = ldg((const uint32_t*)src + threadIdx.x);
-  lds_barrier();
+__device__ __forceinline__ void init_wg_sync(WgSync* ws) {
+  if (threadIdx.x == 0) {
+    ws->r_arrive = 0;
+    ws->xq_parts = 0;
+    ws->t_parts = 0;
+    ws->r_issued = 0;
+    ws->g_arrive = 0;
+    ws->g_release = 0;
+    ws->stop = 0;
+  }
+  __syncthreads();  // the only full-workgroup barrier: nothing is in flight yet
 }
 
 __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int spos[kMaxBatch];
-  __shared__ __align__(16) uint32_t ph_words[kPhaseWords];
-  const Phase& ph = *(const Phase*)ph_words;
+  __shared__ WgSync ws;
+  init_wg_sync(&ws);
+  if (threadIdx.x >= kRowThreads) {
+    weight_waves(P, &ws, smem);
+    return;
+  }
+  RowSync rs{&ws, 0u};
   unsigned gen = P.gen0;
+  unsigned item = 0;
   for (int step = 0; step < P.n_steps; ++step) {
     load_positions(P, spos);
+    rs.sync();
     for (int p = 0; p < P.nphase; ++p) {
-      load_phase(P.prog + p, ph_words);
-      for (int u = blockIdx.x; u < ph.units; u += gridDim.x) {
-        lds_barrier();
-        if (!run_unit(ph, P, step, u, spos, smem)) break;
-      }
-      if (!grid_barrier(P.sync, ++gen)) return;
+      const Phase& ph = phase_at(P.prog, p);
+      for (int u = blockIdx.x; u < ph.units; u += gridDim.x) run_unit(ph, P, step, u, spos, smem, rs, item);
+      ++gen;
+      if (!grid_barrier(P.sync, gen, gen - P.gen0, &ws)) return;
     }
   }
 }
@@ -96,11 +116,24 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
 __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, StepParams P, int step) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int spos[kMaxBatch];
-  __shared__ __align__(16) uint32_t ph_words[kPhaseWords];
-  const Phase& ph = *(const Phase*)ph_words;
-  load_phase(d_ph, ph_words);
+  __shared__ WgSync ws;
+  init_wg_sync(&ws);
+  if (threadIdx.x >= kRowThreads) {
+    if (is_q8_gemv(d_ph)) {
+      WItem it;
+      if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
+      w_issue(d_ph, blockIdx.x, it);
+      if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+      w_terms(it, smem);
+      lds_signal(&ws.t_parts);
+    }
+    return;
+  }
+  RowSync rs{&ws, 0u};
   load_positions(P, spos);
-  run_unit(ph, P, step, blockIdx.x, spos, smem);
+  rs.sync();
+  unsigned item = 0;
+  run_unit(phase_at(d_ph, 0), P, step, blockIdx.x, spos, smem, rs, item);
 }
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s) {
@@ -124,29 +157,24 @@ int step_program_grid(int device) {
 
 // ---- planning ---------------------------------------------------------------------------------
 
-static int pow2_at_least(int v) {
-  int p = 1;
-  while (p < v) p <<= 1;
-  return p;
-}
-
 void plan_gemv(GemvArgs& g, int grid, int* units) {
   const bool silu = g.epi == EPI_SILU_GATE;
   const int items = silu ? g.ff_hidden : g.L.out;
   if (g.L.fmt == FMT_Q8_0) {
     const int nb = g.L.in / 32;
-    // About one unit per workgroup and batch row, at most 4 weight blocks per thread.
+    // About one unit per workgroup and batch row; at most kWBlocks weight blocks per weight-wave
+    // thread and one row-wave thread per row for the row sums.
     int ipw = (items + grid - 1) / grid;
     if (g.epi == EPI_QKV_ROPE && (ipw & 1)) ++ipw;
     const int per_row = silu ? 2 : 1;
-    if (ipw > kStepThreads / per_row) ipw = kStepThreads / per_row;  // one thread per row in the sums
-    while (ipw > 1 && per_row * ipw * nb > 4 * kStepThreads) ipw = (g.epi == EPI_QKV_ROPE) ? ((ipw / 2 + 1) & ~1) : ipw / 2;
+    if (ipw > kRowThreads / per_row) ipw = kRowThreads / per_row;
+    while (ipw > 1 && per_row * ipw * nb > kWBlocks * kWeightThreads) ipw = (g.epi == EPI_QKV_ROPE) ? ((ipw / 2 + 1) & ~1) : ipw / 2;
     if (g.epi == EPI_QKV_ROPE && ipw < 2) ipw = 2;
     g.ipw = ipw;
-    g.maxb = (per_row * ipw * nb + kStepThreads - 1) / kStepThreads;
-    if (g.maxb > 4) g.maxb = 4;
+    g.maxb = (per_row * ipw * nb + kWeightThreads - 1) / kWeightThreads;
+    if (g.maxb > kWBlocks) g.maxb = kWBlocks;
   } else {
-    g.ipw = silu ? kStepThreads / 32 : kStepThreads / 16;
+    g.ipw = silu ? kRowThreads / 32 : kRowThreads / 16;
     g.maxb = 0;
   }
   g.parts = (items + g.ipw - 1) / g.ipw;
@@ -159,17 +187,19 @@ size_t phase_smem(const Phase& ph) {
       const GemvArgs& g = ph.g;
       const int K = g.L.in;
       if (g.L.fmt == FMT_Q8_0) {
-        const int nb = K / 32, nb4 = (nb + 3) & ~3, ts = nb4 + 4;
-        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
+        const int nb = K / 32, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
+        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)nb * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
-      return (size_t)K * 4 + (kStepThreads / 16) * 4 + 64;
+      return (size_t)K * 4 + (kRowThreads / 16) * 4 + 64;
     }
-    case PH_ATTN_SOFTMAX_V:
+    case PH_ATTN:
       return (size_t)(((ph.at.cap + 3) & ~3) + 4) * 4 + 64;
     case PH_ARGMAX:
       return 32 * 4 + 64;
     case PH_NORM:
       return (size_t)ph.nm.d * 4 + 64;
+    case PH_EMBED:
+      return (size_t)(ph.e.n_q + 1) * 4 + 64;
     default:
       return 64;
   }

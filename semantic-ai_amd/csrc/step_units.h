@@ -1,5 +1,5 @@
-// Work units of the decode step, run by one 1024-thread workgroup each.  The same functions
-// back the one-kernel-per-phase launches and the persistent step-program kernel.
+// Work units of the decode step.  The same functions back the persistent step-program kernel
+// and the one-kernel-per-phase launches.
 //
 // Numerics follow the reference's CPU path (crates/semantic-voice-local/src = SVL) operation
 // for operation, so results are bit-identical to the CPU restatement in oracle/:
@@ -9,11 +9,24 @@
 //   * dense matvec with the reference's 16-lane dot (SVL/nn/kernels/mod.rs:66-91).
 //   * attention with the reference's two passes (SVL/nn/kernels/attention.rs:139-168).
 //   * SiLU / GELU-tanh / exp as SVL/nn/kernels/{activation,mod}.rs (FMA variant).
-//   * RMSNorm / LayerNorm statistics in a 64-way blocked order (see blocked_sum).
+//   * RMSNorm / LayerNorm statistics in a 64-way blocked order (see blocked_sums).
 //
 // Data one workgroup writes and another reads within a launch (activations, KV ring, scores,
 // logits, tokens, positions) goes through agent-scope coherent loads and stores (the `sc1`
 // cache policy on gfx950), so no cache-wide fence is needed at phase boundaries.
+//
+// Workgroup roles.  A workgroup is 16 waves.  The row waves (threads [0, 512)) run every
+// unit's dependent chain -- input row, norm, quantization, row sums, epilogues, attention,
+// embedding, argmax -- and the grid barrier.  The weight waves (threads [512, 1024)) only
+// stream Q8_0 weight blocks into registers and compute the block dot products.  Weight waves
+// never join a workgroup barrier: they request the next unit's blocks as soon as the current
+// unit's dot products are written, and issuing those loads may wait on the memory system for
+// microseconds, during which the row waves go on with the epilogue, the grid barrier and the
+// next input row.  The groups hand over through counters in LDS (WgSync); the Q8_0 GEMV units
+// a workgroup runs are numbered in program order ("items"):
+//   xq_parts  += 1 per row wave once its part of item i's quantized input row is in LDS,
+//   t_parts   += 1 per weight wave once its block terms of item i are in LDS.
+// Row waves synchronize among themselves with a counter barrier (RowSync).
 #pragma once
 
 #include "device_math.h"
@@ -29,6 +42,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // conservatively).
 
 #define SVL_GLOBAL __attribute__((address_space(1)))
+#define SVL_CONST __attribute__((address_space(4)))
 
 template <typename T>
 __device__ __forceinline__ const SVL_GLOBAL T* gbl(const T* p) {
@@ -45,6 +59,12 @@ __device__ __forceinline__ T ldg(const T* p) {
 template <typename T>
 __device__ __forceinline__ T ldg_stream(const T* p) {  // read once: non-temporal
   return __builtin_nontemporal_load(gbl(p));
+}
+// Uniform read of memory that no kernel writes while a launch runs (the step program):
+// scalar loads.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  return *(const SVL_CONST T*)p;
 }
 
 // Coherent accesses: data one workgroup writes and another reads within a launch.
@@ -63,32 +83,107 @@ __device__ __forceinline__ float kv_ld(const void* base, size_t idx) {
   return ld_co((const float*)base + idx);
 }
 
+// ---- workgroup roles and LDS hand-over -----------------------------------------------------------
+
+constexpr int kRowWaves = kRowThreads / kWave;
+constexpr int kWeightWaves = kWeightThreads / kWave;
+
+struct WgSync {
+  unsigned r_arrive;   // row-wave barrier arrivals
+  unsigned xq_parts;   // row waves done quantizing an item's input row
+  unsigned t_parts;    // weight waves done with an item's block terms
+  unsigned r_issued;   // row waves that have requested an item's input row
+  unsigned g_arrive;   // row waves whose stores of the phase are complete (grid barrier)
+  unsigned g_release;  // grid barriers of the launch this workgroup has passed
+  unsigned stop;       // raised when a wait gave up or the grid barrier aborted
+};
+
+constexpr unsigned kLdsSpinLimit = 1u << 22;
+
+__device__ __forceinline__ unsigned lds_ld(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits until *ctr reaches `target` (counters only grow; the comparison is wrap-safe).  Returns
+// false once `stop` is raised, or after the spin limit (which raises it).  Long waits (LONG)
+// sleep between polls so that the waiting wave leaves the SIMD and LDS to the others.
+template <bool LONG = false>
+__device__ __forceinline__ bool lds_wait(const unsigned* ctr, unsigned target, unsigned* stop) {
+  unsigned spins = 0;
+  while ((int)(lds_ld(ctr) - target) < 0) {
+    if (lds_ld(stop)) return false;
+    if (++spins > kLdsSpinLimit) {
+      __hip_atomic_store(stop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      return false;
+    }
+    if (LONG) __builtin_amdgcn_s_sleep(2);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  return true;
+}
+
+// This wave's LDS writes complete, then lane 0 adds one to *ctr.
+__device__ __forceinline__ void lds_signal(unsigned* ctr) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  if ((threadIdx.x & (kWave - 1)) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// LDS writes of this wave are visible to its own later reads (LDS operations of a wave complete
+// in order; this keeps the compiler from moving reads above the writes).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Barrier of the row waves.  Every row wave calls sync() the same number of times.
+struct RowSync {
+  WgSync* ws;
+  unsigned epoch;
+  __device__ __forceinline__ void sync() {
+    lds_signal(&ws->r_arrive);
+    epoch += kRowWaves;
+    lds_wait(&ws->r_arrive, epoch, &ws->stop);
+  }
+};
+
 // ---- rows, norms, activation quantization ---------------------------------------------------------
-// A row of K <= 8192 activations is held in registers, thread t owning elements t + 1024 u.
+// A row of K <= 8192 activations is held in registers by the row waves, thread t owning
+// elements t + 512 u for u < KP, KP = row_slots(K) (a compile-time count, so that no branch
+// merges the register arrays).  Slots past K read the clamped address x[K - 1] and hold 0.
 
-constexpr int kPerThread = 8192 / kStepThreads;
+constexpr int kMaxSlots = 8192 / kRowThreads;
 
-// v[u] = x[t + 1024 u] (coherent loads, all in flight together); 0 past K.  Every load is
-// issued (past K at the clamped address x[K - 1]) so that the number of loads in flight is
-// known at compile time and waiting for the row never waits for loads issued after it.
-__device__ __forceinline__ void load_row(const float* x, int K, float (&v)[kPerThread]) {
+__host__ __device__ constexpr int row_slots(int K) {
+  return K <= 2 * kRowThreads ? 2 : (K <= 4 * kRowThreads ? 4 : (K <= 8 * kRowThreads ? 8 : kMaxSlots));
+}
+
+// v[u] = x[t + 512 u] (coherent loads, all in flight together); 0 past K.  When `issued` is
+// given, the wave counts itself there once its loads are requested.
+template <int KP>
+__device__ __forceinline__ void load_row(const float* x, int K, float (&v)[KP], unsigned* issued = nullptr) {
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    const int i = threadIdx.x + u * kStepThreads;
+  for (int u = 0; u < KP; ++u) {
+    const int i = threadIdx.x + u * kRowThreads;
     v[u] = ld_co(x + min(i, K - 1));
   }
+  if (issued) {
+    __builtin_amdgcn_sched_barrier(0);
+    lds_signal(issued);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    const int i = threadIdx.x + u * kStepThreads;
-    if (i >= K) v[u] = 0.0f;
+  for (int u = 0; u < KP; ++u) {
+    const int i = threadIdx.x + u * kRowThreads;
+    v[u] = i < K ? v[u] : 0.0f;
   }
 }
 
-__device__ __forceinline__ void store_row(const float (&v)[kPerThread], int K, float* xs) {
+template <int KP>
+__device__ __forceinline__ void store_row(const float (&v)[KP], int K, float* xs) {
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    if (u * kStepThreads >= K) break;  // uniform
-    const int i = threadIdx.x + u * kStepThreads;
+  for (int u = 0; u < KP; ++u) {
+    const int i = threadIdx.x + u * kRowThreads;
     if (i < K) xs[i] = v[u];
   }
 }
@@ -118,6 +213,7 @@ __device__ __forceinline__ void blocked_sums(const float* xs, int K, float& s, f
     float v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) v[u] = xs[i + u * kWave];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (PLAIN) a = a + v[u];
@@ -136,52 +232,52 @@ __device__ __forceinline__ void blocked_sums(const float* xs, int K, float& s, f
 }
 
 // Norm weights of the elements a thread owns, loaded ahead of the row statistics.
+template <int KP>
 struct NormW {
-  float w[kPerThread], b[kPerThread];
+  float w[KP], b[KP];
 };
 
-__device__ __forceinline__ void load_norm_weights(int norm, const float* nw, const float* nb, int K, NormW& o) {
+template <int KP>
+__device__ __forceinline__ void load_norm_weights(int norm, const float* nw, const float* nb, int K, NormW<KP>& o) {
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) o.w[u] = ldg(nw + min((int)threadIdx.x + u * kStepThreads, K - 1));
-  if (norm == NORM_LAYER) {
+  for (int u = 0; u < KP; ++u) o.w[u] = ldg(nw + min((int)threadIdx.x + u * kRowThreads, K - 1));
 #pragma unroll
-    for (int u = 0; u < kPerThread; ++u) o.b[u] = ldg(nb + min((int)threadIdx.x + u * kStepThreads, K - 1));
-  }
+  for (int u = 0; u < KP; ++u) o.b[u] = norm == NORM_LAYER ? ldg(nb + min((int)threadIdx.x + u * kRowThreads, K - 1)) : 0.0f;
 }
 
 // candle-nn rms_norm (x / m * alpha, m = sqrt(sum(x^2) / K + eps)) or layer_norm
 // ((x - mean) * (1 / sqrt(var + eps)) * w + b, var = sum(x^2) / K - mean^2) of the row in v,
-// in place.  xs (K floats) and stats (2 floats) are LDS scratch; wave 0 computes the
-// statistics.
-__device__ __forceinline__ void norm_regs(float (&v)[kPerThread], int K, int norm, const NormW& nw, float eps, float* xs,
-                                          float* stats) {
+// in place.  xs (K floats) is LDS scratch.
+template <int KP>
+__device__ __forceinline__ void norm_regs(float (&v)[KP], int K, int norm, const NormW<KP>& nw, float eps, float* xs,
+                                          RowSync& rs) {
   store_row(v, K, xs);
-  lds_barrier();
-  if (threadIdx.x < kWave) {
-    float s, s2;
-    if (norm == NORM_LAYER) blocked_sums<true>(xs, K, s, s2);
-    else blocked_sums<false>(xs, K, s, s2);
-    if (threadIdx.x == 0) {
-      if (norm == NORM_RMS) {
-        stats[0] = sqrtf(s2 / (float)K + eps);
-      } else {
-        const float mean = s / (float)K;
-        const float mm = mean * mean;
-        const float var = s2 / (float)K - mm;
-        stats[0] = mean;
-        stats[1] = 1.0f / sqrtf(var + eps);
-      }
-    }
+  rs.sync();
+  // every row wave computes the statistics (lane 0 holds them), so no second barrier is needed
+  float s, s2;
+  if (norm == NORM_LAYER) blocked_sums<true>(xs, K, s, s2);
+  else blocked_sums<false>(xs, K, s, s2);
+  s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));    // lane 0's totals
+  s2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s2)));
+  float s0, s1 = 0.0f;
+  if (norm == NORM_RMS) {
+    s0 = sqrtf(s2 / (float)K + eps);
+  } else {
+    const float mean = s / (float)K;
+    const float mm = mean * mean;
+    const float var = s2 / (float)K - mm;
+    s0 = mean;
+    s1 = 1.0f / sqrtf(var + eps);
   }
-  lds_barrier();
-  const float s0 = stats[0], s1 = stats[1];
+  if (norm == NORM_RMS) {
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    if (u * kStepThreads >= K) break;  // uniform
-    if (norm == NORM_RMS) {
+    for (int u = 0; u < KP; ++u) {
       const float t = v[u] / s0;
       v[u] = t * nw.w[u];
-    } else {
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < KP; ++u) {
       float t = (v[u] - s0) * s1;
       t = t * nw.w[u];
       v[u] = t + nw.b[u];
@@ -194,24 +290,23 @@ __device__ __forceinline__ void norm_regs(float (&v)[kPerThread], int K, int nor
 // q_i = round(x_i * id).  The 32 elements of a block are held by the 32 lanes of a half-wave;
 // after the half-wave maximum, lane u of each half computes d and id of the block of element
 // group u, and every lane takes id back from that lane.
-__device__ __forceinline__ void quantize_regs(const float (&v)[kPerThread], int K, int8_t* xq, float* xdq) {
+template <int KP>
+__device__ __forceinline__ void quantize_regs(const float (&v)[KP], int K, int8_t* xq, float* xdq) {
   const int hl = threadIdx.x & 31;
   float mine = 0.0f;
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    if (u * kStepThreads >= K) break;  // uniform
+  for (int u = 0; u < KP; ++u) {
     const float m = __uint_as_float(half_max_bits(__float_as_uint(fmaxf(fabsf(v[u]), 0.0f))));
-    if (hl == u) mine = m;
+    mine = hl == u ? m : mine;
   }
   const float dm = mine / 127.0f;
   const float idm = dm != 0.0f ? 1.0f / dm : 0.0f;
-  const int own = (threadIdx.x & ~31) + hl * kStepThreads;  // first element of lane hl's block
-  if (hl < kPerThread && own < K) xdq[own / 32] = f16_to_f32(f32_to_f16(dm));
+  const int own = (threadIdx.x & ~31) + hl * kRowThreads;  // first element of lane hl's block
+  if (hl < KP && own < K) xdq[own / 32] = f16_to_f32(f32_to_f16(dm));
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    if (u * kStepThreads >= K) break;  // uniform
+  for (int u = 0; u < KP; ++u) {
     const float id = half_lane(idm, u);
-    const int i = threadIdx.x + u * kStepThreads;
+    const int i = threadIdx.x + u * kRowThreads;
     if (i < K) xq[i] = (int8_t)sat_i8(roundf(v[u] * id));
   }
 }
@@ -323,11 +418,16 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row,
   }
 }
 
-__device__ __forceinline__ int gemv_phys_row(const GemvArgs& a, int i0, int ni, int r) {
-  if (a.epi == EPI_SILU_GATE) return r < ni ? i0 + r : i0 + (r - ni) + a.ff_hidden;
+__device__ __forceinline__ int gemv_phys_row(int epi, int ff_hidden, int i0, int ni, int r) {
+  if (epi == EPI_SILU_GATE) return r < ni ? i0 + r : i0 + (r - ni) + ff_hidden;
   return i0 + r;
 }
 
+__device__ __forceinline__ int gemv_items(const GemvArgs& a) {
+  return a.epi == EPI_SILU_GATE ? a.ff_hidden : a.L.out;
+}
+
+// Epilogue of a unit's ni items by row threads t < ni.
 __device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, int i0, int ni, int p, const EpiIn& in,
                                             const float* Y) {
   const int t = threadIdx.x;
@@ -340,115 +440,202 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, 
   if (a.advance_pos && part == 0 && t == 0) st_co(a.pos + b, p + 1);
 }
 
-__device__ __forceinline__ int gemv_items(const GemvArgs& a) {
-  return a.epi == EPI_SILU_GATE ? a.ff_hidden : a.L.out;
+// Terms are stored block-major, T[blk * ts + r] with an odd stride ts = 2 ipw + 1, so that the
+// row threads (consecutive r) and the weight-wave threads (consecutive blk) both access LDS
+// without bank conflicts.
+__device__ __forceinline__ int term_stride(int ipw) { return 2 * ipw + 1; }
+
+// acc = 0; acc += T[blk * ts + r] for blk = 0 .. nb-1 in order; each batch of 32 terms is
+// read before its additions.
+__device__ __forceinline__ float ordered_row_sum(const float* T, int ts, int r, int nb) {
+  constexpr int U = 32;
+  const float* t = T + r;
+  float acc = 0.0f;
+  int blk = 0;
+  for (; blk + U <= nb; blk += U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = t[(blk + u) * ts];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = acc + v[u];
+  }
+  for (; blk < nb; ++blk) acc = acc + t[blk * ts];
+  return acc;
 }
 
-// Row stride of the per-block terms in LDS: 16-byte aligned, padded.
-__device__ __forceinline__ int term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
-
-// ---- Q8_0 GEMV unit ---------------------------------------------------------------------------
+// ---- Q8_0 GEMV ------------------------------------------------------------------------------------
 // Candle's quantized CPU matmul (SVL/nn/mod.rs:97; BlockQ8_0::vec_dot_unopt): terms
-// (exact i32 block dot as f32 * d_w) * d_x, each row adding its terms in block order.  The
-// unit's weight blocks (one 32-byte block per thread and round) are loaded before the input is
-// staged, since they do not depend on it.
+// (exact i32 block dot as f32 * d_w) * d_x, each row adding its terms in block order.  A unit
+// is `ipw` items (rows, or gate/value row pairs of the SiLU gate) of one batch row.
+
+struct Q8Geom {
+  int K, nb, b, part, i0, ni, NR, total, ts;
+};
+
+__device__ __forceinline__ Q8Geom q8_geom(int K, int items, int ipw, int parts, bool silu, int unit) {
+  Q8Geom g;
+  g.K = K;
+  g.nb = K / 32;
+  g.b = unit / parts;
+  g.part = unit - g.b * parts;
+  g.i0 = g.part * ipw;
+  g.ni = min(ipw, items - g.i0);
+  g.NR = silu ? 2 * g.ni : g.ni;
+  g.total = g.NR * g.nb;
+  g.ts = term_stride(ipw);
+  return g;
+}
+
+// LDS of a Q8_0 unit: xs [K] f32 | xq [K] int8 | xdq [nb, padded to 4] f32 | T [nb][ts] f32 |
+// Y [2 ipw] f32.
+struct Q8Lds {
+  float* xs;
+  int8_t* xq;
+  float* xdq;
+  float* T;
+  float* Y;
+};
+
+__device__ __forceinline__ Q8Lds q8_lds(unsigned char* smem, int K, int nb, int ipw, int ts) {
+  Q8Lds l;
+  l.xs = (float*)smem;
+  l.xq = (int8_t*)(l.xs + K);
+  l.xdq = (float*)(l.xq + K);
+  l.T = l.xdq + ((nb + 3) & ~3);
+  l.Y = l.T + nb * ts;
+  return l;
+}
+
+// Row-wave part of Q8_0 GEMV item `item`: input row, norm, quantization, then (once the weight
+// waves have written the terms) the ordered row sums and the epilogue.
+template <int KP>
+__device__ __forceinline__ void gemv_q8_rows(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
+                                             RowSync& rs, unsigned item) {
+  const Q8Geom g = q8_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
+  const Q8Lds l = q8_lds(smem, g.K, g.nb, a.ipw, g.ts);
+  const int p = spos[g.b];
+  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
+  // rows wider than 4096 (row_slots 16) are never normalized (d_model <= 4096)
+  constexpr bool kNorm = KP <= 8;
+  NormW<kNorm ? KP : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, g.K, nwt);
+  float v[KP];
+  load_row(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
+  if constexpr (kNorm) {
+    if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
+  }
+  // the weight waves have read the previous item's quantized row
+  lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
+  quantize_regs(v, g.K, l.xq, l.xdq);
+  lds_signal(&rs.ws->xq_parts);
+  // one thread per row adds the row's terms in block order once every term is written
+  const bool many = g.NR > kWave;  // uniform
+  if (many || threadIdx.x < kWave) {
+    lds_wait(&rs.ws->t_parts, (item + 1) * kWeightWaves, &rs.ws->stop);
+    if ((int)threadIdx.x < g.NR) l.Y[threadIdx.x] = ordered_row_sum(l.T, g.ts, threadIdx.x, g.nb);
+  }
+  if (many) {
+    rs.sync();
+  } else {
+    if (threadIdx.x >= kWave) return;
+    wave_lds_fence();
+  }
+  gemv_finish(a, g.b, g.part, g.i0, g.ni, p, in, l.Y);
+}
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-template <int MAXB>
-__device__ __forceinline__ void gemv_q8_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
-  const int K = a.L.in, nb = K / 32;
-  const int b = unit / a.parts, part = unit % a.parts;
-  const bool silu = a.epi == EPI_SILU_GATE;
-  const int i0 = part * a.ipw;
-  const int ni = min(a.ipw, gemv_items(a) - i0);
-  const int NR = silu ? 2 * ni : ni;
-  const int total = NR * nb;
-  const int ts = term_stride(nb);
-  const int p = spos[b];
-  float* xs = (float*)smem;             // K
-  int8_t* xq = (int8_t*)(xs + K);       // K
-  float* xdq = (float*)(xq + K);        // nb (+ pad to 16 bytes)
-  float* T = xdq + ((nb + 3) & ~3);     // 2 * ipw * ts
-  float* Y = T + 2 * a.ipw * ts;        // 2 * ipw (first 2 floats: norm statistics)
+// Weight-wave state of one item: the item's geometry and this thread's weight blocks.
+struct WItem {
+  Q8Geom g;
+  int ipw;
+  int maxb;
+  v4i wa[kWBlocks], wb[kWBlocks];
+  uint32_t wd[kWBlocks];
+};
 
-  // The epilogue inputs, the row and its norm weights are requested before the weight blocks:
-  // loads complete in order, so the norm and the quantization run while the weights stream in.
-  const EpiIn in = gemv_epi_prefetch(a, b, i0 + min((int)threadIdx.x, ni - 1), p);
-  NormW nwt;
-  if (a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
-  float v[kPerThread];
-  load_row(a.x + (size_t)b * a.x_stride, K, v);
-  __builtin_amdgcn_sched_barrier(0);
-  const int8_t* wq = (const int8_t*)a.L.w;
-  v4i wa[MAXB], wb[MAXB];
-  uint32_t wd[MAXB];
-  // block k of this thread: index threadIdx.x + 1024 k = r * nb + blk, stepped without division
-  int rk[MAXB], bk[MAXB];
-  {
-    int r = threadIdx.x / nb, blk = threadIdx.x - (threadIdx.x / nb) * nb;
-    const int dr = kStepThreads / nb, db = kStepThreads - dr * nb;
+// Requests this weight-wave thread's blocks of unit `unit` of GEMV phase `ph` (descriptor read
+// with scalar loads).  Block k of thread w is index w + 512 k = r * nb + blk of the unit.
+__device__ __forceinline__ void w_issue(const Phase* ph, int unit, WItem& it) {
+  const int K = ld_const(&ph->g.L.in);
+  const int epi = ld_const(&ph->g.epi);
+  const int ff_hidden = ld_const(&ph->g.ff_hidden);
+  const int items = epi == EPI_SILU_GATE ? ff_hidden : ld_const(&ph->g.L.out);
+  it.ipw = ld_const(&ph->g.ipw);
+  it.maxb = ld_const(&ph->g.maxb);
+  it.g = q8_geom(K, items, it.ipw, ld_const(&ph->g.parts), epi == EPI_SILU_GATE, unit);
+  const int8_t* wq = (const int8_t*)ld_const(&ph->g.L.w);
+  const uint16_t* sc = (const uint16_t*)ld_const(&ph->g.L.scale);
+  const int nb = it.g.nb;
+  const int w = threadIdx.x - kRowThreads;
+  int r = w / nb, blk = w - r * nb;
+  const int dr = kWeightThreads / nb, db = kWeightThreads - dr * nb;
 #pragma unroll
-    for (int k = 0; k < MAXB; ++k) {
-      rk[k] = r;
-      bk[k] = blk;
-      r += dr;
-      blk += db;
-      if (blk >= nb) {
-        blk -= nb;
-        ++r;
-      }
+  for (int k = 0; k < kWBlocks; ++k) {
+    if (k >= it.maxb) break;  // uniform
+    if (w + k * kWeightThreads < it.g.total) {
+      const size_t row = (size_t)gemv_phys_row(epi, ff_hidden, it.g.i0, it.g.ni, r);
+      const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
+      it.wa[k] = ldg_stream(wp);
+      it.wb[k] = ldg_stream(wp + 1);
+      it.wd[k] = ldg(sc + row * nb + blk);
+    }
+    r += dr;
+    blk += db;
+    if (blk >= nb) {
+      blk -= nb;
+      ++r;
     }
   }
-  // Every thread issues MAXB block loads (past the unit's blocks: the unit's first block again),
-  // so their number is known at compile time.
-#pragma unroll
-  for (int k = 0; k < MAXB; ++k) {
-    const bool live = (int)threadIdx.x + k * kStepThreads < total;
-    const int r = live ? rk[k] : 0, blk = live ? bk[k] : 0;
-    const size_t row = (size_t)gemv_phys_row(a, i0, ni, r);
-    const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
-    wa[k] = ldg_stream(wp);
-    wb[k] = ldg_stream(wp + 1);
-    wd[k] = ldg(a.L.scale + row * nb + blk);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  if (a.norm != NORM_NONE) norm_regs(v, K, a.norm, nwt, a.eps, xs, Y);
-  quantize_regs(v, K, xq, xdq);
-  lds_barrier();
-#pragma unroll
-  for (int k = 0; k < MAXB; ++k) {
-    const int idx = threadIdx.x + k * kStepThreads;
-    if (idx < total) {
-      const int r = rk[k], blk = bk[k];
-      const v4i xa = *(const v4i*)(xq + blk * 32);
-      const v4i xb = *(const v4i*)(xq + blk * 32 + 16);
-      int s = sdot4(wa[k].x, xa.x, 0);
-      s = sdot4(wa[k].y, xa.y, s);
-      s = sdot4(wa[k].z, xa.z, s);
-      s = sdot4(wa[k].w, xa.w, s);
-      s = sdot4(wb[k].x, xb.x, s);
-      s = sdot4(wb[k].y, xb.y, s);
-      s = sdot4(wb[k].z, xb.z, s);
-      s = sdot4(wb[k].w, xb.w, s);
-      float t = (float)s * f16_to_f32((uint16_t)wd[k]);
-      T[r * ts + blk] = t * xdq[blk];
-    }
-  }
-  lds_barrier();
-  if ((int)threadIdx.x < NR) Y[threadIdx.x] = ordered_sum(T + threadIdx.x * ts, nb);
-  lds_barrier();
-  gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
-// ---- dense GEMV unit ----------------------------------------------------------------------------
+// The item's block terms T[r][blk] = ((f32)(sum qw * qx) * d_w) * d_x into LDS.
+__device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
+  const Q8Lds l = q8_lds(smem, it.g.K, it.g.nb, it.ipw, it.g.ts);
+  const int nb = it.g.nb;
+  const int w = threadIdx.x - kRowThreads;
+  int r = w / nb, blk = w - r * nb;
+  const int dr = kWeightThreads / nb, db = kWeightThreads - dr * nb;
+#pragma unroll
+  for (int k = 0; k < kWBlocks; ++k) {
+    if (k >= it.maxb) break;  // uniform
+    if (w + k * kWeightThreads < it.g.total) {
+      const v4i xa = *(const v4i*)(l.xq + blk * 32);
+      const v4i xb = *(const v4i*)(l.xq + blk * 32 + 16);
+      int s = sdot4(it.wa[k].x, xa.x, 0);
+      s = sdot4(it.wa[k].y, xa.y, s);
+      s = sdot4(it.wa[k].z, xa.z, s);
+      s = sdot4(it.wa[k].w, xa.w, s);
+      s = sdot4(it.wb[k].x, xb.x, s);
+      s = sdot4(it.wb[k].y, xb.y, s);
+      s = sdot4(it.wb[k].z, xb.z, s);
+      s = sdot4(it.wb[k].w, xb.w, s);
+      const float t = (float)s * f16_to_f32((uint16_t)it.wd[k]);
+      l.T[blk * it.g.ts + r] = t * l.xdq[blk];
+    }
+    r += dr;
+    blk += db;
+    if (blk >= nb) {
+      blk -= nb;
+      ++r;
+    }
+  }
+}
+
+__device__ __forceinline__ bool is_q8_gemv(const Phase* ph) {
+  return ld_const(&ph->kind) == PH_GEMV && ld_const(&ph->g.L.fmt) == FMT_Q8_0;
+}
+
+// ---- dense GEMV unit (row waves) -----------------------------------------------------------------
 // The reference's matvec (SVL/nn/kernels/matvec.rs:239-246) with its 16-lane dot
 // (kernels/mod.rs:66-91): 16 threads per row, thread i accumulating x[16c + i] * w[16c + i]
-// with FMA over c, then the pairwise lane sum and the scalar tail.  Up to 64 rows per unit
-// (32 gate/value pairs for the SiLU gate).
+// with FMA over c, then the pairwise lane sum and the scalar tail.  32 rows per unit (16
+// gate/value pairs for the SiLU gate).
 
-template <bool BF16W>
-__device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
+template <bool BF16W, int KP>
+__device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
+                                                RowSync& rs) {
   const int K = a.L.in;
   const int b = unit / a.parts, part = unit % a.parts;
   const bool silu = a.epi == EPI_SILU_GATE;
@@ -457,23 +644,25 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
   const int NR = silu ? 2 * ni : ni;
   const int p = spos[b];
   float* xs = (float*)smem;   // K
-  float* Y = xs + K;          // kStepThreads / 16 (first 2 floats: norm statistics)
-  EpiIn in;
-  if ((int)threadIdx.x < ni) in = gemv_epi_prefetch(a, b, i0 + threadIdx.x, p);
-  NormW nwt;
-  if (a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
-  float v[kPerThread];
+  float* Y = xs + K;          // kRowThreads / 16
+  const EpiIn in = gemv_epi_prefetch(a, b, i0 + min((int)threadIdx.x, ni - 1), p);
+  constexpr bool kNorm = KP <= 8;  // rows wider than 4096 are never normalized (d_model <= 4096)
+  NormW<kNorm ? KP : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
+  float v[KP];
   load_row(a.x + (size_t)b * a.x_stride, K, v);
-  if (a.norm != NORM_NONE) {
-    norm_regs(v, K, a.norm, nwt, a.eps, xs, Y);
-    lds_barrier();  // every read of xs by the statistics is done
+  if constexpr (kNorm) {
+    if (a.norm != NORM_NONE) {
+      norm_regs(v, K, a.norm, nwt, a.eps, xs, rs);
+      rs.sync();  // every read of xs by the statistics is done
+    }
   }
   store_row(v, K, xs);
-  lds_barrier();
+  rs.sync();
   const int g = threadIdx.x / 16, li = threadIdx.x % 16;
   const int chunks = K / 16;
   if (g < NR) {
-    const size_t row = (size_t)gemv_phys_row(a, i0, ni, g);
+    const size_t row = (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, g);
     float acc = 0.0f;
     int c = 0;
     if (BF16W) {
@@ -510,118 +699,80 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
       Y[g] = acc + tail;
     }
   }
-  lds_barrier();
+  rs.sync();
   gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
-__device__ __forceinline__ void gemv_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem) {
-  if (a.L.fmt == FMT_Q8_0) {
-    switch (a.maxb) {
-      case 1: gemv_q8_unit<1>(a, unit, spos, smem); break;
-      case 2: gemv_q8_unit<2>(a, unit, spos, smem); break;
-      case 3: gemv_q8_unit<3>(a, unit, spos, smem); break;
-      default: gemv_q8_unit<4>(a, unit, spos, smem); break;
-    }
-  } else if (a.L.fmt == FMT_BF16) {
-    gemv_dense_unit<true>(a, unit, spos, smem);
-  } else {
-    gemv_dense_unit<false>(a, unit, spos, smem);
-  }
-}
+// ---- attention unit (row waves) ------------------------------------------------------------------
+// One unit per (stream, head).  The query at position p attends to keys
+// max(0, p - window + 1) ..= p (transformer.rs:385) in the ring, in the reference's order
+// (attention.rs:139-168): w_j = scale * dot(q, k_j) with the 16-lane dot (16 threads per key,
+// 32 keys per pass, four passes of loads in flight), max, e_j = exp(w_j - max), the sum of e_j
+// in key order, then out = sum over keys in order of mul_add(e_j / sum, v_j, out); wave w
+// produces dims [32w, 32w + 32).
 
-// ---- attention units ----------------------------------------------------------------------------
-// The query at position p attends to keys max(0, p - window + 1) ..= p (transformer.rs:385) in
-// the ring, in the reference's order (attention.rs:139-168):
-//   scores:    w_j = scale * dot(q, k_j) with the 16-lane dot; 64 keys per unit, one per
-//              16-thread group.  Units are chunk-major (chunk = unit / (B * H)), so once a
-//              chunk is past every stream's keys the workgroup has no more work in the phase.
-//   softmax_v: max, e_j = exp(w_j - max), sum of e_j in key order, then
-//              out = sum over keys in order of mul_add(e_j / sum, v_j, out).  One unit per
-//              (stream, head); wave w produces dims [32w, 32w + 32).
-
-constexpr int kKeysPerUnit = kStepThreads / 16;
+constexpr int kKeysPerPass = kRowThreads / 16;
 
 __device__ __forceinline__ int visible_keys(const AttnArgs& a, int p) {
   return a.window > 0 ? min(p + 1, a.window) : p + 1;
 }
 
-// Returns false when no later unit of this phase has keys to score.
 template <int HD, bool BF16KV>
-__device__ __forceinline__ bool attn_scores_unit(const AttnArgs& a, int unit, const int* spos) {
-  const int chunk = unit / (a.B * a.H);
-  const int bh = unit % (a.B * a.H);
-  const int b = bh / a.H, h = bh % a.H;
-  const int p = spos[b];
-  const int L = visible_keys(a, p);
-  if (chunk * kKeysPerUnit >= L) {
-    int lmax = 0;
-    for (int i = 0; i < a.B; ++i) lmax = max(lmax, visible_keys(a, spos[i]));
-    return chunk * kKeysPerUnit < lmax;
-  }
-  const int jj = chunk * kKeysPerUnit + threadIdx.x / 16;
-  const int li = threadIdx.x % 16;
-  constexpr int C = HD / 16;
-  const int kvh = h / (a.H / a.KVH);
-  const float* qp = a.q + (size_t)b * a.H * HD + (size_t)h * HD + li;
-  float q[C], kv[C];
-  const bool live = jj < L;
-  const int j = p + 1 - L + jj;
-  const size_t base = ((((size_t)b * a.KVH + kvh) * (size_t)a.cap) + (size_t)(live ? j % a.cap : 0)) * HD + li;
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    q[c] = ld_co(qp + c * 16);
-    kv[c] = kv_ld<BF16KV>(a.kc, base + c * 16);
-  }
-  float acc = 0.0f;
-#pragma unroll
-  for (int c = 0; c < C; ++c) acc = fmaf(q[c], kv[c], acc);
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
-  if (live && li == 0) st_co(a.scores + ((size_t)b * a.H + h) * a.cap + jj, a.scale * (acc + 0.0f));
-  return true;
-}
-
-template <int HD, bool BF16KV>
-__device__ __forceinline__ void attn_softmax_v_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem) {
+__device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem, RowSync& rs) {
   float* w = (float*)smem;                     // L weights (16-byte aligned)
   float* sum_slot = w + ((a.cap + 3) & ~3);    // 1
   const int h = unit % a.H, b = unit / a.H;
   const int p = spos[b];
   const int L = visible_keys(a, p);
   const int first = p + 1 - L;
-  const float* sc = a.scores + ((size_t)b * a.H + h) * a.cap;
-  for (int j0 = 0; j0 < L; j0 += 8 * kStepThreads) {
-    float v[8];
+  const int kvh = h / (a.H / a.KVH);
+  const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
+  // scores
+  constexpr int C = HD / 16;
+  constexpr int PASS = 4;
+  const int li = threadIdx.x % 16, grp = threadIdx.x / 16;
+  float q[C];
+  const float* qp = a.q + (size_t)b * a.H * HD + (size_t)h * HD + li;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = j0 + threadIdx.x + u * kStepThreads;
-      if (j < L) v[u] = ld_co(sc + j);
+  for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
+  for (int j0 = 0; j0 < L; j0 += PASS * kKeysPerPass) {
+    float kv[PASS][C];
+#pragma unroll
+    for (int pp = 0; pp < PASS; ++pp) {
+      const int jj = j0 + pp * kKeysPerPass + grp;
+      const size_t base = (head_base + (size_t)(jj < L ? (first + jj) % a.cap : 0)) * HD + li;
+#pragma unroll
+      for (int c = 0; c < C; ++c) kv[pp][c] = kv_ld<BF16KV>(a.kc, base + c * 16);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = j0 + threadIdx.x + u * kStepThreads;
-      if (j < L) w[j] = v[u];
+    for (int pp = 0; pp < PASS; ++pp) {
+      const int jj = j0 + pp * kKeysPerPass + grp;
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) acc = fmaf(q[c], kv[pp][c], acc);
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
+      if (jj < L && li == 0) w[jj] = a.scale * (acc + 0.0f);
     }
   }
-  lds_barrier();
+  rs.sync();
+  // softmax
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (wave == 0) {
     float mx = -__builtin_huge_valf();
     for (int j = lane; j < L; j += kWave) mx = fmaxf(mx, w[j]);
     mx = wave_max(mx);
     for (int j = lane; j < L; j += kWave) w[j] = ref_exp(w[j] - mx);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done before lane 0 reads them
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();
     if (lane == 0) sum_slot[0] = ordered_sum(w, L);
   }
-  lds_barrier();
+  rs.sync();
   const float sum = sum_slot[0];
-  for (int j = threadIdx.x; j < L; j += kStepThreads) w[j] = w[j] / sum;
-  lds_barrier();
+  for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = w[j] / sum;
+  rs.sync();
+  // weighted values
   if (wave < HD / 32 && lane < 32) {
     const int d = wave * 32 + lane;
-    const int kvh = h / (a.H / a.KVH);
-    const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
     constexpr int CH = 16;
     float acc = 0.0f;
     float cur[CH], nxt[CH];
@@ -644,52 +795,53 @@ __device__ __forceinline__ void attn_softmax_v_unit(const AttnArgs& a, int unit,
   }
 }
 
-__device__ __forceinline__ bool attn_scores_dispatch(const AttnArgs& a, int unit, const int* spos) {
+__device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const int* spos, unsigned char* smem,
+                                              RowSync& rs) {
   if (a.hd == 128) {
-    if (a.kv_bf16) return attn_scores_unit<128, true>(a, unit, spos);
-    return attn_scores_unit<128, false>(a, unit, spos);
-  }
-  if (a.kv_bf16) return attn_scores_unit<64, true>(a, unit, spos);
-  return attn_scores_unit<64, false>(a, unit, spos);
-}
-
-__device__ __forceinline__ void attn_softmax_v_dispatch(const AttnArgs& a, int unit, const int* spos, unsigned char* smem) {
-  if (a.hd == 128) {
-    if (a.kv_bf16) attn_softmax_v_unit<128, true>(a, unit, spos, smem);
-    else attn_softmax_v_unit<128, false>(a, unit, spos, smem);
+    if (a.kv_bf16) attn_unit<128, true>(a, unit, spos, smem, rs);
+    else attn_unit<128, false>(a, unit, spos, smem, rs);
   } else {
-    if (a.kv_bf16) attn_softmax_v_unit<64, true>(a, unit, spos, smem);
-    else attn_softmax_v_unit<64, false>(a, unit, spos, smem);
+    if (a.kv_bf16) attn_unit<64, true>(a, unit, spos, smem, rs);
+    else attn_unit<64, false>(a, unit, spos, smem, rs);
   }
 }
 
-// ---- embedding, argmax, norm, copies ----------------------------------------------------------
+// ---- embedding, argmax, norm, copies (row waves) -------------------------------------------------
 
 // SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
-// ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 1024.
-__device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit, const int* spos) {
-  const int chunks = (a.d + kStepThreads - 1) / kStepThreads;
+// ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 512.
+// The stream's tokens are staged in LDS first, then every table row is requested at once.
+__device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit,
+                                           const int* spos, unsigned char* smem, RowSync& rs) {
+  constexpr int G = 32;  // table rows in flight per round
+  uint32_t* stok = (uint32_t*)smem;  // [0]: text token, [1 + c]: token of codebook c
+  const int chunks = (a.d + kRowThreads - 1) / kRowThreads;
   const int b = unit / chunks;
-  const int i = (unit % chunks) * kStepThreads + threadIdx.x;
-  if (i >= a.d) return;
   const bool initial = a.initial_at_zero && spos[b] == 0;
-  const uint32_t* au = audio + (size_t)b * a.n_q;
-  uint32_t t = text ? ldg(text + b) : ld_co(a.fb_tok + b);
-  t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
+  if ((int)threadIdx.x <= a.n_q) {
+    uint32_t t;
+    if (threadIdx.x == 0) {
+      t = text ? ldg(text + b) : ld_co(a.fb_tok + b);
+      t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
+    } else {
+      t = initial ? (uint32_t)a.card : ldg(audio + (size_t)b * a.n_q + threadIdx.x - 1);
+      t = t > (uint32_t)a.card ? (uint32_t)a.card : t;
+    }
+    stok[threadIdx.x] = t;
+  }
+  rs.sync();
+  const int i = (unit % chunks) * kRowThreads + threadIdx.x;
+  if (i >= a.d) return;
   const size_t rows = (size_t)a.card + 1;
+  const uint32_t t = stok[0];
   float x = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.text_emb + (size_t)t * a.d + i))
                           : ldg((const float*)a.text_emb + (size_t)t * a.d + i);
-  constexpr int G = 16;  // codebooks per round: tokens, then rows, then the adds in order
   for (int c0 = 0; c0 < a.n_q; c0 += G) {
-    uint32_t tok[G];
     float e[G];
-#pragma unroll
-    for (int u = 0; u < G; ++u) tok[u] = c0 + u < a.n_q ? (initial ? (uint32_t)a.card : ldg(au + c0 + u)) : 0u;
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       if (c0 + u < a.n_q) {
-        const uint32_t tk = tok[u] > (uint32_t)a.card ? (uint32_t)a.card : tok[u];
-        const size_t idx = ((size_t)(c0 + u) * rows + tk) * a.d + i;
+        const size_t idx = ((size_t)(c0 + u) * rows + stok[1 + c0 + u]) * a.d + i;
         e[u] = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.emb + idx)) : ldg((const float*)a.emb + idx);
       }
     }
@@ -701,24 +853,25 @@ __device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* t
 }
 
 // argmax over logits[b] (first index of the maximum); unit = stream.
-__device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsigned char* smem) {
+__device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsigned char* smem,
+                                            RowSync& rs) {
   float* sv = (float*)smem;
-  int* si = (int*)(sv + 16);
+  int* si = (int*)(sv + kRowWaves);
   const int b = unit;
   const float* lg = a.logits + (size_t)b * a.V;
   float best = -__builtin_huge_valf();
   int idx = 0x7fffffff;
-  constexpr int R = 8;
-  for (int i0 = 0; i0 < a.V; i0 += R * kStepThreads) {
+  constexpr int R = 16;
+  for (int i0 = 0; i0 < a.V; i0 += R * kRowThreads) {
     float v[R];
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const int i = i0 + threadIdx.x + u * kStepThreads;
+      const int i = i0 + threadIdx.x + u * kRowThreads;
       if (i < a.V) v[u] = ld_co(lg + i);
     }
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-      const int i = i0 + threadIdx.x + u * kStepThreads;
+      const int i = i0 + threadIdx.x + u * kRowThreads;
       if (i < a.V && (idx == 0x7fffffff || v[u] > best)) {
         best = v[u];
         idx = i;
@@ -739,11 +892,11 @@ __device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, 
     sv[wave] = best;
     si[wave] = idx;
   }
-  lds_barrier();
+  rs.sync();
   if (threadIdx.x == 0) {
     float bv = sv[0];
     int bi = si[0];
-    for (int w = 1; w < kStepThreads / kWave; ++w) {
+    for (int w = 1; w < kRowWaves; ++w) {
       if (si[w] != 0x7fffffff && (bi == 0x7fffffff || sv[w] > bv || (sv[w] == bv && si[w] < bi))) {
         bv = sv[w];
         bi = si[w];
@@ -756,52 +909,83 @@ __device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, 
 }
 
 // y[b] = norm(x[b]); unit = stream.
-__device__ __forceinline__ void norm_unit(const NormArgs& a, int unit, unsigned char* smem) {
+template <int KP>
+__device__ __forceinline__ void norm_unit(const NormArgs& a, int unit, unsigned char* smem, RowSync& rs) {
   float* xs = (float*)smem;
-  NormW nwt;
+  NormW<KP> nwt;
   load_norm_weights(a.norm, a.w, a.b, a.d, nwt);
-  float v[kPerThread];
+  float v[KP];
   load_row(a.x + (size_t)unit * a.x_stride, a.d, v);
-  norm_regs(v, a.d, a.norm, nwt, a.eps, xs, xs + a.d);
+  norm_regs(v, a.d, a.norm, nwt, a.eps, xs, rs);
 #pragma unroll
-  for (int u = 0; u < kPerThread; ++u) {
-    const int i = threadIdx.x + u * kStepThreads;
+  for (int u = 0; u < KP; ++u) {
+    const int i = threadIdx.x + u * kRowThreads;
     if (i < a.d) st_co(a.y + (size_t)unit * a.y_stride + i, v[u]);
   }
 }
 
-// y[b][0..n) = x[b][0..n); unit = (stream, 1024-element chunk).
+// y[b][0..n) = x[b][0..n); unit = (stream, 512-element chunk).
 __device__ __forceinline__ void copy_unit(const float* x, int x_stride, float* y, int y_stride, int n, int unit) {
-  const int chunks = (n + kStepThreads - 1) / kStepThreads;
+  const int chunks = (n + kRowThreads - 1) / kRowThreads;
   const int b = unit / chunks;
-  const int i = (unit % chunks) * kStepThreads + threadIdx.x;
+  const int i = (unit % chunks) * kRowThreads + threadIdx.x;
   if (i < n) st_co(y + (size_t)b * y_stride + i, ld_co(x + (size_t)b * x_stride + i));
 }
 
-// Runs work unit `unit` of phase `ph` for step `step` of a launch; `spos` holds the streams'
-// positions at the start of the step.  Returns false when the workgroup has no later unit in
-// this phase.
-__device__ __forceinline__ bool run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
-                                         unsigned char* smem) {
+// Row-wave part of work unit `unit` of phase `ph` for step `step` of a launch; `spos` holds
+// the streams' positions at the start of the step, `item` counts the workgroup's Q8_0 GEMV
+// units.
+__device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
+                                         unsigned char* smem, RowSync& rs, unsigned& item) {
+  if (ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
+    switch (row_slots(ph.g.L.in)) {
+      case 2: gemv_q8_rows<2>(ph.g, unit, spos, smem, rs, item); break;
+      case 4: gemv_q8_rows<4>(ph.g, unit, spos, smem, rs, item); break;
+      case 8: gemv_q8_rows<8>(ph.g, unit, spos, smem, rs, item); break;
+      default: gemv_q8_rows<kMaxSlots>(ph.g, unit, spos, smem, rs, item); break;
+    }
+    ++item;
+    return;
+  }
+  rs.sync();  // the previous unit's readers of LDS are done
   switch (ph.kind) {
     case PH_EMBED: {
       const uint32_t* text = P.text ? P.text + (size_t)step * P.text_stride : nullptr;
-      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit, spos);
+      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit, spos, smem, rs);
       break;
     }
     case PH_GEMV:
-      gemv_unit(ph.g, unit, spos, smem);
+      switch (row_slots(ph.g.L.in)) {
+        case 2:
+          if (ph.g.L.fmt == FMT_BF16) gemv_dense_unit<true, 2>(ph.g, unit, spos, smem, rs);
+          else gemv_dense_unit<false, 2>(ph.g, unit, spos, smem, rs);
+          break;
+        case 4:
+          if (ph.g.L.fmt == FMT_BF16) gemv_dense_unit<true, 4>(ph.g, unit, spos, smem, rs);
+          else gemv_dense_unit<false, 4>(ph.g, unit, spos, smem, rs);
+          break;
+        case 8:
+          if (ph.g.L.fmt == FMT_BF16) gemv_dense_unit<true, 8>(ph.g, unit, spos, smem, rs);
+          else gemv_dense_unit<false, 8>(ph.g, unit, spos, smem, rs);
+          break;
+        default:
+          if (ph.g.L.fmt == FMT_BF16) gemv_dense_unit<true, kMaxSlots>(ph.g, unit, spos, smem, rs);
+          else gemv_dense_unit<false, kMaxSlots>(ph.g, unit, spos, smem, rs);
+          break;
+      }
       break;
-    case PH_ATTN_SCORES:
-      return attn_scores_dispatch(ph.at, unit, spos);
-    case PH_ATTN_SOFTMAX_V:
-      attn_softmax_v_dispatch(ph.at, unit, spos, smem);
+    case PH_ATTN:
+      attn_dispatch(ph.at, unit, spos, smem, rs);
       break;
     case PH_ARGMAX:
-      argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem);
+      argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem, rs);
       break;
     case PH_NORM:
-      norm_unit(ph.nm, unit, smem);
+      switch (row_slots(ph.nm.d)) {  // d_model <= 4096
+        case 2: norm_unit<2>(ph.nm, unit, smem, rs); break;
+        case 4: norm_unit<4>(ph.nm, unit, smem, rs); break;
+        default: norm_unit<8>(ph.nm, unit, smem, rs); break;
+      }
       break;
     case PH_COPY_IN:
       copy_unit(P.fwd_in + (size_t)step * ph.cp.n, ph.cp.x_stride, ph.cp.y, ph.cp.y_stride, ph.cp.n, unit);
@@ -810,7 +994,43 @@ __device__ __forceinline__ bool run_unit(const Phase& ph, const StepParams& P, i
       copy_unit(ph.cp.x, ph.cp.x_stride, P.fwd_out + (size_t)step * ph.cp.n, ph.cp.y_stride, ph.cp.n, unit);
       break;
   }
-  return true;
+}
+
+// Weight waves of a launch: the Q8_0 GEMV units of this workgroup in program order
+// (steps x phases x units u = blockIdx.x + k * gridDim.x).  Advances (step, p, u) to the next
+// one; false when there is none.
+__device__ __forceinline__ bool w_next(const StepParams& P, int& step, int& p, int& u) {
+  if (p >= 0) {
+    u += gridDim.x;
+    if (u < ld_const(&P.prog[p].units)) return true;
+  }
+  for (;;) {
+    if (++p >= P.nphase) {
+      p = 0;
+      if (++step >= P.n_steps) return false;
+    }
+    if (is_q8_gemv(P.prog + p) && (int)blockIdx.x < ld_const(&P.prog[p].units)) {
+      u = blockIdx.x;
+      return true;
+    }
+  }
+}
+
+// The weight-wave loop: request an item's blocks, wait for its quantized row, write its terms.
+__device__ __forceinline__ void weight_waves(const StepParams& P, WgSync* ws, unsigned char* smem) {
+  int step = 0, p = -1, u = 0;
+  unsigned item = 0;
+  WItem it;
+  while (w_next(P, step, p, u)) {
+    // the blocks are requested right after the row waves have requested the item's input row,
+    // so that neither the row nor the row waves' stores and barrier traffic queue behind them
+    if (!lds_wait<true>(&ws->r_issued, (item + 1) * kRowWaves, &ws->stop)) return;
+    w_issue(P.prog + p, u, it);
+    if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return;
+    w_terms(it, smem);
+    lds_signal(&ws->t_parts);
+    ++item;
+  }
 }
 
 }  // namespace svl

@@ -133,7 +133,6 @@ struct svl_state {
   std::vector<int64_t> pos_host;
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
-  float* scores = nullptr;    // [B][H][slots]
   float* in = nullptr;        // TTS latent staging [B][latent_dim]
   float* fwd = nullptr;       // transformer forward staging (input then output)
   size_t fwd_cap = 0;
@@ -330,9 +329,10 @@ int check_config(const svl_config* c) {
   if (c->d_model % 32) return set_error(SVL_ERR_CONFIG, "d_model must be a multiple of 32");
   if (c->ff_hidden <= 0 || c->ff_hidden % 32) return set_error(SVL_ERR_CONFIG, "ff_hidden must be a positive multiple of 32");
   if ((c->num_heads * c->head_dim) % 32) return set_error(SVL_ERR_CONFIG, "attention width must be a multiple of 32");
-  // the GEMV prologue stages one input row in LDS (5 bytes per element, 64 KiB per workgroup)
-  if (c->d_model > 8192 || c->ff_hidden > 8192 || c->num_heads * c->head_dim > 8192)
-    return set_error(SVL_ERR_CONFIG, "d_model, ff_hidden and num_heads * head_dim must be <= 8192");
+  // a GEMV input row is held by 512 row-wave threads, 16 elements each (8 for normalized rows)
+  if (c->d_model > 4096) return set_error(SVL_ERR_CONFIG, "d_model must be <= 4096");
+  if (c->ff_hidden > 8192 || c->num_heads * c->head_dim > 8192)
+    return set_error(SVL_ERR_CONFIG, "ff_hidden and num_heads * head_dim must be <= 8192");
   // attention stages one head's weights over the window in LDS
   if (c->context > 16000) return set_error(SVL_ERR_CONFIG, "context must be <= 16000");
   if (c->norm_kind != SVL_NORM_LAYER && c->norm_kind != SVL_NORM_RMS) return set_error(SVL_ERR_CONFIG, "unknown norm");
@@ -488,12 +488,8 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     a.at.window = c.context;
     a.at.kv_bf16 = kv_bf16;
     a.at.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
-    a.at.scores = s->scores;
     a.at.out = s->att;
-    a.kind = PH_ATTN_SCORES;
-    a.units = s->B * H * ((s->slots + kStepThreads / 16 - 1) / (kStepThreads / 16));
-    out.push_back(a);
-    a.kind = PH_ATTN_SOFTMAX_V;
+    a.kind = PH_ATTN;
     a.units = s->B * H;
     out.push_back(a);
     // out_proj + residual (layer scale if any)
@@ -583,7 +579,7 @@ int build_programs(const svl_model* m, svl_state* s) {
     e.e.initial_at_zero = 1;
     e.e.pos = s->pos;
     e.e.x = s->x;
-    e.units = s->B * ((d + kStepThreads - 1) / kStepThreads);
+    e.units = s->B * ((d + kRowThreads - 1) / kRowThreads);
     P.push_back(e);
     build_layers(m, s, P);
     Phase t = gemv_phase(s, m->text_linear);
@@ -657,7 +653,7 @@ int build_programs(const svl_model* m, svl_state* s) {
     ci.cp.y_stride = d;
     ci.cp.B = s->B;
     ci.cp.n = d;
-    ci.units = s->B * ((d + kStepThreads - 1) / kStepThreads);
+    ci.units = s->B * ((d + kRowThreads - 1) / kRowThreads);
     P.push_back(ci);
     build_layers(m, s, P);
     Phase co = ci;
@@ -773,7 +769,6 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * width * 4), s->h = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.text_card, 1) * 4), s->logits = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.d_model, c.z_dim) * 4), s->z = (float*)p;
-  if (!rc) rc = s->alloc(&p, (size_t)batch * c.num_heads * slots * 4), s->scores = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.latent_dim, 1) * 4), s->in = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;

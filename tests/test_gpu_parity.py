@@ -53,6 +53,42 @@ def test_q8_0_quantize_and_dequantize_bit_exact():
         assert np.array_equal(f32.view(np.uint32), oracle.dequantize_q8_0(ob, w.shape[1]).view(np.uint32)), name
 
 
+def test_f16_widening_exhaustive():
+    """Every binary16 bit pattern through the GPU's f16 -> f32 upload equals numpy's exact
+    widening (NaNs stay NaN)."""
+    s = W.S1_SMALL
+    t = W.make_weights(s, "f32", seed=21)
+    name = "transformer.layers.0.gating.linear_in.weight"
+    shape = t[name][1]
+    n = shape[0] * shape[1]
+    assert n >= 65536
+    bits = (np.arange(n) % 65536).astype(np.uint16).reshape(shape)
+    t[name] = (W.F16, shape, bits)
+    g = svl.Model(s.config(0), t)
+    got, _ = g.linear_weight("0.ff1")
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_q8_0_quantize_scales_across_the_f16_range():
+    """Block maxima from 1e-9 to 4e6: scales d = amax / 127 cover f16 subnormals, normals and
+    overflow; the GPU's blocks equal the oracle's."""
+    s = W.S1_SMALL
+    t = W.make_weights(s, "q8_0", seed=22)
+    name = "transformer.layers.1.gating.linear_in.weight"
+    shape = t[name][1]
+    rng = np.random.default_rng(23)
+    w = rng.standard_normal(shape).astype(np.float32)
+    blocks = w.reshape(-1, 32)
+    blocks *= (10.0 ** rng.uniform(-9, 6.6, size=(blocks.shape[0], 1))).astype(np.float32)
+    t[name] = (W.F32, shape, blocks.reshape(shape))
+    g = svl.Model(s.config(W.Q8_0), t)
+    _, got = g.linear_weight("1.ff1")
+    assert np.array_equal(got, oracle.quantize_q8_0(t[name][2]))
+
+
 def test_q8_0_candle_blocks_round_trip():
     s = W.S1_SMALL
     t = W.make_weights(s, "q8_0", seed=2)
