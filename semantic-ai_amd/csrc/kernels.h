@@ -73,6 +73,8 @@ struct EmbedArgs {
   int initial_at_zero;      // a stream at position 0 sees `card` audio tokens
   int* pos;
   float* x;                 // [B][d]
+  void* stage;              // [B][n_q][d] table rows of the next step's audio tokens, gathered
+                            // during the previous step (table element type), or null
 };
 
 struct ArgmaxArgs {

@@ -810,9 +810,11 @@ __device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const
 
 // SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
 // ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 512.
-// The stream's tokens are staged in LDS first, then every table row is requested at once.
+// The stream's tokens are staged in LDS first, then every table row is requested at once.  When
+// `staged`, the audio rows are read from the copies gathered during the previous step (random
+// table rows cost an address-translation miss each; the copies are contiguous).
 __device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit,
-                                           const int* spos, unsigned char* smem, RowSync& rs) {
+                                           const int* spos, bool staged, unsigned char* smem, RowSync& rs) {
   constexpr int G = 32;  // table rows in flight per round
   uint32_t* stok = (uint32_t*)smem;  // [0]: text token, [1 + c]: token of codebook c
   const int chunks = (a.d + kRowThreads - 1) / kRowThreads;
@@ -837,19 +839,36 @@ __device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* t
   float x = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.text_emb + (size_t)t * a.d + i))
                           : ldg((const float*)a.text_emb + (size_t)t * a.d + i);
   for (int c0 = 0; c0 < a.n_q; c0 += G) {
+    // every load is issued (past n_q: the last codebook's row again), so none waits for another
     float e[G];
 #pragma unroll
     for (int u = 0; u < G; ++u) {
-      if (c0 + u < a.n_q) {
-        const size_t idx = ((size_t)(c0 + u) * rows + stok[1 + c0 + u]) * a.d + i;
+      const int c = min(c0 + u, a.n_q - 1);
+      if (staged) {  // the rows were copied next to each other during the previous step
+        const size_t idx = ((size_t)b * a.n_q + c) * a.d + i;
+        e[u] = a.tables_bf16 ? bf16_to_f32(ld_co((const uint16_t*)a.stage + idx)) : ld_co((const float*)a.stage + idx);
+      } else {
+        const size_t idx = ((size_t)c * rows + stok[1 + c]) * a.d + i;
         e[u] = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.emb + idx)) : ldg((const float*)a.emb + idx);
       }
     }
 #pragma unroll
-    for (int u = 0; u < G; ++u)
-      if (c0 + u < a.n_q) x = x + e[u];
+    for (int u = 0; u < G; ++u) x = c0 + u < a.n_q ? x + e[u] : x;
   }
   st_co(a.x + (size_t)b * a.d + i, x);
+}
+
+// Copies the table rows of step `step`'s audio tokens of stream b, codebook c (unit = b * n_q + c)
+// into a.stage, for the next step's embedding.  Positions only grow within a launch, so a later
+// step never has a stream at position 0.
+__device__ __forceinline__ void gather_unit(const EmbedArgs& a, const uint32_t* audio, int unit) {
+  const int b = unit / a.n_q, c = unit % a.n_q;
+  uint32_t tok = ldg(audio + (size_t)b * a.n_q + c);
+  tok = tok > (uint32_t)a.card ? (uint32_t)a.card : tok;
+  const int words = a.d * (a.tables_bf16 ? 2 : 4) / 4;  // d is a multiple of 32
+  const uint32_t* src = (const uint32_t*)((const char*)a.emb + ((size_t)c * (a.card + 1) + tok) * (size_t)words * 4);
+  uint32_t* dst = (uint32_t*)((char*)a.stage + ((size_t)b * a.n_q + c) * (size_t)words * 4);
+  for (int i = threadIdx.x; i < words; i += kRowThreads) st_co(dst + i, ldg(src + i));
 }
 
 // argmax over logits[b] (first index of the maximum); unit = stream.
@@ -951,7 +970,8 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
   switch (ph.kind) {
     case PH_EMBED: {
       const uint32_t* text = P.text ? P.text + (size_t)step * P.text_stride : nullptr;
-      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit, spos, smem, rs);
+      const bool staged = ph.e.stage != nullptr && step > 0 && !P.text;
+      embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit, spos, staged, smem, rs);
       break;
     }
     case PH_GEMV:
@@ -974,9 +994,12 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
           break;
       }
       break;
-    case PH_ATTN:
-      attn_dispatch(ph.at, unit, spos, smem, rs);
+    case PH_ATTN: {
+      const int heads = ph.at.B * ph.at.H;
+      if (unit < heads) attn_dispatch(ph.at, unit, spos, smem, rs);
+      else if (step + 1 < P.n_steps && !P.text) gather_unit(ph.e, P.audio + (size_t)(step + 1) * P.audio_stride, unit - heads);
       break;
+    }
     case PH_ARGMAX:
       argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem, rs);
       break;

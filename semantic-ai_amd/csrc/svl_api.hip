@@ -137,6 +137,7 @@ struct svl_state {
   float* fwd = nullptr;       // transformer forward staging (input then output)
   size_t fwd_cap = 0;
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
+  void* stage = nullptr;      // STT: next step's audio embedding rows [B][n_q][d]
   uint32_t* tok_out = nullptr;
   // step programs and the grid barrier of the persistent kernel
   Program stt, tts, fwd_prog;
@@ -579,9 +580,19 @@ int build_programs(const svl_model* m, svl_state* s) {
     e.e.initial_at_zero = 1;
     e.e.pos = s->pos;
     e.e.x = s->x;
+    e.e.stage = s->stage;
     e.units = s->B * ((d + kRowThreads - 1) / kRowThreads);
     P.push_back(e);
     build_layers(m, s, P);
+    // the first attention phase (16 of 256 workgroups busy) also gathers the next step's
+    // audio embedding rows
+    for (Phase& ph : P) {
+      if (ph.kind == PH_ATTN) {
+        ph.e = e.e;
+        ph.units += s->B * c.n_q;
+        break;
+      }
+    }
     Phase t = gemv_phase(s, m->text_linear);
     t.g.x = s->x;
     t.g.x_stride = d;
@@ -705,7 +716,7 @@ int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
     HIP_TRY(launch_step_program(P, s->grid, p.smem, s->stream));
     s->gen += need;
   } else {
-    P.n_steps = 1;
+    P.n_steps = (int)n_steps;  // the units see the launch's step count (next-step gathers)
     for (int64_t step = 0; step < n_steps; ++step)
       for (int i = 0; i < P.nphase; ++i)
         HIP_TRY(launch_phase(p.dev + i, p.phases[i].units, P, (int)step, p.smem, s->stream));
@@ -771,6 +782,8 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.d_model, c.z_dim) * 4), s->z = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * std::max(c.latent_dim, 1) * 4), s->in = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
+  if (!rc && c.kind == SVL_MODEL_STT)
+    rc = s->alloc(&p, (size_t)batch * c.n_q * c.d_model * (m->tables_bf16 ? 2 : 4)), s->stage = p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, sizeof(SyncState)), s->sync = (SyncState*)p;
   if (!rc && hipMemsetAsync(s->sync, 0, sizeof(SyncState), s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
