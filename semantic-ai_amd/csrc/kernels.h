@@ -49,6 +49,9 @@ struct GemvArgs {
   int cap;
   int kv_bf16;
   int advance_pos;
+  // batched Q8_0 path (PH_QUANT / PH_QGEMM): the quantized input rows of the whole batch
+  int8_t* xq;          // [B][L.in]
+  float* xdq;          // [B][L.in / 32] (f16-rounded block scales)
 };
 
 struct AttnArgs {
@@ -105,7 +108,8 @@ struct CopyArgs {           // y[b][0..n) = x[b][0..n)
 };
 
 // One phase of a step program: a unit function applied to `units` work units.
-enum PhaseKind { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN = 2, PH_ARGMAX = 4, PH_NORM = 5, PH_COPY_IN = 6, PH_COPY_OUT = 7 };
+enum PhaseKind { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN = 2, PH_ARGMAX = 4, PH_NORM = 5, PH_COPY_IN = 6, PH_COPY_OUT = 7,
+                 PH_QUANT = 8, PH_QGEMM = 9 };
 
 struct Phase {
   int kind;
@@ -151,6 +155,9 @@ constexpr int kStepThreads = 1024;                       // workgroup of the ste
 constexpr int kRowThreads = 512;                         // row waves: threads [0, 512)
 constexpr int kWeightThreads = kStepThreads - kRowThreads;  // weight waves: threads [512, 1024)
 constexpr int kWBlocks = 6;                              // Q8_0 blocks per weight-wave thread and unit
+constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8_0 linears as MFMA GEMMs
+constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit
+constexpr int kTileBatch = 64;   // batch rows of a GEMM unit
 constexpr int kMaxBatch = 1024;
 
 hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s);
@@ -159,6 +166,8 @@ int step_program_grid(int device);
 size_t phase_smem(const Phase& ph);
 // Fills the unit layout of a GEMV phase (ipw, parts, maxb, units) for `grid` workgroups.
 void plan_gemv(GemvArgs& g, int grid, int* units);
+// Unit layout of a batched Q8_0 GEMM phase (units = row tiles x batch tiles; parts = row tiles).
+void plan_qgemm(GemvArgs& g, int* units);
 
 hipError_t launch_q8_quantize(const float* w, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_from_blocks(const uint8_t* blocks, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);

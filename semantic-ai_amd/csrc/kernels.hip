@@ -181,6 +181,15 @@ void plan_gemv(GemvArgs& g, int grid, int* units) {
   *units = g.parts * g.B;
 }
 
+void plan_qgemm(GemvArgs& g, int* units) {
+  const bool silu = g.epi == EPI_SILU_GATE;
+  const int items = silu ? g.ff_hidden : g.L.out;
+  g.ipw = silu ? kTileRows / 2 : kTileRows;
+  g.parts = (items + g.ipw - 1) / g.ipw;
+  g.maxb = 0;
+  *units = g.parts * ((g.B + kTileBatch - 1) / kTileBatch);
+}
+
 size_t phase_smem(const Phase& ph) {
   switch (ph.kind) {
     case PH_GEMV: {
@@ -200,6 +209,12 @@ size_t phase_smem(const Phase& ph) {
       return (size_t)ph.nm.d * 4 + 64;
     case PH_EMBED:
       return (size_t)(ph.e.n_q + 1) * 4 + 64;
+    case PH_QUANT: {
+      const int K = ph.g.L.in, nb4 = (K / 32 + 3) & ~3;
+      return (size_t)K * 4 + K + (size_t)nb4 * 4 + 64;
+    }
+    case PH_QGEMM:
+      return (size_t)kTileRows * kTileBatch * 4 + 64;
     default:
       return 64;
   }

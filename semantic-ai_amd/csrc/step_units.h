@@ -627,6 +627,112 @@ __device__ __forceinline__ bool is_q8_gemv(const Phase* ph) {
   return ld_const(&ph->kind) == PH_GEMV && ld_const(&ph->g.L.fmt) == FMT_Q8_0;
 }
 
+// ---- batched Q8_0 GEMM (lockstep batches; row waves) ----------------------------------------------
+// The same arithmetic as the Q8_0 GEMV, with the int8 block dots of a tile of 32 output rows x 64
+// batch rows done by v_mfma_i32_16x16x32_i8 (one instruction per 16 x 16 sub-tile and block:
+// K = 32 is exactly one block).  Per block and output, ((f32)dot * d_w) * d_x is added to the
+// output's sum in block order, as in the GEMV.  The activations are quantized once per batch
+// row by a PH_QUANT phase before the GEMM phase.
+//
+// Operand layouts of v_mfma_i32_16x16x32_i8 (one 64-lane wave): lane l supplies row l % 16 of A
+// (and column l % 16 of B) at k = 8 (l / 16) .. 8 (l / 16) + 7 as 8 packed int8; it receives
+// D[4 (l / 16) + i][l % 16], i = 0 .. 3.
+
+// Quantizes x[b] (after the norm, if any) into xq[b] / xdq[b]; unit = batch row.
+template <int KP>
+__device__ __forceinline__ void quant_unit(const GemvArgs& a, int b, unsigned char* smem, RowSync& rs) {
+  const int K = a.L.in, nb = K / 32;
+  float* xs = (float*)smem;
+  int8_t* xq = (int8_t*)(xs + K);
+  float* xdq = (float*)(xq + K);
+  constexpr bool kNorm = KP <= 8;
+  NormW<kNorm ? KP : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
+  float v[KP];
+  load_row(a.x + (size_t)b * a.x_stride, K, v);
+  if constexpr (kNorm) {
+    if (a.norm != NORM_NONE) norm_regs(v, K, a.norm, nwt, a.eps, xs, rs);
+  }
+  quantize_regs(v, K, xq, xdq);
+  rs.sync();
+  uint32_t* dq = (uint32_t*)(a.xq + (size_t)b * K);
+  for (int i = threadIdx.x; i < K / 4; i += kRowThreads) st_co(dq + i, ((const uint32_t*)xq)[i]);
+  for (int i = threadIdx.x; i < nb; i += kRowThreads) st_co(a.xdq + (size_t)b * nb + i, xdq[i]);
+}
+
+typedef long v_i8x8;
+
+// One GEMM unit: output rows of row tile `part`, batch rows of batch tile `bt`.  Wave w computes
+// the 16 x 16 sub-tile of tile rows 16 (w / 4) .. and batch rows 16 (w % 4) ..; the results meet
+// in LDS for the epilogues.
+__device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
+                                           RowSync& rs) {
+  const int K = a.L.in, nb = K / 32;
+  const bool silu = a.epi == EPI_SILU_GATE;
+  const int part = unit % a.parts, bt = unit / a.parts;
+  const int i0 = part * a.ipw;
+  const int ni = min(a.ipw, gemv_items(a) - i0);
+  const int NR = silu ? 2 * ni : ni;  // tile rows in use
+  const int b0 = bt * kTileBatch;
+  const int nbat = min(kTileBatch, a.B - b0);
+  float* Y = (float*)smem;            // [kTileRows][kTileBatch]
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int r0 = 16 * (wave / 4), c0 = 16 * (wave % 4);
+  // this lane's A row and B column (clamped to valid rows; their results are not used)
+  const int ar = min(r0 + lane % 16, NR - 1), bc = min(c0 + lane % 16, nbat - 1);
+  const size_t arow = (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, ar);
+  const int kq = 8 * (lane / 16);
+  const int8_t* wa = (const int8_t*)a.L.w + arow * K + kq;
+  const int8_t* xb = a.xq + (size_t)(b0 + bc) * K + kq;
+  // D rows of this lane: r0 + 4 (lane / 16) + i; their weight scales and the column's x scales
+  size_t drow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    drow[i] = (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(r0 + 4 * (lane / 16) + i, NR - 1));
+  const float* dxp = a.xdq + (size_t)(b0 + bc) * nb;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int CH = 8;  // blocks per round of loads
+  for (int k0 = 0; k0 < nb; k0 += CH) {
+    v_i8x8 av[CH], bv[CH];
+    float dw[CH][4], dx[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int k = min(k0 + u, nb - 1);
+      av[u] = ldg_stream((const v_i8x8*)(wa + (size_t)k * 32));
+      bv[u] = ld_co((const v_i8x8*)(xb + (size_t)k * 32));
+      dx[u] = ld_co(dxp + k);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dw[u][i] = f16_to_f32(ldg(a.L.scale + drow[i] * nb + k));
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      if (k0 + u >= nb) break;  // uniform
+      v4i c = {0, 0, 0, 0};
+      c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u], c, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float t = (float)c[i] * dw[u][i];
+        acc[i] = acc[i] + t * dx[u];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) Y[(r0 + 4 * (lane / 16) + i) * kTileBatch + c0 + lane % 16] = acc[i];
+  rs.sync();
+  // epilogues: item t of the tile for batch row b0 + j
+  for (int e = threadIdx.x; e < ni * nbat; e += kRowThreads) {
+    const int t = e % ni, j = e / ni;
+    const int b = b0 + j, row = i0 + t, p = spos[b];
+    const float y = Y[t * kTileBatch + j];
+    const float yp = a.epi == EPI_QKV_ROPE ? Y[(t ^ 1) * kTileBatch + j] : 0.0f;
+    const float yv = silu ? Y[(ni + t) * kTileBatch + j] : 0.0f;
+    const EpiIn in = gemv_epi_prefetch(a, b, row, p);
+    gemv_epilogue(a, b, row, p, in, y, yp, yv);
+  }
+  if (a.advance_pos && part == 0)
+    for (int j = threadIdx.x; j < nbat; j += kRowThreads) st_co(a.pos + b0 + j, spos[b0 + j] + 1);
+}
+
 // ---- dense GEMV unit (row waves) -----------------------------------------------------------------
 // The reference's matvec (SVL/nn/kernels/matvec.rs:239-246) with its 16-lane dot
 // (kernels/mod.rs:66-91): 16 threads per row, thread i accumulating x[16c + i] * w[16c + i]
@@ -1000,6 +1106,17 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       else if (step + 1 < P.n_steps && !P.text) gather_unit(ph.e, P.audio + (size_t)(step + 1) * P.audio_stride, unit - heads);
       break;
     }
+    case PH_QUANT:
+      switch (row_slots(ph.g.L.in)) {
+        case 2: quant_unit<2>(ph.g, unit, smem, rs); break;
+        case 4: quant_unit<4>(ph.g, unit, smem, rs); break;
+        case 8: quant_unit<8>(ph.g, unit, smem, rs); break;
+        default: quant_unit<kMaxSlots>(ph.g, unit, smem, rs); break;
+      }
+      break;
+    case PH_QGEMM:
+      qgemm_unit(ph.g, unit, spos, smem, rs);
+      break;
     case PH_ARGMAX:
       argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem, rs);
       break;

@@ -138,6 +138,8 @@ struct svl_state {
   size_t fwd_cap = 0;
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
   void* stage = nullptr;      // STT: next step's audio embedding rows [B][n_q][d]
+  int8_t* xqb = nullptr;      // batched Q8_0 path: quantized input rows [B][width]
+  float* xdqb = nullptr;      //                    and their block scales [B][width / 32]
   uint32_t* tok_out = nullptr;
   // step programs and the grid barrier of the persistent kernel
   Program stt, tts, fwd_prog;
@@ -441,7 +443,22 @@ Phase gemv_phase(const svl_state* s, const LinearDev& L) {
   return ph;
 }
 
+// A Q8_0 linear of a lockstep batch of at least kBatchMfma streams runs as two phases: the
+// input rows are normalized and quantized once (PH_QUANT, one unit per stream), then an MFMA
+// GEMM reads every weight block once per 64 streams (PH_QGEMM).  Otherwise one GEMV phase.
 void add_gemv(const svl_state* s, std::vector<Phase>& out, Phase ph) {
+  if (ph.g.L.fmt == FMT_Q8_0 && s->B >= kBatchMfma) {
+    ph.g.xq = s->xqb;
+    ph.g.xdq = s->xdqb;
+    Phase q = ph;
+    q.kind = PH_QUANT;
+    q.units = s->B;
+    out.push_back(q);
+    ph.kind = PH_QGEMM;
+    plan_qgemm(ph.g, &ph.units);
+    out.push_back(ph);
+    return;
+  }
   plan_gemv(ph.g, s->grid, &ph.units);
   out.push_back(ph);
 }
@@ -550,7 +567,7 @@ int upload_program(svl_state* s, Program& p) {
 int refresh_rope(svl_state* s, Program& p, const float* rope) {
   bool changed = false;
   for (Phase& ph : p.phases)
-    if (ph.kind == PH_GEMV && ph.g.epi == EPI_QKV_ROPE && ph.g.rope != rope) {
+    if ((ph.kind == PH_GEMV || ph.kind == PH_QGEMM) && ph.g.epi == EPI_QKV_ROPE && ph.g.rope != rope) {
       ph.g.rope = rope;
       changed = true;
     }
@@ -784,6 +801,11 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
   if (!rc && c.kind == SVL_MODEL_STT)
     rc = s->alloc(&p, (size_t)batch * c.n_q * c.d_model * (m->tables_bf16 ? 2 : 4)), s->stage = p;
+  if (!rc && batch >= kBatchMfma) {
+    const int wmax = std::max(std::max(c.d_model, c.num_heads * c.head_dim), c.ff_hidden);
+    rc = s->alloc(&p, (size_t)batch * wmax), s->xqb = (int8_t*)p;
+    if (!rc) rc = s->alloc(&p, (size_t)batch * (wmax / 32) * 4), s->xdqb = (float*)p;
+  }
   if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, sizeof(SyncState)), s->sync = (SyncState*)p;
   if (!rc && hipMemsetAsync(s->sync, 0, sizeof(SyncState), s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");

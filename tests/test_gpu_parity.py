@@ -147,6 +147,34 @@ def test_lockstep_batch_equals_independent_streams():
         assert np.array_equal(g.recognize(audio[b][:, None, :], one)[:, 0], batched[:, b]), b
 
 
+def test_mfma_batch_equals_independent_streams():
+    """A lockstep batch large enough for the MFMA GEMM path (20 streams at different positions):
+    logits and tokens bit-identical to each stream stepped alone through the GEMV path."""
+    s = W.S1_SMALL
+    _, g, _ = build(s, "q8_0", seed=24)
+    B, n = 20, 10
+    audio = W.audio_tokens(s, n, seed=25, batch=B)
+    st = g.init_state(batch=B)
+    caches = []
+    for b in range(B):
+        ks, vs = W.prefill_caches(s, (7 * b) % 30, seed=40 + b)
+        caches.append((ks, vs))
+        st.load_stream(b, ks, vs)
+    singles = []
+    for b in range(B):
+        one = g.init_state()
+        one.load_stream(0, *caches[b])
+        singles.append(one)
+    text = np.full(B, s.text_card, dtype=np.uint32)
+    for i in range(n):
+        tb, lb = g.step(text, audio[:, i], st, want_logits=True)
+        for b in range(B):
+            t1, l1 = g.step([text[b]], audio[b, i][None], singles[b], want_logits=True)
+            assert np.array_equal(lb[b].view(np.uint32), l1[0].view(np.uint32)), (i, b)
+            assert tb[b] == t1[0]
+        text = tb.astype(np.uint32)
+
+
 def test_state_duplicate_reset_and_caches():
     s = W.S1_SMALL
     _, g, o = build(s, "f32", seed=9)
