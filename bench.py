@@ -11,6 +11,8 @@ Other workloads (one JSON line each, same fields):
   stt1b-q8-b64   64 lockstep streams, each ring pre-filled to a seeded fill in [1, 750], 128
                  steps; linears run as int8 MFMA GEMMs; a step advances all 64 streams.
   stt1b-bf16-b1  the default workload with bf16 linears (dense 16-lane-dot GEMV), 256 steps.
+  stt2.6b-q4k-b1 STT-2.6B shape (24 layers, d_model 2560, 20 heads x 128, gated SiLU 6912, window
+                 3000) with every linear in candle Q4K (activations quantized to Q8K), 256 steps.
   tts-f32-b1     Pocket-TTS backbone (6 layers, d 1024, 16 x 64, GELU 4096, LayerNorm), f32,
                  256 prefilled positions, 128 steps of seeded N(0, 1) latents; one call per step
                  (the reference returns to the host every frame).
@@ -40,7 +42,7 @@ for p in (ROOT, PKG):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ["stt1b-q8-b1", "stt1b-q8-b64", "stt1b-bf16-b1", "tts-f32-b1"]
+WORKLOADS = ["stt1b-q8-b1", "stt1b-q8-b64", "stt1b-bf16-b1", "stt2.6b-q4k-b1", "tts-f32-b1"]
 
 
 def traffic_file(workload):
@@ -134,8 +136,8 @@ def bench_stt(args, wl, steps, warmup):
     from svl import hip
     from svl import workloads as W
 
-    shape = W.S1
-    dtype = "bf16" if wl == "stt1b-bf16-b1" else "q8_0"
+    shape = W.S2 if wl == "stt2.6b-q4k-b1" else W.S1
+    dtype = {"stt1b-bf16-b1": "bf16", "stt2.6b-q4k-b1": "q4k"}.get(wl, "q8_0")
     B = 64 if wl == "stt1b-q8-b64" else 1
     t0 = time.perf_counter()
     tensors = W.make_weights(shape, dtype, seed=0)
@@ -162,6 +164,7 @@ def bench_stt(args, wl, steps, warmup):
     achieved = bytes_launch / (gpu_ms / 1e3) / 1e9
     name = {"stt1b-q8-b1": "stt-1b q8_0 greedy decode, batch 1, from position 0",
             "stt1b-bf16-b1": "stt-1b bf16 greedy decode, batch 1, from position 0",
+            "stt2.6b-q4k-b1": "stt-2.6b q4k greedy decode, batch 1, from position 0",
             "stt1b-q8-b64": "stt-1b q8_0 greedy decode, 64 lockstep streams, rings pre-filled to U[1, 750]"}[wl]
     config = {"workload": name, "layers": shape.num_layers, "d_model": shape.d_model, "heads": shape.num_heads,
               "head_dim": shape.head_dim, "ff_hidden": shape.ff_hidden, "window": shape.context,
@@ -170,8 +173,9 @@ def bench_stt(args, wl, steps, warmup):
     if B > 1:
         config["tokens_per_s"] = round(steps * B / (gpu_ms / 1e3), 1)
         config["mean_fill"] = round(float(np.mean(fills)), 1)
-    dt = ("q8_0 (int8 x int8 -> int32 block dots, f32 scales and sums)" if dtype == "q8_0"
-          else "bf16 weights, f32 arithmetic (16-lane FMA dot)")
+    dt = {"q8_0": "q8_0 (int8 x int8 -> int32 block dots, f32 scales and sums)",
+          "q4k": "q4k x q8k (4-bit x int8 -> int32 sub-block dots, f32 scales and lane sums)",
+          "bf16": "bf16 weights, f32 arithmetic (16-lane FMA dot)"}[dtype]
     line = base_line(steps / (gpu_ms / 1e3), steps, warmup, gpu_ms / steps, dt,
                      "synthetic (seeded N(0, 0.02) weights, uniform audio ids, greedy text feedback)", config)
     line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -273,7 +277,7 @@ def main():
     ap.add_argument("--workload", choices=WORKLOADS, default=WORKLOADS[0])
     ap.add_argument("--steps", type=int, default=0, help="timed steps (default 256; 128 for b64 and tts)")
     ap.add_argument("--warmup", type=int, default=-1, help="warm-up steps (default: as many as timed)")
-    ap.add_argument("--cpu-steps", type=int, default=64)
+    ap.add_argument("--cpu-steps", type=int, default=0, help="oracle steps (default 64; 16 for q4k)")
     ap.add_argument("--cpu-threads", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
@@ -286,6 +290,7 @@ def main():
         calibrate_copy(args.calibrate_copy)
         return
     wl = args.workload
+    args.cpu_steps = args.cpu_steps or (16 if wl == "stt2.6b-q4k-b1" else 64)
     steps = args.steps or (128 if wl in ("stt1b-q8-b64", "tts-f32-b1") else 256)
     warmup = steps if args.warmup < 0 else args.warmup
     line = bench_tts(args, steps, warmup) if wl == "tts-f32-b1" else bench_stt(args, wl, steps, warmup)

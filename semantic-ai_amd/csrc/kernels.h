@@ -13,6 +13,11 @@ enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 
 // One linear layer as held on the device.
 //   FMT_F32 / FMT_BF16: w = [out][in] row-major.
 //   FMT_Q8_0: w = int8 quants [out][in]; scale = f16 block scales [out][in/32].
+//   FMT_Q4K: w = 144-byte super-blocks [out][in/256]: f16 d, f16 dmin and the 12 bytes of packed
+//     6-bit sub-block scales and mins exactly as candle's BlockQ4K holds them, then the 128 quant
+//     bytes with each 32-byte group lane-grouped: byte 4 l + g of a group is candle's byte
+//     8 g + l of it, so that one dword holds the four values that i32 lane l of the vec_dot
+//     adds for the group's two sub-blocks (low and high nibbles).
 struct LinearDev {
   int fmt = FMT_F32;
   int out = 0, in = 0;
@@ -25,7 +30,8 @@ struct GemvArgs {
   int B;               // batch rows
   int ipw;             // work items per unit (rows, or gate/value pairs for the SiLU gate)
   int parts;           // units per batch row = ceil(items / ipw)
-  int maxb;            // Q8_0: weight blocks per weight-wave thread and unit (1 .. kWBlocks)
+  int maxb;            // Q8_0 / Q4K: weight blocks per weight-wave thread and unit
+                       // (1 .. kWBlocks, Q4K 1 .. kQ4Blocks)
   const float* x;      // input [B][x_stride]
   int x_stride;
   int norm;            // NormKind applied to x in the prologue
@@ -155,12 +161,24 @@ constexpr int kStepThreads = 1024;                       // workgroup of the ste
 constexpr int kRowThreads = 512;                         // row waves: threads [0, 512)
 constexpr int kWeightThreads = kStepThreads - kRowThreads;  // weight waves: threads [512, 1024)
 constexpr int kWBlocks = 6;                              // Q8_0 blocks per weight-wave thread and unit
+constexpr int kQ4Blocks = 2;                             // Q4K super-blocks per weight-wave thread and unit
+constexpr int kQ4Terms = 9;   // f32 terms per Q4K super-block and row: 8 lane sums and the min term
 constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8_0 linears as MFMA GEMMs
 constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit
 constexpr int kTileBatch = 64;   // batch rows of a GEMM unit
 constexpr int kMaxBatch = 1024;
 
-hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s);
+// Unit families of a step program.  The persistent kernel is compiled for a few family sets, so
+// that a program is run by a kernel holding only the registers of the units it has.
+enum UnitFamily : unsigned {
+  FAM_Q8 = 1,     // Q8_0 GEMV (row waves + weight waves)
+  FAM_Q4K = 2,    // Q4K GEMV (row waves + weight waves)
+  FAM_DENSE = 4,  // f32 / bf16 GEMV
+  FAM_BATCH = 8,  // batched Q8_0: activation quantization + MFMA GEMM
+  FAM_ALL = 15,
+};
+unsigned program_families(const Phase* phases, int n);
+hipError_t launch_step_program(const StepParams& p, unsigned families, int grid, size_t smem, hipStream_t s);
 hipError_t launch_phase(const Phase* d_ph, int units, const StepParams& p, int step, size_t smem, hipStream_t s);
 int step_program_grid(int device);
 size_t phase_smem(const Phase& ph);
@@ -172,6 +190,9 @@ void plan_qgemm(GemvArgs& g, int* units);
 hipError_t launch_q8_quantize(const float* w, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_from_blocks(const uint8_t* blocks, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_to_blocks(const int8_t* qs, const uint16_t* d, int rows, int K, uint8_t* blocks, hipStream_t s);
+hipError_t launch_q4k_quantize(const float* w, int rows, int K, uint8_t* blocks, hipStream_t s);
+hipError_t launch_q4k_from_blocks(const uint8_t* candle, int rows, int K, uint8_t* blocks, hipStream_t s);
+hipError_t launch_q4k_to_blocks(const uint8_t* blocks, int rows, int K, uint8_t* candle, hipStream_t s);
 hipError_t launch_dequant(const LinearDev& L, float* out, hipStream_t s);
 hipError_t launch_f16_to_f32(const uint16_t* x, float* y, size_t n, hipStream_t s);
 hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, size_t n, hipStream_t s);

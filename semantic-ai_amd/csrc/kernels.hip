@@ -89,13 +89,14 @@ __device__ __forceinline__ void init_wg_sync(WgSync* ws) {
   __syncthreads();  // the only full-workgroup barrier: nothing is in flight yet
 }
 
+template <unsigned F>
 __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int spos[kMaxBatch];
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) {
-    weight_waves(P, &ws, smem);
+    if constexpr ((F & (FAM_Q8 | FAM_Q4K)) != 0) weight_waves<F>(P, &ws, smem);
     return;
   }
   RowSync rs{&ws, 0u};
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
     rs.sync();
     for (int p = 0; p < P.nphase; ++p) {
       const Phase& ph = phase_at(P.prog, p);
-      for (int u = blockIdx.x; u < ph.units; u += gridDim.x) run_unit(ph, P, step, u, spos, smem, rs, item);
+      for (int u = blockIdx.x; u < ph.units; u += gridDim.x) run_unit<F>(ph, P, step, u, spos, smem, rs, item);
       ++gen;
       if (!grid_barrier(P.sync, gen, gen - P.gen0, &ws)) return;
     }
@@ -119,12 +120,19 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, 
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) {
-    if (is_q8_gemv(d_ph)) {
-      WItem it;
+    if (is_split_gemv(d_ph)) {
       if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
-      w_issue(d_ph, blockIdx.x, it);
-      if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
-      w_terms(it, smem);
+      if (ld_const(&d_ph->g.L.fmt) == FMT_Q4K) {
+        WItemQ4 it;
+        w_issue_q4k(d_ph, blockIdx.x, it);
+        if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+        w_terms_q4k(it, smem);
+      } else {
+        WItem it;
+        w_issue(d_ph, blockIdx.x, it);
+        if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+        w_terms(it, smem);
+      }
       lds_signal(&ws.t_parts);
     }
     return;
@@ -133,14 +141,29 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, 
   load_positions(P, spos);
   rs.sync();
   unsigned item = 0;
-  run_unit(phase_at(d_ph, 0), P, step, blockIdx.x, spos, smem, rs, item);
+  run_unit<FAM_ALL>(phase_at(d_ph, 0), P, step, blockIdx.x, spos, smem, rs, item);
 }
 
-hipError_t launch_step_program(const StepParams& p, int grid, size_t smem, hipStream_t s) {
+unsigned program_families(const Phase* phases, int n) {
+  unsigned f = 0;
+  for (int i = 0; i < n; ++i) {
+    const Phase& ph = phases[i];
+    if (ph.kind == PH_GEMV) f |= ph.g.L.fmt == FMT_Q8_0 ? FAM_Q8 : (ph.g.L.fmt == FMT_Q4K ? FAM_Q4K : FAM_DENSE);
+    if (ph.kind == PH_QUANT || ph.kind == PH_QGEMM) f |= FAM_BATCH;
+  }
+  return f;
+}
+
+hipError_t launch_step_program(const StepParams& p, unsigned families, int grid, size_t smem, hipStream_t s) {
   StepParams args = p;
   void* kargs[] = {&args};
-  return hipLaunchCooperativeKernel((const void*)step_program_kernel, dim3(grid), dim3(kStepThreads), kargs,
-                                    (unsigned)smem, s);
+  const void* k;
+  if ((families & ~(unsigned)FAM_Q8) == 0) k = (const void*)step_program_kernel<FAM_Q8>;
+  else if ((families & ~(unsigned)(FAM_Q8 | FAM_BATCH)) == 0) k = (const void*)step_program_kernel<FAM_Q8 | FAM_BATCH>;
+  else if ((families & ~(unsigned)FAM_Q4K) == 0) k = (const void*)step_program_kernel<FAM_Q4K>;
+  else if ((families & ~(unsigned)FAM_DENSE) == 0) k = (const void*)step_program_kernel<FAM_DENSE>;
+  else k = (const void*)step_program_kernel<FAM_ALL>;
+  return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kStepThreads), kargs, (unsigned)smem, s);
 }
 
 hipError_t launch_phase(const Phase* d_ph, int units, const StepParams& p, int step, size_t smem, hipStream_t s) {
@@ -173,6 +196,18 @@ void plan_gemv(GemvArgs& g, int grid, int* units) {
     g.ipw = ipw;
     g.maxb = (per_row * ipw * nb + kWeightThreads - 1) / kWeightThreads;
     if (g.maxb > kWBlocks) g.maxb = kWBlocks;
+  } else if (g.L.fmt == FMT_Q4K) {
+    // The same with 256-value super-blocks, at most kQ4Blocks of them per weight-wave thread.
+    const int nb = g.L.in / 256;
+    int ipw = (items + grid - 1) / grid;
+    if (g.epi == EPI_QKV_ROPE && (ipw & 1)) ++ipw;
+    const int per_row = silu ? 2 : 1;
+    if (ipw > kRowThreads / per_row) ipw = kRowThreads / per_row;
+    while (ipw > 1 && per_row * ipw * nb > kQ4Blocks * kWeightThreads) ipw = (g.epi == EPI_QKV_ROPE) ? ((ipw / 2 + 1) & ~1) : ipw / 2;
+    if (g.epi == EPI_QKV_ROPE && ipw < 2) ipw = 2;
+    g.ipw = ipw;
+    g.maxb = (per_row * ipw * nb + kWeightThreads - 1) / kWeightThreads;
+    if (g.maxb > kQ4Blocks) g.maxb = kQ4Blocks;
   } else {
     g.ipw = silu ? kRowThreads / 32 : kRowThreads / 16;
     g.maxb = 0;
@@ -198,6 +233,11 @@ size_t phase_smem(const Phase& ph) {
       if (g.L.fmt == FMT_Q8_0) {
         const int nb = K / 32, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
         return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)nb * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
+      }
+      if (g.L.fmt == FMT_Q4K) {
+        const int nb = K / 256, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
+        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
+               (size_t)nb * kQ4Terms * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
       return (size_t)K * 4 + (kRowThreads / 16) * 4 + 64;
     }
@@ -272,12 +312,194 @@ hipError_t launch_q8_to_blocks(const int8_t* qs, const uint16_t* d, int rows, in
   return hipGetLastError();
 }
 
-// Dequantization: Q8_0 closed form q * f32(d); dense bf16 widening; f32 copy.
+// ---- Q4K ----------------------------------------------------------------------------------------
+// Device layout: candle's 144-byte BlockQ4K with the quant bytes of each 32-byte group
+// lane-grouped (device byte 4 l + g = candle byte 8 g + l; see q4k_lane_pos).
+
+__device__ __forceinline__ int32_t sat_i32(float v) {
+  if (v != v) return 0;
+  if (v >= 2147483647.0f) return 2147483647;
+  if (v <= -2147483648.0f) return (-2147483647 - 1);
+  return (int32_t)v;
+}
+__device__ __forceinline__ int32_t nearest_int(float v) { return sat_i32(roundf(v)); }
+// f32::max / f32::min (a NaN operand yields the other one).
+__device__ __forceinline__ float rmax(float a, float b) { return a != a ? b : (b != b ? a : (a > b ? a : b)); }
+__device__ __forceinline__ float rmin(float a, float b) { return a != a ? b : (b != b ? a : (a < b ? a : b)); }
+// a < b under f32::total_cmp (-0.0 orders before +0.0).
+__device__ __forceinline__ bool total_lt(float a, float b) {
+  int32_t ia = __float_as_int(a), ib = __float_as_int(b);
+  ia ^= (int32_t)(((uint32_t)(ia >> 31)) >> 1);
+  ib ^= (int32_t)(((uint32_t)(ib >> 31)) >> 1);
+  return ia < ib;
+}
+
+// GGML get_scale_min_k4: the 6-bit scale and min of sub-block j from the 12 packed bytes.
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, int& m) {
+  if (j < 4) {
+    d = q[j] & 63;
+    m = q[j + 4] & 63;
+  } else {
+    d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+// make_qkx1_quants(nmax = 15, ntry = 5) of 32 values: iterative least-squares fit of a scale
+// and a (non-positive) offset; returns scale and -offset.
+__device__ void qkx1_fit(const float* x, float& scale_out, float& min_out) {
+  constexpr int n = 32, nmax = 15, ntry = 5;
+  uint8_t L[n];
+  for (int i = 0; i < n; ++i) L[i] = 0;
+  float mn = x[0], mx = x[0];
+  for (int i = 1; i < n; ++i)
+    if (total_lt(x[i], mn)) mn = x[i];  // first minimum
+  for (int i = 1; i < n; ++i)
+    if (!total_lt(x[i], mx)) mx = x[i];  // last maximum
+  if (mx == mn) {
+    scale_out = 0.0f;
+    min_out = 0.0f;
+    return;
+  }
+  mn = rmin(mn, 0.0f);
+  float iscale = (float)nmax / (mx - mn);
+  float scale = 1.0f / iscale;
+  for (int itry = 0; itry < ntry; ++itry) {
+    float sumlx = 0.0f;
+    int32_t suml2 = 0;
+    bool changed = false;
+    for (int i = 0; i < n; ++i) {
+      int32_t li = nearest_int(iscale * (x[i] - mn));
+      li = li < 0 ? 0 : (li > nmax ? nmax : li);
+      if ((uint8_t)li != L[i]) {
+        L[i] = (uint8_t)li;
+        changed = true;
+      }
+      sumlx += (x[i] - mn) * (float)li;
+      suml2 += li * li;
+    }
+    scale = sumlx / (float)suml2;
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) sum += x[i] - scale * (float)L[i];
+    mn = sum / (float)n;
+    if (mn > 0.0f) mn = 0.0f;
+    iscale = 1.0f / scale;
+    if (!changed) break;
+  }
+  scale_out = scale;
+  min_out = -mn;
+}
+
+// candle BlockQ4K::from_float on the GPU: one thread per 256-value super-block.
+__global__ void q4k_quantize_kernel(const float* w, size_t nblocks, uint8_t* out) {
+  const size_t blk = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (blk >= nblocks) return;
+  const float* xb = w + blk * 256;
+  uint8_t* b = out + blk * 144;
+  float mins[8], scales[8];
+  for (int j = 0; j < 8; ++j) qkx1_fit(xb + 32 * j, scales[j], mins[j]);
+  float max_scale = 0.0f, max_min = 0.0f;
+  for (int j = 0; j < 8; ++j) max_scale = rmax(scales[j], max_scale);
+  for (int j = 0; j < 8; ++j) max_min = rmax(mins[j], max_min);
+  const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+  const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+  uint8_t sc[12];
+  for (int j = 0; j < 12; ++j) sc[j] = 0;
+  for (int j = 0; j < 8; ++j) {
+    const int32_t lsi = nearest_int(inv_scale * scales[j]);
+    const int32_t lmi = nearest_int(inv_min * mins[j]);
+    const uint8_t ls = (uint8_t)(lsi < 63 ? lsi : 63);
+    const uint8_t lm = (uint8_t)(lmi < 63 ? lmi : 63);
+    if (j < 4) {
+      sc[j] = ls;
+      sc[j + 4] = lm;
+    } else {
+      sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+      sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+      sc[j] |= (uint8_t)((lm >> 4) << 6);
+    }
+  }
+  const uint16_t dh = f32_to_f16(max_scale / 63.0f), mh = f32_to_f16(max_min / 63.0f);
+  b[0] = (uint8_t)(dh & 0xFF);
+  b[1] = (uint8_t)(dh >> 8);
+  b[2] = (uint8_t)(mh & 0xFF);
+  b[3] = (uint8_t)(mh >> 8);
+  for (int j = 0; j < 12; ++j) b[4 + j] = sc[j];
+  const float dd = f16_to_f32(dh), dmin = f16_to_f32(mh);
+  uint8_t L[256];
+  for (int i = 0; i < 256; ++i) L[i] = 0;
+  for (int j = 0; j < 8; ++j) {
+    int s, m;
+    scale_min_k4(j, sc, s, m);
+    const float d = dd * (float)s;
+    if (d != 0.0f) {
+      const float dm = dmin * (float)m;
+      for (int ii = 0; ii < 32; ++ii) {
+        int32_t l = nearest_int((xb[32 * j + ii] + dm) / d);
+        L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
+      }
+    }
+  }
+  // candle byte 32 g + e of group g holds L[64 g + e] | L[64 g + 32 + e] << 4
+  for (int g = 0; g < 4; ++g)
+    for (int e = 0; e < 32; ++e)
+      b[16 + 32 * g + q4k_lane_pos(e)] = (uint8_t)(L[64 * g + e] | (L[64 * g + 32 + e] << 4));
+}
+
+hipError_t launch_q4k_quantize(const float* w, int rows, int K, uint8_t* blocks, hipStream_t s) {
+  const size_t nb = (size_t)rows * (K / 256);
+  hipLaunchKernelGGL(q4k_quantize_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, s, w, nb, blocks);
+  return hipGetLastError();
+}
+
+// candle blocks <-> device blocks (the quant bytes regrouped, everything else as it is).
+__global__ void q4k_regroup_kernel(const uint8_t* src, size_t nblocks, uint8_t* dst, bool to_device) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= nblocks * 144) return;
+  const size_t blk = i / 144;
+  const int o = (int)(i - blk * 144);
+  int t = o;
+  if (o >= 16) {
+    const int g = (o - 16) / 32, e = (o - 16) % 32;
+    t = 16 + 32 * g + q4k_lane_pos(e);
+  }
+  if (to_device) dst[blk * 144 + t] = src[i];
+  else dst[i] = src[blk * 144 + t];
+}
+
+hipError_t launch_q4k_from_blocks(const uint8_t* candle, int rows, int K, uint8_t* blocks, hipStream_t s) {
+  const size_t nb = (size_t)rows * (K / 256);
+  hipLaunchKernelGGL(q4k_regroup_kernel, dim3((unsigned)((nb * 144 + 255) / 256)), dim3(256), 0, s, candle, nb, blocks, true);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4k_to_blocks(const uint8_t* blocks, int rows, int K, uint8_t* candle, hipStream_t s) {
+  const size_t nb = (size_t)rows * (K / 256);
+  hipLaunchKernelGGL(q4k_regroup_kernel, dim3((unsigned)((nb * 144 + 255) / 256)), dim3(256), 0, s, blocks, nb, candle, false);
+  return hipGetLastError();
+}
+
+// Q4K closed form of element e (< 256) of a device block: (d * sc) * q - dmin * m, unfused.
+__device__ float q4k_value(const uint8_t* b, int e) {
+  const float d = f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+  const float dmin = f16_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+  const int g = e / 64, hi = (e % 64) >= 32, ee = e % 32;
+  const uint8_t byte = b[16 + 32 * g + q4k_lane_pos(ee)];
+  const int q = hi ? byte >> 4 : byte & 0xF;
+  int s, m;
+  scale_min_k4(2 * g + hi, b + 4, s, m);
+  const float d1 = d * (float)s, m1 = dmin * (float)m;
+  const float t = d1 * (float)q;
+  return t - m1;
+}
+
+// Dequantization: Q8_0 closed form q * f32(d); Q4K closed form; dense bf16 widening; f32 copy.
 __global__ void dequant_kernel(LinearDev L, float* out) {
   size_t n = (size_t)L.out * L.in;
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   if (L.fmt == FMT_Q8_0) out[i] = (float)((const int8_t*)L.w)[i] * f16_to_f32(L.scale[i / 32]);
+  else if (L.fmt == FMT_Q4K) out[i] = q4k_value((const uint8_t*)L.w + (i / 256) * 144, (int)(i % 256));
   else if (L.fmt == FMT_BF16) out[i] = bf16_to_f32(((const uint16_t*)L.w)[i]);
   else out[i] = ((const float*)L.w)[i];
 }

@@ -623,8 +623,284 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
   }
 }
 
-__device__ __forceinline__ bool is_q8_gemv(const Phase* ph) {
-  return ld_const(&ph->kind) == PH_GEMV && ld_const(&ph->g.L.fmt) == FMT_Q8_0;
+// ---- Q4K GEMV ------------------------------------------------------------------------------------
+// Candle's Q4K x Q8K CPU matmul (BlockQ4K::vec_dot_unopt against the activation row quantized by
+// BlockQ8K::from_float).  Per weight super-block and row, the i32 lane sums
+// aux[l] = sum over sub-blocks s of sc_s * (sum over g of q4 * q8 at element 32 s + 8 g + l) and
+// the min term sumi = sum over 16-groups j of bsum_j * m_{j/2} are exact; the row adds
+// (d_w * d_x) * (f32)aux[l] to lane sum l and subtracts (dmin_w * d_x) * (f32)sumi, super-block
+// by super-block, and ends with min_sum + (((s_0 + s_1) + ...) + s_7).  The weight waves write
+// the nine f32 terms of every (row, super-block) into LDS; the row waves add them in order.
+
+// LDS words of the Q8K quantizer's per-wave maxima: two item parities x (max |x| bits, value) x
+// 8 row waves x row slots.
+__host__ __device__ constexpr int q4k_red_words(int K) { return 2 * 2 * kRowWaves * row_slots(K); }
+
+// LDS of a Q4K unit: xs [K] f32 | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
+// bs [nb][16] i32 | red [q4k_red_words(K)] | T [nb][9][ts] f32 | Y [2 ipw] f32.
+struct Q4Lds {
+  float* xs;
+  int8_t* xq;
+  float* xd;
+  int* bs;
+  float* red;
+  float* T;
+  float* Y;
+};
+
+__device__ __forceinline__ Q4Lds q4_lds(unsigned char* smem, int K, int nb, int ts) {
+  Q4Lds l;
+  l.xs = (float*)smem;
+  l.xq = (int8_t*)(l.xs + K);
+  l.xd = (float*)(l.xq + K);
+  l.bs = (int*)(l.xd + ((nb + 3) & ~3));
+  l.red = (float*)(l.bs + nb * 16);
+  l.T = l.red + q4k_red_words(K);
+  l.Y = l.T + nb * kQ4Terms * ts;
+  return l;
+}
+
+__device__ __forceinline__ Q8Geom q4_geom(int K, int items, int ipw, int parts, bool silu, int unit) {
+  Q8Geom g = q8_geom(K, items, ipw, parts, silu, unit);
+  g.nb = K / 256;
+  g.total = g.NR * g.nb;
+  return g;
+}
+
+// Byte offset of element e (< 32) of a 32-value group in the lane-grouped order.
+__host__ __device__ constexpr int q4k_lane_pos(int e) { return ((e & 7) << 2) | (e >> 3); }
+
+// BlockQ8K::from_float of a register row (elements t + 512 u): per 256 values, mx = the value of
+// largest magnitude (the first one on ties), iscale = -128 / mx, q = min(round(iscale * x), 127),
+// d = 1 / iscale (all zero when the block is); bs = sums of 16 consecutive quants.  A block is
+// the 4 waves of one half of the row threads in one slot.  The first part publishes each wave's
+// maximum (in `red`, by item parity) and synchronizes the row waves; the second part writes the
+// quants once the weight waves are done with the previous item's.
+template <int KP>
+__device__ __forceinline__ void q8k_wave_maxima(const float (&v)[KP], float* red, RowSync& rs) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int u = 0; u < KP; ++u) {
+    const uint32_t a = __float_as_uint(fabsf(v[u]));
+    const uint32_t hm = half_max_bits(a);
+    const uint32_t m = max((uint32_t)__builtin_amdgcn_readlane((int)hm, 0), (uint32_t)__builtin_amdgcn_readlane((int)hm, 32));
+    const unsigned long long hit = __ballot(a == m);
+    const int first = (int)__builtin_ctzll(hit);
+    const float val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[u]), first));
+    if (lane == 0) {
+      red[(u * kRowWaves + wave) * 2] = __uint_as_float(m);
+      red[(u * kRowWaves + wave) * 2 + 1] = val;
+    }
+  }
+  rs.sync();
+}
+
+template <int KP>
+__device__ __forceinline__ void q8k_write(const float (&v)[KP], int K, const float* red, int8_t* xq, float* xd, int* bs) {
+  const int half = threadIdx.x / 256;
+#pragma unroll
+  for (int u = 0; u < KP; ++u) {
+    uint32_t best = 0;
+    float mx = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int o = (u * kRowWaves + 4 * half + w) * 2;
+      const uint32_t m = __float_as_uint(red[o]);
+      const float val = red[o + 1];
+      mx = m > best ? val : mx;
+      best = m > best ? m : best;
+    }
+    const float iscale = best != 0 ? -128.0f / mx : 0.0f;
+    const int i = threadIdx.x + u * kRowThreads;
+    const int q = best != 0 ? sat_i8(fminf(roundf(iscale * v[u]), 127.0f)) : 0;
+    int s = q;
+    s += __shfl_xor(s, 8, 16);
+    s += __shfl_xor(s, 4, 16);
+    s += __shfl_xor(s, 2, 16);
+    s += __shfl_xor(s, 1, 16);
+    if (i < K) {
+      xq[(i & ~31) | q4k_lane_pos(i & 31)] = (int8_t)q;
+      if ((i & 15) == 0) bs[i >> 4] = s;
+      if ((i & 255) == 0) xd[i >> 8] = best != 0 ? 1.0f / iscale : 0.0f;
+    }
+  }
+}
+
+// acc over the nine term rows of row r: lane sums l < 8 in super-block order, the min term
+// subtracted in super-block order, then min_sum + (((s_0 + s_1) + ...) + s_7).
+__device__ __forceinline__ float q4k_row_sum(const float* T, int ts, int r, int nb) {
+  const float* t = T + r;
+  float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  float mins = 0.0f;
+  for (int blk = 0; blk < nb; ++blk) {
+    float v[kQ4Terms];
+#pragma unroll
+    for (int c = 0; c < kQ4Terms; ++c) v[c] = t[(blk * kQ4Terms + c) * ts];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s[c] = s[c] + v[c];
+    mins = mins - v[8];
+  }
+  float s8 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) s8 = s8 + s[c];
+  return mins + s8;
+}
+
+// Row-wave part of Q4K GEMV item `item` (the Q8_0 item's flow with the Q8K quantizer).
+template <int KP>
+__device__ __forceinline__ void gemv_q4k_rows(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
+                                              RowSync& rs, unsigned item) {
+  const Q8Geom g = q4_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
+  const Q4Lds l = q4_lds(smem, g.K, g.nb, g.ts);
+  const int p = spos[g.b];
+  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
+  constexpr bool kNorm = KP <= 8;
+  NormW<kNorm ? KP : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, g.K, nwt);
+  float v[KP];
+  load_row(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
+  if constexpr (kNorm) {
+    if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
+  }
+  float* red = l.red + (item & 1) * (q4k_red_words(g.K) / 2);
+  q8k_wave_maxima(v, red, rs);
+  // the weight waves have read the previous item's quantized row
+  lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
+  q8k_write(v, g.K, red, l.xq, l.xd, l.bs);
+  lds_signal(&rs.ws->xq_parts);
+  const bool many = g.NR > kWave;  // uniform
+  if (many || threadIdx.x < kWave) {
+    lds_wait(&rs.ws->t_parts, (item + 1) * kWeightWaves, &rs.ws->stop);
+    if ((int)threadIdx.x < g.NR) l.Y[threadIdx.x] = q4k_row_sum(l.T, g.ts, threadIdx.x, g.nb);
+  }
+  if (many) {
+    rs.sync();
+  } else {
+    if (threadIdx.x >= kWave) return;
+    wave_lds_fence();
+  }
+  gemv_finish(a, g.b, g.part, g.i0, g.ni, p, in, l.Y);
+}
+
+// Weight-wave state of one Q4K item: per super-block slot the 16-byte header and the 128 quant
+// bytes.
+struct WItemQ4 {
+  Q8Geom g;
+  int ipw;
+  int maxb;
+  v4i h[kQ4Blocks];
+  v4i q[kQ4Blocks][8];
+};
+
+__device__ __forceinline__ void w_issue_q4k(const Phase* ph, int unit, WItemQ4& it) {
+  const int K = ld_const(&ph->g.L.in);
+  const int epi = ld_const(&ph->g.epi);
+  const int ff_hidden = ld_const(&ph->g.ff_hidden);
+  const int items = epi == EPI_SILU_GATE ? ff_hidden : ld_const(&ph->g.L.out);
+  it.ipw = ld_const(&ph->g.ipw);
+  it.maxb = ld_const(&ph->g.maxb);
+  it.g = q4_geom(K, items, it.ipw, ld_const(&ph->g.parts), epi == EPI_SILU_GATE, unit);
+  const unsigned char* wb = (const unsigned char*)ld_const(&ph->g.L.w);
+  const int nb = it.g.nb;
+  const int w = threadIdx.x - kRowThreads;
+  int r = w / nb, blk = w - r * nb;
+  const int dr = kWeightThreads / nb, db = kWeightThreads - dr * nb;
+#pragma unroll
+  for (int k = 0; k < kQ4Blocks; ++k) {
+    if (k >= it.maxb) break;  // uniform
+    if (w + k * kWeightThreads < it.g.total) {
+      const size_t row = (size_t)gemv_phys_row(epi, ff_hidden, it.g.i0, it.g.ni, r);
+      const v4i* bp = (const v4i*)(wb + (row * nb + blk) * 144);
+      it.h[k] = ldg(bp);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) it.q[k][j] = ldg_stream(bp + 1 + j);
+    }
+    r += dr;
+    blk += db;
+    if (blk >= nb) {
+      blk -= nb;
+      ++r;
+    }
+  }
+}
+
+__device__ __forceinline__ int q4k_lane(const v4i& a, const v4i& b, int l) {
+  switch (l) {
+    case 0: return a.x;
+    case 1: return a.y;
+    case 2: return a.z;
+    case 3: return a.w;
+    case 4: return b.x;
+    case 5: return b.y;
+    case 6: return b.z;
+    default: return b.w;
+  }
+}
+
+// The item's terms: T[blk][l][r] = (d_w * d_x) * (f32)aux[l] for l < 8 and
+// T[blk][8][r] = (dmin_w * d_x) * (f32)sumi.
+__device__ __forceinline__ void w_terms_q4k(const WItemQ4& it, unsigned char* smem) {
+  const Q4Lds l = q4_lds(smem, it.g.K, it.g.nb, it.g.ts);
+  const int nb = it.g.nb;
+  const int w = threadIdx.x - kRowThreads;
+  int r = w / nb, blk = w - r * nb;
+  const int dr = kWeightThreads / nb, db = kWeightThreads - dr * nb;
+#pragma unroll
+  for (int k = 0; k < kQ4Blocks; ++k) {
+    if (k >= it.maxb) break;  // uniform
+    if (w + k * kWeightThreads < it.g.total) {
+      // get_scale_min_k4 for all eight sub-blocks, four bytes at a time
+      const uint32_t s0 = (uint32_t)it.h[k].y, s1 = (uint32_t)it.h[k].z, s2 = (uint32_t)it.h[k].w;
+      const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
+      const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | (((s0 >> 6) & 0x03030303u) << 4);
+      const uint32_t mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | (((s1 >> 6) & 0x03030303u) << 4);
+      const int* xw = (const int*)(l.xq + blk * 256);
+      int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t scw = j < 2 ? sc_lo : sc_hi;
+        const int sa = (int)((scw >> (16 * (j & 1))) & 0xFF);      // sub-block 2 j
+        const int sb = (int)((scw >> (16 * (j & 1) + 8)) & 0xFF);  // sub-block 2 j + 1
+        const v4i xa0 = *(const v4i*)(xw + 16 * j), xa1 = *(const v4i*)(xw + 16 * j + 4);
+        const v4i xb0 = *(const v4i*)(xw + 16 * j + 8), xb1 = *(const v4i*)(xw + 16 * j + 12);
+#pragma unroll
+        for (int ln = 0; ln < 8; ++ln) {
+          const uint32_t dw = (uint32_t)q4k_lane(it.q[k][2 * j], it.q[k][2 * j + 1], ln);
+          const int lo = (int)(dw & 0x0F0F0F0Fu), hi = (int)((dw >> 4) & 0x0F0F0F0Fu);
+          aux[ln] += sa * sdot4(lo, q4k_lane(xa0, xa1, ln), 0) + sb * sdot4(hi, q4k_lane(xb0, xb1, ln), 0);
+        }
+      }
+      const int* bs = l.bs + blk * 16;
+      int sumi = 0;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int s = jj / 2;
+        const uint32_t mw = s < 4 ? mn_lo : mn_hi;
+        sumi += bs[jj] * (int)((mw >> (8 * (s & 3))) & 0xFF);
+      }
+      const float xd = l.xd[blk];
+      const uint32_t hd = (uint32_t)it.h[k].x;
+      const float d = f16_to_f32((uint16_t)(hd & 0xFFFF)) * xd;
+      const float dm = f16_to_f32((uint16_t)(hd >> 16)) * xd;
+      float* T = l.T + blk * kQ4Terms * it.g.ts + r;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) T[c * it.g.ts] = d * (float)aux[c];
+      T[8 * it.g.ts] = dm * (float)sumi;
+    }
+    r += dr;
+    blk += db;
+    if (blk >= nb) {
+      blk -= nb;
+      ++r;
+    }
+  }
+}
+
+// GEMV phases whose units the row waves and the weight waves share (quantized weights).
+__device__ __forceinline__ bool is_split_gemv(const Phase* ph) {
+  if (ld_const(&ph->kind) != PH_GEMV) return false;
+  const int fmt = ld_const(&ph->g.L.fmt);
+  return fmt == FMT_Q8_0 || fmt == FMT_Q4K;
 }
 
 // ---- batched Q8_0 GEMM (lockstep batches; row waves) ----------------------------------------------
@@ -1060,14 +1336,25 @@ __device__ __forceinline__ void copy_unit(const float* x, int x_stride, float* y
 // Row-wave part of work unit `unit` of phase `ph` for step `step` of a launch; `spos` holds
 // the streams' positions at the start of the step, `item` counts the workgroup's Q8_0 GEMV
 // units.
+template <unsigned F>
 __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
                                          unsigned char* smem, RowSync& rs, unsigned& item) {
-  if (ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
+  if ((F & FAM_Q8) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
     switch (row_slots(ph.g.L.in)) {
       case 2: gemv_q8_rows<2>(ph.g, unit, spos, smem, rs, item); break;
       case 4: gemv_q8_rows<4>(ph.g, unit, spos, smem, rs, item); break;
       case 8: gemv_q8_rows<8>(ph.g, unit, spos, smem, rs, item); break;
       default: gemv_q8_rows<kMaxSlots>(ph.g, unit, spos, smem, rs, item); break;
+    }
+    ++item;
+    return;
+  }
+  if ((F & FAM_Q4K) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q4K) {
+    switch (row_slots(ph.g.L.in)) {
+      case 2: gemv_q4k_rows<2>(ph.g, unit, spos, smem, rs, item); break;
+      case 4: gemv_q4k_rows<4>(ph.g, unit, spos, smem, rs, item); break;
+      case 8: gemv_q4k_rows<8>(ph.g, unit, spos, smem, rs, item); break;
+      default: gemv_q4k_rows<kMaxSlots>(ph.g, unit, spos, smem, rs, item); break;
     }
     ++item;
     return;
@@ -1081,6 +1368,7 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       break;
     }
     case PH_GEMV:
+      if constexpr (!(F & FAM_DENSE)) break;
       switch (row_slots(ph.g.L.in)) {
         case 2:
           if (ph.g.L.fmt == FMT_BF16) gemv_dense_unit<true, 2>(ph.g, unit, spos, smem, rs);
@@ -1107,6 +1395,7 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       break;
     }
     case PH_QUANT:
+      if constexpr (!(F & FAM_BATCH)) break;
       switch (row_slots(ph.g.L.in)) {
         case 2: quant_unit<2>(ph.g, unit, smem, rs); break;
         case 4: quant_unit<4>(ph.g, unit, smem, rs); break;
@@ -1115,6 +1404,7 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       }
       break;
     case PH_QGEMM:
+      if constexpr (!(F & FAM_BATCH)) break;
       qgemm_unit(ph.g, unit, spos, smem, rs);
       break;
     case PH_ARGMAX:
@@ -1136,7 +1426,7 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
   }
 }
 
-// Weight waves of a launch: the Q8_0 GEMV units of this workgroup in program order
+// Weight waves of a launch: the quantized GEMV units of this workgroup in program order
 // (steps x phases x units u = blockIdx.x + k * gridDim.x).  Advances (step, p, u) to the next
 // one; false when there is none.
 __device__ __forceinline__ bool w_next(const StepParams& P, int& step, int& p, int& u) {
@@ -1149,7 +1439,7 @@ __device__ __forceinline__ bool w_next(const StepParams& P, int& step, int& p, i
       p = 0;
       if (++step >= P.n_steps) return false;
     }
-    if (is_q8_gemv(P.prog + p) && (int)blockIdx.x < ld_const(&P.prog[p].units)) {
+    if (is_split_gemv(P.prog + p) && (int)blockIdx.x < ld_const(&P.prog[p].units)) {
       u = blockIdx.x;
       return true;
     }
@@ -1157,17 +1447,25 @@ __device__ __forceinline__ bool w_next(const StepParams& P, int& step, int& p, i
 }
 
 // The weight-wave loop: request an item's blocks, wait for its quantized row, write its terms.
+template <unsigned F>
 __device__ __forceinline__ void weight_waves(const StepParams& P, WgSync* ws, unsigned char* smem) {
   int step = 0, p = -1, u = 0;
   unsigned item = 0;
-  WItem it;
   while (w_next(P, step, p, u)) {
     // the blocks are requested right after the row waves have requested the item's input row,
     // so that neither the row nor the row waves' stores and barrier traffic queue behind them
     if (!lds_wait<true>(&ws->r_issued, (item + 1) * kRowWaves, &ws->stop)) return;
-    w_issue(P.prog + p, u, it);
-    if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return;
-    w_terms(it, smem);
+    if ((F & FAM_Q4K) && (!(F & FAM_Q8) || ld_const(&P.prog[p].g.L.fmt) == FMT_Q4K)) {
+      WItemQ4 it4;
+      w_issue_q4k(P.prog + p, u, it4);
+      if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return;
+      w_terms_q4k(it4, smem);
+    } else {
+      WItem it;
+      w_issue(P.prog + p, u, it);
+      if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return;
+      w_terms(it, smem);
+    }
     lds_signal(&ws->t_parts);
     ++item;
   }

@@ -207,8 +207,22 @@ int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string&
   L->out = out_f;
   L->in = in_f;
   const size_t count = (size_t)out_f * in_f;
-  if (t->dtype == SVL_Q4K || (t->dtype != SVL_Q8_0 && quantize == SVL_Q4K && in_f % 256 == 0))
-    return set_error(SVL_ERR_CONFIG, "tensor %s: Q4K linears are not supported yet", name.c_str());
+  if (t->dtype == SVL_Q4K) {
+    if (in_f % 256) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: Q4K needs in %% 256 == 0", name.c_str());
+    const size_t bytes = count / 256 * 144;
+    void *w, *tmp;
+    TRY(m->alloc(&w, bytes));
+    HIP_TRY(hipMalloc(&tmp, bytes));
+    HIP_TRY(hipMemcpy(tmp, t->data, bytes, hipMemcpyHostToDevice));
+    hipError_t e = launch_q4k_from_blocks((const uint8_t*)tmp, out_f, in_f, (uint8_t*)w, m->stream);
+    hipError_t e2 = hipStreamSynchronize(m->stream);
+    hipFree(tmp);
+    HIP_TRY(e);
+    HIP_TRY(e2);
+    L->fmt = FMT_Q4K;
+    L->w = w;
+    return 0;
+  }
   if (t->dtype == SVL_Q8_0) {
     if (in_f % 32) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: Q8_0 needs in %% 32 == 0", name.c_str());
     void *qs, *d, *tmp;
@@ -228,6 +242,22 @@ int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string&
   }
   if (t->dtype != SVL_F32 && t->dtype != SVL_BF16 && t->dtype != SVL_F16)
     return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: unsupported dtype %d", name.c_str(), t->dtype);
+  if (quantize == SVL_Q4K && in_f % 256 == 0) {
+    float* f = nullptr;
+    TRY(upload_f32(m, t, count, &f));
+    void* w;
+    TRY(m->alloc(&w, count / 256 * 144));
+    HIP_TRY(launch_q4k_quantize(f, out_f, in_f, (uint8_t*)w, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    // the f32 staging copy is released right away
+    m->allocs.pop_back();
+    m->allocs.pop_back();
+    hipFree(f);
+    m->allocs.push_back(w);
+    L->fmt = FMT_Q4K;
+    L->w = w;
+    return 0;
+  }
   if (quantize == SVL_Q8_0 && in_f % 32 == 0) {
     float* f = nullptr;
     TRY(upload_f32(m, t, count, &f));
@@ -730,7 +760,7 @@ int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
     }
     P.n_steps = (int)n_steps;
     P.gen0 = s->gen;
-    HIP_TRY(launch_step_program(P, s->grid, p.smem, s->stream));
+    HIP_TRY(launch_step_program(P, program_families(p.phases.data(), P.nphase), s->grid, p.smem, s->stream));
     s->gen += need;
   } else {
     P.n_steps = (int)n_steps;  // the units see the launch's step count (next-step gathers)
@@ -890,7 +920,16 @@ int svl_model_linear_weight(const svl_model* m, const char* name, float* f32, si
     hipFree(tmp);
     HIP_TRY(e);
   }
-  if (blocks) {
+  if (blocks && L->fmt == FMT_Q4K) {
+    if (block_bytes != n / 256 * 144) return set_error(SVL_ERR_INVALID_INPUT, "block buffer size mismatch");
+    uint8_t* tmp;
+    HIP_TRY(hipMalloc(&tmp, block_bytes));
+    hipError_t e = launch_q4k_to_blocks((const uint8_t*)L->w, L->out, L->in, tmp, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e == hipSuccess) e = hipMemcpy(blocks, tmp, block_bytes, hipMemcpyDeviceToHost);
+    hipFree(tmp);
+    HIP_TRY(e);
+  } else if (blocks) {
     if (L->fmt != FMT_Q8_0) return set_error(SVL_ERR_INVALID_INPUT, "linear %s is not quantized", name);
     if (block_bytes != n / 32 * 34) return set_error(SVL_ERR_INVALID_INPUT, "block buffer size mismatch");
     uint8_t* tmp;

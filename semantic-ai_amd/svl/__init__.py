@@ -170,19 +170,22 @@ class Model:
         self.close()
 
     def linear_weight(self, name: str):
-        """(dequantized f32 [out, in], candle Q8_0 block bytes or None) as held on the GPU."""
+        """(dequantized f32 [out, in], candle Q8_0 or Q4K block bytes [out, ...] or None) as held
+        on the GPU."""
         out, inp = self._linear_shape(name)
         w = np.empty((out, inp), dtype=np.float32)
-        blocks = None
         L = load_library()
         _check(L.svl_model_linear_weight(self.h, name.encode(), _p(w), w.size, None, 0))
-        try:
-            b = np.empty(out * inp // 32 * 34, dtype=np.uint8)
-            _check(L.svl_model_linear_weight(self.h, name.encode(), None, 0, _p(b), b.size))
-            blocks = b.reshape(out, inp // 32 * 34)
-        except SvlError:
-            blocks = None
-        return w, blocks
+        for values, nbytes in ((32, 34), (256, 144)):  # Q8_0, Q4K
+            if inp % values:
+                continue
+            b = np.empty(out * inp // values * nbytes, dtype=np.uint8)
+            try:
+                _check(L.svl_model_linear_weight(self.h, name.encode(), None, 0, _p(b), b.size))
+            except SvlError:
+                continue
+            return w, b.reshape(out, inp // values * nbytes)
+        return w, None
 
     def _linear_shape(self, name: str):
         c = self.cfg

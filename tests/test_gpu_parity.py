@@ -101,6 +101,82 @@ def test_q8_0_candle_blocks_round_trip():
     assert np.array_equal(blocks, blocked["transformer.layers.0.self_attn.in_proj_weight"][2])
 
 
+def test_q4k_quantize_and_dequantize_bit_exact():
+    """The GPU's Q4K quantizer (scale/min fit per 32-value sub-block, 6-bit packing) writes the
+    oracle's block bytes; the GPU's dequantization equals the oracle's closed form."""
+    s = W.S2_SMALL
+    t, g, _ = build(s, "q4k", seed=30)
+    for name in ["text_linear", "0.in_proj", "1.out_proj", "1.ff1", "0.ff2"]:
+        w = t[_tensor_for(name, s)][2]
+        f32, blocks = g.linear_weight(name)
+        ob = oracle.quantize_q4k(w)
+        assert blocks is not None and np.array_equal(blocks, ob), name
+        assert np.array_equal(f32.view(np.uint32), oracle.dequantize_q4k(ob, w.shape[1]).view(np.uint32)), name
+
+
+def test_q4k_quantize_across_magnitudes_and_offsets():
+    """Super-blocks from 1e-6 to 1e3 in magnitude, some all-positive (min term zero), some
+    constant (scale zero): GPU blocks equal the oracle's."""
+    s = W.S2_SMALL
+    t = W.make_weights(s, "q4k", seed=31)
+    name = "transformer.layers.1.gating.linear_in.weight"
+    shape = t[name][1]
+    rng = np.random.default_rng(32)
+    w = rng.standard_normal(shape).astype(np.float32).reshape(-1, 256)
+    w *= (10.0 ** rng.uniform(-6, 3, size=(w.shape[0], 1))).astype(np.float32)
+    w[::7] = np.abs(w[::7]) + np.float32(0.5)
+    w[::11, :32] = np.float32(0.25)
+    w[::13] = np.float32(-1.5)
+    t[name] = (W.F32, shape, w.reshape(shape))
+    g = svl.Model(s.config(W.Q4K), t)
+    _, got = g.linear_weight("1.ff1")
+    assert np.array_equal(got, oracle.quantize_q4k(t[name][2]))
+
+
+def test_q4k_candle_blocks_round_trip():
+    """Candle Q4K block bytes handed to the model come back unchanged, and the model computes
+    with them as with its own quantization of the same floats."""
+    s = W.S2_SMALL
+    t = W.make_weights(s, "q4k", seed=33)
+    blocked = dict(t)
+    for name, (dt, shp, data) in t.items():
+        if dt == W.F32 and len(shp) == 2 and shp[1] % 256 == 0:
+            blocked[name] = (W.Q4K, shp, oracle.quantize_q4k(data))
+    g = svl.Model(s.config(0), blocked)
+    _, blocks = g.linear_weight("0.ff1")
+    assert np.array_equal(blocks, blocked["transformer.layers.0.gating.linear_in.weight"][2])
+    g2 = svl.Model(s.config(W.Q4K), t)
+    audio = W.audio_tokens(s, 12, seed=34)[0]
+    a = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    b = g2.recognize(audio[:, None, :], g2.init_state())[:, 0]
+    assert np.array_equal(a, b)
+
+
+def test_q4k_steps_match_oracle():
+    """Q4K linears (activations quantized to Q8K): 64 steps through a window of 40, logits
+    bit-exact to the oracle's Q4K x Q8K vec_dot, tokens equal."""
+    s = W.S2_SMALL
+    _, g, o = build(s, "q4k", seed=35)
+    gs, os_ = g.init_state(), o.new_state()
+    audio = W.audio_tokens(s, 64, seed=36)[0]
+    text = s.text_card
+    for i in range(64):
+        tg, lg = g.step([text], audio[i][None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, audio[i], want_logits=True)
+        assert tg[0] == to, f"step {i}"
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), \
+            f"step {i}: max diff {float(np.max(np.abs(lg[0] - lo)))}"
+        text = int(tg[0])
+
+
+def test_q4k_recognize_matches_oracle_greedy():
+    s = W.S2_SMALL
+    _, g, o = build(s, "q4k", seed=37)
+    audio = W.audio_tokens(s, 150, seed=38)[0]
+    got = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    assert np.array_equal(got, o.new_state().stt_greedy(audio))
+
+
 @pytest.mark.parametrize("dtype", ["q8_0", "bf16", "f32"])
 def test_stt_small_steps_match_oracle(dtype):
     """64 steps through a window of 24 (the ring wraps twice): logits bit-exact, tokens equal."""
