@@ -167,6 +167,18 @@ constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8
 constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit
 constexpr int kTileBatch = 64;   // batch rows of a GEMM unit
 constexpr int kMaxBatch = 1024;
+constexpr int kGemmChunk = 4;    // Q8_0 blocks (128 bytes of K) per LDS stage of a GEMM unit
+constexpr int kGemmStages = 6;   // LDS stages of a GEMM unit (kGemmStages - 1 chunks in flight)
+// weights [kTileRows][128] | activations [kTileBatch][128] | weight scales [kTileRows][4] (f16 in
+// the low half of a dword: a 2-byte direct load fills a 4-byte LDS slot per lane) | activation
+// scales [kTileBatch][4] f32
+constexpr int kGemmStageBytes = kTileRows * 128 + kTileBatch * 128 + kTileRows * kGemmChunk * 4 + kTileBatch * kGemmChunk * 4;
+// s_waitcnt immediates (vmcnt only): at most 2 (kGemmStages - 2), 3 (kGemmStages - 2) or 0
+// vector memory operations outstanding
+constexpr int vm_wait_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 2));
+constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 2));
+constexpr int kVmWait0 = vm_wait_imm(0);
 
 // Unit families of a step program.  The persistent kernel is compiled for a few family sets, so
 // that a program is run by a kernel holding only the registers of the units it has.

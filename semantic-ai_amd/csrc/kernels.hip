@@ -254,7 +254,7 @@ size_t phase_smem(const Phase& ph) {
       return (size_t)K * 4 + K + (size_t)nb4 * 4 + 64;
     }
     case PH_QGEMM:
-      return (size_t)kTileRows * kTileBatch * 4 + 64;
+      return (size_t)kTileRows * kTileBatch * 4 + (size_t)kGemmStages * kGemmStageBytes + 64;
     default:
       return 64;
   }

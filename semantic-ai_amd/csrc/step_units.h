@@ -938,9 +938,129 @@ __device__ __forceinline__ void quant_unit(const GemvArgs& a, int b, unsigned ch
 
 typedef long v_i8x8;
 
-// One GEMM unit: output rows of row tile `part`, batch rows of batch tile `bt`.  Wave w computes
-// the 16 x 16 sub-tile of tile rows 16 (w / 4) .. and batch rows 16 (w % 4) ..; the results meet
-// in LDS for the epilogues.
+// One GEMM unit: output rows of row tile `part`, batch rows of batch tile `bt`.  K is streamed in
+// chunks of kGemmChunk blocks through a ring of kGemmStages LDS stages, filled by direct
+// global -> LDS loads issued kGemmStages - 1 chunks ahead (W and X rows with their 16-byte
+// segments XOR-swizzled by row, so that the MFMA operand reads spread over the banks).  Wave w
+// computes the 16 x 16 sub-tile of tile rows 16 (w / 4) .. and batch rows 16 (w % 4) ..; the
+// results meet in LDS for the epilogues.
+#define SVL_LDS __attribute__((address_space(3)))
+
+// Lane i's BYTES at src land at dst_wave_base + i * BYTES (dst is wave-uniform); a 2-byte load
+// fills the low half of the 4-byte slot dst_wave_base + 4 i.  CO: coherent (agent scope) load, for
+// data written by other workgroups during the launch.
+template <int BYTES, bool CO>
+__device__ __forceinline__ void lds_dma(const void* src, unsigned char* dst_wave_base) {
+  const SVL_GLOBAL void* g = (const SVL_GLOBAL void*)src;
+  SVL_LDS void* l = (SVL_LDS void*)dst_wave_base;
+  if constexpr (BYTES == 16) {
+    if constexpr (CO) __builtin_amdgcn_global_load_lds(g, l, 16, 0, 16);
+    else __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+  } else if constexpr (BYTES == 4) {
+    if constexpr (CO) __builtin_amdgcn_global_load_lds(g, l, 4, 0, 16);
+    else __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
+  } else {
+    static_assert(BYTES == 2, "2, 4 or 16 bytes per lane");
+    if constexpr (CO) __builtin_amdgcn_global_load_lds(g, l, 2, 0, 16);
+    else __builtin_amdgcn_global_load_lds(g, l, 2, 0, 0);
+  }
+}
+
+struct GemmStage {
+  unsigned char* w;   // [kTileRows][128] int8, swizzled
+  unsigned char* x;   // [kTileBatch][128] int8, swizzled
+  uint32_t* dw;       // [kTileRows][kGemmChunk] f16 in the low half
+  float* dx;          // [kTileBatch][kGemmChunk]
+};
+
+__device__ __forceinline__ GemmStage gemm_stage(unsigned char* smem, int s) {
+  unsigned char* base = smem + kTileRows * kTileBatch * 4 + s * kGemmStageBytes;
+  GemmStage g;
+  g.w = base;
+  g.x = base + kTileRows * 128;
+  g.dw = (uint32_t*)(g.x + kTileBatch * 128);
+  g.dx = (float*)(g.dw + kTileRows * kGemmChunk);
+  return g;
+}
+
+// Byte offset of 16-byte segment `seg` of row j in a swizzled 128-byte row.
+__device__ __forceinline__ int swz(int j, int seg) { return j * 128 + ((seg ^ (j & 7)) << 4); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(size_t)(const SVL_LDS void*)p; }
+
+// One lane's operands of a chunk: the A and B fragments of its four blocks, the weight scales of
+// its four D rows and the activation scales of its D column.  The reads and their wait are one
+// statement: the compiler would otherwise wait for every direct load still landing in the other
+// stages before the first read.
+// RowSync::sync for the GEMM loop, its LDS accesses written out so that the compiler does not
+// wait for the direct loads in flight before them (it cannot tell the counters from the stages).
+// Prior LDS reads of the wave have completed (gemm_read waits for them).
+__device__ __forceinline__ void gemm_sync(RowSync& rs) {
+  const uint32_t ctr = lds_addr(&rs.ws->r_arrive), stop = lds_addr(&rs.ws->stop);
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    const uint32_t one = 1;
+    asm volatile("ds_add_u32 %0, %1" : : "v"(ctr), "v"(one) : "memory");
+  }
+  rs.epoch += kRowWaves;
+  unsigned spins = 0;
+  for (;;) {
+    uint32_t v, st;
+    asm volatile(
+        "ds_read_b32 %0, %2\n\t"
+        "ds_read_b32 %1, %3\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v), "=&v"(st)
+        : "v"(ctr), "v"(stop)
+        : "memory");
+    v = __builtin_amdgcn_readfirstlane(v);
+    st = __builtin_amdgcn_readfirstlane(st);
+    if ((int)(v - rs.epoch) >= 0 || st) break;
+    if (++spins > kLdsSpinLimit) {
+      const uint32_t one = 1;
+      asm volatile("ds_write_b32 %0, %1" : : "v"(stop), "v"(one) : "memory");
+      break;
+    }
+  }
+}
+
+struct GemmOps {
+  v_i8x8 a[4], b[4];
+  uint4 dw[4];
+  float4 dx;
+};
+
+__device__ __forceinline__ void gemm_read(const GemmStage& st, int ja, int jb, int g, int r0, GemmOps& o) {
+  uint32_t aa[4], ba[4], da[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int seg = 2 * kk + g / 2, inner = 8 * (g & 1);
+    aa[kk] = lds_addr(st.w) + swz(ja, seg) + inner;
+    ba[kk] = lds_addr(st.x) + swz(jb, seg) + inner;
+    da[kk] = lds_addr(st.dw) + (r0 + 4 * g + kk) * (kGemmChunk * 4);
+  }
+  const uint32_t xa = lds_addr(st.dx) + jb * (kGemmChunk * 4);
+  asm volatile(
+      "ds_read_b64 %0, %13\n\t"
+      "ds_read_b64 %1, %14\n\t"
+      "ds_read_b64 %2, %15\n\t"
+      "ds_read_b64 %3, %16\n\t"
+      "ds_read_b64 %4, %17\n\t"
+      "ds_read_b64 %5, %18\n\t"
+      "ds_read_b64 %6, %19\n\t"
+      "ds_read_b64 %7, %20\n\t"
+      "ds_read_b128 %8, %21\n\t"
+      "ds_read_b128 %9, %22\n\t"
+      "ds_read_b128 %10, %23\n\t"
+      "ds_read_b128 %11, %24\n\t"
+      "ds_read_b128 %12, %25\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o.a[0]), "=&v"(o.a[1]), "=&v"(o.a[2]), "=&v"(o.a[3]), "=&v"(o.b[0]), "=&v"(o.b[1]), "=&v"(o.b[2]),
+        "=&v"(o.b[3]), "=&v"(o.dw[0]), "=&v"(o.dw[1]), "=&v"(o.dw[2]), "=&v"(o.dw[3]), "=&v"(o.dx)
+      : "v"(aa[0]), "v"(aa[1]), "v"(aa[2]), "v"(aa[3]), "v"(ba[0]), "v"(ba[1]), "v"(ba[2]), "v"(ba[3]), "v"(da[0]),
+        "v"(da[1]), "v"(da[2]), "v"(da[3]), "v"(xa)
+      : "memory");
+}
+
 __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
                                            RowSync& rs) {
   const int K = a.L.in, nb = K / 32;
@@ -952,48 +1072,70 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
   const int b0 = bt * kTileBatch;
   const int nbat = min(kTileBatch, a.B - b0);
   float* Y = (float*)smem;            // [kTileRows][kTileBatch]
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int r0 = 16 * (wave / 4), c0 = 16 * (wave % 4);
-  // this lane's A row and B column (clamped to valid rows; their results are not used)
-  const int ar = min(r0 + lane % 16, NR - 1), bc = min(c0 + lane % 16, nbat - 1);
-  const size_t arow = (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, ar);
-  const int kq = 8 * (lane / 16);
-  const int8_t* wa = (const int8_t*)a.L.w + arow * K + kq;
-  const int8_t* xb = a.xq + (size_t)(b0 + bc) * K + kq;
-  // D rows of this lane: r0 + 4 (lane / 16) + i; their weight scales and the column's x scales
-  size_t drow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    drow[i] = (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(r0 + 4 * (lane / 16) + i, NR - 1));
-  const float* dxp = a.xdq + (size_t)(b0 + bc) * nb;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  constexpr int CH = 8;  // blocks per round of loads
-  for (int k0 = 0; k0 < nb; k0 += CH) {
-    v_i8x8 av[CH], bv[CH];
-    float dw[CH][4], dx[CH];
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int k = min(k0 + u, nb - 1);
-      av[u] = ldg_stream((const v_i8x8*)(wa + (size_t)k * 32));
-      bv[u] = ld_co((const v_i8x8*)(xb + (size_t)k * 32));
-      dx[u] = ld_co(dxp + k);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dw[u][i] = f16_to_f32(ldg(a.L.scale + drow[i] * nb + k));
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  // ---- loads of one chunk: wave w brings X rows 8w..8w+7; waves 0-3 W rows 8w..8w+7, waves 4-5
+  // the weight scales of rows 16 (w - 4) .., waves 6-7 the activation scales of batch rows
+  // 32 (w - 6) .. (two loads).  Rows past the tile load the last row in use; blocks past K load
+  // the last block (their results are never used).
+  const int lrow = 8 * wave + lane / 8, lslot = lane % 8;
+  const int8_t* xsrc = a.xq + (size_t)(b0 + min(lrow, nbat - 1)) * K;
+  const int8_t* wsrc = (const int8_t*)a.L.w +
+                       (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(wave < 4 ? lrow : 0, NR - 1)) * K;
+  const int srow = 16 * (wave & 1) + lane / 4, sblk = lane % 4;
+  const uint16_t* dwsrc = a.L.scale + (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(srow, NR - 1)) * nb;
+  const int xrow0 = 32 * (wave & 1) + lane / 4;
+  const float* dxsrc0 = a.xdq + (size_t)(b0 + min(xrow0, nbat - 1)) * nb;
+  const float* dxsrc1 = a.xdq + (size_t)(b0 + min(xrow0 + 16, nbat - 1)) * nb;
+  auto issue = [&](int c) {
+    const GemmStage st = gemm_stage(smem, c % kGemmStages);
+    const int seg = lslot ^ (lrow & 7);
+    const int off = min(128 * c + 16 * seg, K - 16);
+    lds_dma<16, true>(xsrc + off, st.x + wave * 1024);
+    const int k = min(kGemmChunk * c + sblk, nb - 1);
+    if (wave < 4) {
+      lds_dma<16, false>(wsrc + off, st.w + wave * 1024);
+    } else if (wave < 6) {
+      lds_dma<2, false>(dwsrc + k, (unsigned char*)st.dw + (wave - 4) * 256);
+    } else {
+      lds_dma<4, true>(dxsrc0 + k, (unsigned char*)st.dx + (wave - 6) * 512);
+      lds_dma<4, true>(dxsrc1 + k, (unsigned char*)st.dx + (wave - 6) * 512 + 256);
     }
+  };
+  const int nch = (nb + kGemmChunk - 1) / kGemmChunk;
+  __builtin_amdgcn_s_waitcnt(kVmWait0);  // no older stores interleave with the counted loads
+  for (int c = 0; c < min(kGemmStages - 1, nch); ++c) issue(c);
+  const int r0 = 16 * (wave / 4), c0 = 16 * (wave % 4);
+  const int g = lane / 16, ja = r0 + lane % 16, jb = c0 + lane % 16;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < nch; ++c) {
+    // this wave's loads of chunk c have landed (later chunks may still be in flight)
+    if (c + kGemmStages - 1 <= nch) {
+      if (wave < 6) __builtin_amdgcn_s_waitcnt(kVmWait2);
+      else __builtin_amdgcn_s_waitcnt(kVmWait3);
+    } else {
+      __builtin_amdgcn_s_waitcnt(kVmWait0);
+    }
+    gemm_sync(rs);  // chunk c is in LDS everywhere; every wave is done with chunk c - 1
+    if (c + kGemmStages - 1 < nch) issue(c + kGemmStages - 1);
+    GemmOps o;
+    gemm_read(gemm_stage(smem, c % kGemmStages), ja, jb, g, r0, o);
+    const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      if (k0 + u >= nb) break;  // uniform
-      v4i c = {0, 0, 0, 0};
-      c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u], bv[u], c, 0, 0, 0);
+    for (int kk = 0; kk < kGemmChunk; ++kk) {
+      if (kGemmChunk * c + kk >= nb) break;  // uniform
+      v4i cc = {0, 0, 0, 0};
+      cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], cc, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float t = (float)c[i] * dw[u][i];
-        acc[i] = acc[i] + t * dx[u];
+        const uint32_t dwp = kk == 0 ? o.dw[i].x : (kk == 1 ? o.dw[i].y : (kk == 2 ? o.dw[i].z : o.dw[i].w));
+        const float dw = f16_to_f32((uint16_t)(dwp & 0xFFFF));
+        const float t = (float)cc[i] * dw;
+        acc[i] = acc[i] + t * dxs[kk];
       }
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) Y[(r0 + 4 * (lane / 16) + i) * kTileBatch + c0 + lane % 16] = acc[i];
+  for (int i = 0; i < 4; ++i) Y[(r0 + 4 * g + i) * kTileBatch + jb] = acc[i];
   rs.sync();
   // epilogues: item t of the tile for batch row b0 + j
   for (int e = threadIdx.x; e < ni * nbat; e += kRowThreads) {
