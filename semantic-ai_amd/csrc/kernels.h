@@ -179,6 +179,9 @@ constexpr int vm_wait_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); 
 constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 2));
 constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 2));
 constexpr int kVmWait0 = vm_wait_imm(0);
+constexpr int kAttnChunkBytes = 16384;  // K or V rows per LDS stage of an attention unit
+constexpr int kAttnStages = 6;
+constexpr int kAttnVmWait = vm_wait_imm(2 * (kAttnStages - 2));  // two direct loads per wave and chunk
 
 // Unit families of a step program.  The persistent kernel is compiled for a few family sets, so
 // that a program is run by a kernel holding only the registers of the units it has.

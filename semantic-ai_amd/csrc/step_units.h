@@ -1230,58 +1230,143 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
 // ---- attention unit (row waves) ------------------------------------------------------------------
 // One unit per (stream, head).  The query at position p attends to keys
 // max(0, p - window + 1) ..= p (transformer.rs:385) in the ring, in the reference's order
-// (attention.rs:139-168): w_j = scale * dot(q, k_j) with the 16-lane dot (16 threads per key,
-// 32 keys per pass, four passes of loads in flight), max, e_j = exp(w_j - max), the sum of e_j
-// in key order, then out = sum over keys in order of mul_add(e_j / sum, v_j, out); wave w
-// produces dims [32w, 32w + 32).
-
-constexpr int kKeysPerPass = kRowThreads / 16;
+// (attention.rs:139-168): w_j = scale * dot(q, k_j) with the 16-lane dot (16 threads per key),
+// max, e_j = exp(w_j - max), the sum of e_j in key order, then out = sum over keys in order of
+// mul_add(e_j / sum, v_j, out), thread d owning dim d.  K and then V rows stream through
+// kAttnStages LDS stages of kAttnChunkBytes by direct loads issued kAttnStages - 1 chunks ahead;
+// the LDS reads of the stages are written out (see gemm_read).
 
 __device__ __forceinline__ int visible_keys(const AttnArgs& a, int p) {
   return a.window > 0 ? min(p + 1, a.window) : p + 1;
 }
 
+__device__ __forceinline__ void lds_write_f32(uint32_t addr, float v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+
+// v[i] = the f32 (BF16: the widened bf16) at LDS byte addr + i * STEP, i < N (N = 4 or 8).
+template <int N, int STEP, bool BF16>
+__device__ __forceinline__ void lds_read_strided(uint32_t addr, float (&v)[N]) {
+  uint32_t r[8];
+  if constexpr (N == 8 && !BF16) {
+    asm volatile(
+        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:%9\n\tds_read_b32 %2, %8 offset:%10\n\t"
+        "ds_read_b32 %3, %8 offset:%11\n\tds_read_b32 %4, %8 offset:%12\n\tds_read_b32 %5, %8 offset:%13\n\t"
+        "ds_read_b32 %6, %8 offset:%14\n\tds_read_b32 %7, %8 offset:%15\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(addr), "i"(STEP), "i"(2 * STEP), "i"(3 * STEP), "i"(4 * STEP), "i"(5 * STEP), "i"(6 * STEP),
+          "i"(7 * STEP)
+        : "memory");
+  } else if constexpr (N == 8) {
+    asm volatile(
+        "ds_read_u16 %0, %8\n\tds_read_u16 %1, %8 offset:%9\n\tds_read_u16 %2, %8 offset:%10\n\t"
+        "ds_read_u16 %3, %8 offset:%11\n\tds_read_u16 %4, %8 offset:%12\n\tds_read_u16 %5, %8 offset:%13\n\t"
+        "ds_read_u16 %6, %8 offset:%14\n\tds_read_u16 %7, %8 offset:%15\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(addr), "i"(STEP), "i"(2 * STEP), "i"(3 * STEP), "i"(4 * STEP), "i"(5 * STEP), "i"(6 * STEP),
+          "i"(7 * STEP)
+        : "memory");
+  } else if constexpr (!BF16) {
+    static_assert(N == 4, "4 or 8 values");
+    asm volatile(
+        "ds_read_b32 %0, %4\n\tds_read_b32 %1, %4 offset:%5\n\tds_read_b32 %2, %4 offset:%6\n\t"
+        "ds_read_b32 %3, %4 offset:%7\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(addr), "i"(STEP), "i"(2 * STEP), "i"(3 * STEP)
+        : "memory");
+  } else {
+    static_assert(N == 4, "4 or 8 values");
+    asm volatile(
+        "ds_read_u16 %0, %4\n\tds_read_u16 %1, %4 offset:%5\n\tds_read_u16 %2, %4 offset:%6\n\t"
+        "ds_read_u16 %3, %4 offset:%7\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(addr), "i"(STEP), "i"(2 * STEP), "i"(3 * STEP)
+        : "memory");
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = BF16 ? __uint_as_float(r[i] << 16) : __uint_as_float(r[i]);
+}
+
+// Eight consecutive f32 at a 16-byte aligned LDS byte address.
+__device__ __forceinline__ void lds_read8_f32(uint32_t addr, float (&v)[8]) {
+  float4 x, y;
+  asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(x), "=&v"(y)
+               : "v"(addr)
+               : "memory");
+  v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+}
+
 template <int HD, bool BF16KV>
 __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem, RowSync& rs) {
-  float* w = (float*)smem;                     // L weights (16-byte aligned)
-  float* sum_slot = w + ((a.cap + 3) & ~3);    // 1
-  const int h = unit % a.H, b = unit / a.H;
+  constexpr int RB = HD * (BF16KV ? 2 : 4);   // bytes of a K or V row
+  constexpr int R = kAttnChunkBytes / RB;     // rows per stage
+  constexpr int C = HD / 16;
+  // the descriptor's fields are read once: the written-out LDS accesses below count as memory
+  // clobbers, after which the compiler would read the descriptor again (and wait for every load
+  // in flight before using the value)
+  const int cap = a.cap, H = a.H;
+  const float scale = a.scale;
+  const void* kc = a.kc;
+  const void* vc = a.vc;
+  float* out = a.out;
+  float* w = (float*)(smem + kAttnStages * kAttnChunkBytes);  // L weights (16-byte aligned)
+  float* sum_slot = w + ((cap + 7) & ~7) + 8;  // reads of w run up to 7 past the last key
+  const int h = unit % H, b = unit / H;
   const int p = spos[b];
   const int L = visible_keys(a, p);
   const int first = p + 1 - L;
-  const int kvh = h / (a.H / a.KVH);
-  const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)a.cap;
-  // scores
-  constexpr int C = HD / 16;
-  constexpr int PASS = 4;
+  const int kvh = h / (H / a.KVH);
+  const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)cap;
+  const float* qp = a.q + (size_t)b * H * HD + (size_t)h * HD + threadIdx.x % 16;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  const int nch = (L + R - 1) / R;
+  // This thread's two 16-byte pieces of every chunk: piece o is byte o * 8192 + 1024 wave + 16 lane
+  // of the chunk, i.e. row (that / RB), column (that % RB).
+  const int off0 = wave * 1024 + lane * 16, off1 = off0 + 8192;
+  const int row0 = off0 / RB, col0 = off0 % RB, row1 = off1 / RB, col1 = off1 % RB;
+  auto issue = [&](const void* kv, int c) {
+    unsigned char* st = smem + (c % kAttnStages) * kAttnChunkBytes;
+    const int j0 = min(c * R + row0, L - 1), j1 = min(c * R + row1, L - 1);
+    const unsigned char* g = (const unsigned char*)kv;
+    lds_dma<16, true>(g + (head_base + (size_t)((first + j0) % cap)) * RB + col0, st + wave * 1024);
+    lds_dma<16, true>(g + (head_base + (size_t)((first + j1) % cap)) * RB + col1, st + 8192 + wave * 1024);
+  };
+  auto wait_chunk = [&](int c) {  // this wave's pieces of chunk c have landed
+    if (c + kAttnStages - 1 <= nch) __builtin_amdgcn_s_waitcnt(kAttnVmWait);
+    else __builtin_amdgcn_s_waitcnt(kVmWait0);
+  };
+  // ---- scores w_j = scale * dot16(q, k_j): 16 threads per key (thread i accumulating dims
+  // i, i + 16, ... with FMA, then the pairwise lane sum), keys j0 + 32 pass + group
   const int li = threadIdx.x % 16, grp = threadIdx.x / 16;
   float q[C];
-  const float* qp = a.q + (size_t)b * a.H * HD + (size_t)h * HD + li;
 #pragma unroll
   for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
-  for (int j0 = 0; j0 < L; j0 += PASS * kKeysPerPass) {
-    float kv[PASS][C];
+  // the query has arrived and no older store interleaves with the counted loads
+  __builtin_amdgcn_s_waitcnt(kVmWait0);
+  for (int c = 0; c < min(kAttnStages - 1, nch); ++c) issue(kc, c);
+  for (int c = 0; c < nch; ++c) {
+    wait_chunk(c);
+    gemm_sync(rs);  // chunk c is in LDS everywhere; every wave is done with chunk c - 1
+    if (c + kAttnStages - 1 < nch) issue(kc, c + kAttnStages - 1);
+    const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes);
 #pragma unroll
-    for (int pp = 0; pp < PASS; ++pp) {
-      const int jj = j0 + pp * kKeysPerPass + grp;
-      const size_t base = (head_base + (size_t)(jj < L ? (first + jj) % a.cap : 0)) * HD + li;
-#pragma unroll
-      for (int c = 0; c < C; ++c) kv[pp][c] = kv_ld<BF16KV>(a.kc, base + c * 16);
-    }
-#pragma unroll
-    for (int pp = 0; pp < PASS; ++pp) {
-      const int jj = j0 + pp * kKeysPerPass + grp;
+    for (int pass = 0; pass < R / 32; ++pass) {
+      const int r = pass * 32 + grp, jj = c * R + r;
+      float kv[C];
+      lds_read_strided<C, 16 * (BF16KV ? 2 : 4), BF16KV>(st + r * RB + li * (BF16KV ? 2 : 4), kv);
       float acc = 0.0f;
 #pragma unroll
-      for (int c = 0; c < C; ++c) acc = fmaf(q[c], kv[pp][c], acc);
+      for (int cc = 0; cc < C; ++cc) acc = fmaf(q[cc], kv[cc], acc);
 #pragma unroll
       for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
-      if (jj < L && li == 0) w[jj] = a.scale * (acc + 0.0f);
+      if (jj < L && li == 0) lds_write_f32(lds_addr(w + jj), scale * (acc + 0.0f));
     }
   }
-  rs.sync();
-  // softmax
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  __builtin_amdgcn_s_waitcnt(kVmWait0);
+  gemm_sync(rs);
+  // ---- softmax: max, e_j = exp(w_j - max), the sum of e_j in key order, e_j / sum
   if (wave == 0) {
     float mx = -__builtin_huge_valf();
     for (int j = lane; j < L; j += kWave) mx = fmaxf(mx, w[j]);
@@ -1294,29 +1379,29 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   const float sum = sum_slot[0];
   for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = w[j] / sum;
   rs.sync();
-  // weighted values
-  if (wave < HD / 32 && lane < 32) {
-    const int d = wave * 32 + lane;
-    constexpr int CH = 16;
-    float acc = 0.0f;
-    float cur[CH], nxt[CH];
+  // ---- out_d = mul_add(w_j, v_jd, out_d) over keys in order; thread d < HD owns dim d
+  for (int c = 0; c < min(kAttnStages - 1, nch); ++c) issue(vc, c);
+  float acc = 0.0f;
+  const int d = min((int)threadIdx.x, HD - 1);
+  for (int c = 0; c < nch; ++c) {
+    wait_chunk(c);
+    gemm_sync(rs);
+    if (c + kAttnStages - 1 < nch) issue(vc, c + kAttnStages - 1);
+    if (wave < HD / kWave) {
+      const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes) + d * (BF16KV ? 2 : 4);
 #pragma unroll
-    for (int u = 0; u < CH; ++u)
-      cur[u] = u < L ? kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + u) % a.cap)) * HD + d) : 0.0f;
-    for (int j = 0; j < L; j += CH) {
+      for (int r0 = 0; r0 < R; r0 += 8) {
+        if (c * R + r0 >= L) break;  // uniform
+        float wv[8], vv[8];
+        lds_read8_f32(lds_addr(w + c * R + r0), wv);
+        lds_read_strided<8, RB, BF16KV>(st + r0 * RB, vv);
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int jn = j + CH + u;
-        nxt[u] = jn < L ? kv_ld<BF16KV>(a.vc, (head_base + (size_t)((first + jn) % a.cap)) * HD + d) : 0.0f;
+        for (int u = 0; u < 8; ++u)
+          if (c * R + r0 + u < L) acc = fmaf(wv[u], vv[u], acc);
       }
-#pragma unroll
-      for (int u = 0; u < CH; ++u)
-        if (j + u < L) acc = fmaf(w[j + u], cur[u], acc);
-#pragma unroll
-      for (int u = 0; u < CH; ++u) cur[u] = nxt[u];
     }
-    st_co(a.out + (size_t)b * a.H * HD + (size_t)h * HD + d, acc);
   }
+  if ((int)threadIdx.x < HD) st_co(out + (size_t)b * H * HD + (size_t)h * HD + threadIdx.x, acc);
 }
 
 __device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const int* spos, unsigned char* smem,
