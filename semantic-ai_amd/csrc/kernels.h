@@ -173,15 +173,17 @@ constexpr int kGemmStages = 6;   // LDS stages of a GEMM unit (kGemmStages - 1 c
 // the low half of a dword: a 2-byte direct load fills a 4-byte LDS slot per lane) | activation
 // scales [kTileBatch][4] f32
 constexpr int kGemmStageBytes = kTileRows * 128 + kTileBatch * 128 + kTileRows * kGemmChunk * 4 + kTileBatch * kGemmChunk * 4;
-// s_waitcnt immediates (vmcnt only): at most 2 (kGemmStages - 2), 3 (kGemmStages - 2) or 0
-// vector memory operations outstanding
+constexpr int kSyncChunks = 2;   // stages consumed between two row-wave barriers
+// s_waitcnt immediates (vmcnt only): the direct loads of the kGemmStages - 2 kSyncChunks chunks
+// after the ones about to be consumed may still be in flight (2 or 3 loads per wave and chunk), or
+// none
 constexpr int vm_wait_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 2));
-constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 2));
+constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 2 * kSyncChunks));
+constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 2 * kSyncChunks));
 constexpr int kVmWait0 = vm_wait_imm(0);
 constexpr int kAttnChunkBytes = 16384;  // K or V rows per LDS stage of an attention unit
 constexpr int kAttnStages = 6;
-constexpr int kAttnVmWait = vm_wait_imm(2 * (kAttnStages - 2));  // two direct loads per wave and chunk
+constexpr int kAttnVmWait = vm_wait_imm(2 * (kAttnStages - 2 * kSyncChunks));  // two direct loads per wave and chunk
 
 // Unit families of a step program.  The persistent kernel is compiled for a few family sets, so
 // that a program is run by a kernel holding only the registers of the units it has.

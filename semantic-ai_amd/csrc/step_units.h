@@ -1102,35 +1102,42 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
     }
   };
   const int nch = (nb + kGemmChunk - 1) / kGemmChunk;
+  constexpr int S = kSyncChunks, AHEAD = kGemmStages - kSyncChunks;  // chunks per sync, chunks issued ahead
   __builtin_amdgcn_s_waitcnt(kVmWait0);  // no older stores interleave with the counted loads
-  for (int c = 0; c < min(kGemmStages - 1, nch); ++c) issue(c);
+  for (int c = 0; c < min(AHEAD, nch); ++c) issue(c);
   const int r0 = 16 * (wave / 4), c0 = 16 * (wave % 4);
   const int g = lane / 16, ja = r0 + lane % 16, jb = c0 + lane % 16;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c = 0; c < nch; ++c) {
-    // this wave's loads of chunk c have landed (later chunks may still be in flight)
-    if (c + kGemmStages - 1 <= nch) {
+  for (int c = 0; c < nch; c += S) {
+    // this wave's loads of chunks c .. c + S - 1 have landed (later chunks may still be in flight)
+    if (c + AHEAD <= nch) {
       if (wave < 6) __builtin_amdgcn_s_waitcnt(kVmWait2);
       else __builtin_amdgcn_s_waitcnt(kVmWait3);
     } else {
       __builtin_amdgcn_s_waitcnt(kVmWait0);
     }
-    gemm_sync(rs);  // chunk c is in LDS everywhere; every wave is done with chunk c - 1
-    if (c + kGemmStages - 1 < nch) issue(c + kGemmStages - 1);
-    GemmOps o;
-    gemm_read(gemm_stage(smem, c % kGemmStages), ja, jb, g, r0, o);
-    const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
+    gemm_sync(rs);  // chunks c .. are in LDS everywhere; every wave is done with the chunks before
 #pragma unroll
-    for (int kk = 0; kk < kGemmChunk; ++kk) {
-      if (kGemmChunk * c + kk >= nb) break;  // uniform
-      v4i cc = {0, 0, 0, 0};
-      cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], cc, 0, 0, 0);
+    for (int u = 0; u < S; ++u)
+      if (c + AHEAD + u < nch) issue(c + AHEAD + u);
+#pragma unroll 1
+    for (int u = 0; u < S; ++u) {
+      if (c + u >= nch) break;  // uniform
+      GemmOps o;
+      gemm_read(gemm_stage(smem, (c + u) % kGemmStages), ja, jb, g, r0, o);
+      const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t dwp = kk == 0 ? o.dw[i].x : (kk == 1 ? o.dw[i].y : (kk == 2 ? o.dw[i].z : o.dw[i].w));
-        const float dw = f16_to_f32((uint16_t)(dwp & 0xFFFF));
-        const float t = (float)cc[i] * dw;
-        acc[i] = acc[i] + t * dxs[kk];
+      for (int kk = 0; kk < kGemmChunk; ++kk) {
+        if (kGemmChunk * (c + u) + kk >= nb) break;  // uniform
+        v4i cc = {0, 0, 0, 0};
+        cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], cc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t dwp = kk == 0 ? o.dw[i].x : (kk == 1 ? o.dw[i].y : (kk == 2 ? o.dw[i].z : o.dw[i].w));
+          const float dw = f16_to_f32((uint16_t)(dwp & 0xFFFF));
+          const float t = (float)cc[i] * dw;
+          acc[i] = acc[i] + t * dxs[kk];
+        }
       }
     }
   }
@@ -1333,8 +1340,9 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
     lds_dma<16, true>(g + (head_base + (size_t)((first + j0) % cap)) * RB + col0, st + wave * 1024);
     lds_dma<16, true>(g + (head_base + (size_t)((first + j1) % cap)) * RB + col1, st + 8192 + wave * 1024);
   };
-  auto wait_chunk = [&](int c) {  // this wave's pieces of chunk c have landed
-    if (c + kAttnStages - 1 <= nch) __builtin_amdgcn_s_waitcnt(kAttnVmWait);
+  constexpr int S = kSyncChunks, AHEAD = kAttnStages - kSyncChunks;  // chunks per sync, chunks issued ahead
+  auto wait_chunks = [&](int c) {  // this wave's pieces of chunks c .. c + S - 1 have landed
+    if (c + AHEAD <= nch) __builtin_amdgcn_s_waitcnt(kAttnVmWait);
     else __builtin_amdgcn_s_waitcnt(kVmWait0);
   };
   // ---- scores w_j = scale * dot16(q, k_j): 16 threads per key (thread i accumulating dims
@@ -1345,15 +1353,19 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
   // the query has arrived and no older store interleaves with the counted loads
   __builtin_amdgcn_s_waitcnt(kVmWait0);
-  for (int c = 0; c < min(kAttnStages - 1, nch); ++c) issue(kc, c);
-  for (int c = 0; c < nch; ++c) {
-    wait_chunk(c);
-    gemm_sync(rs);  // chunk c is in LDS everywhere; every wave is done with chunk c - 1
-    if (c + kAttnStages - 1 < nch) issue(kc, c + kAttnStages - 1);
-    const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes);
+  for (int c = 0; c < min(AHEAD, nch); ++c) issue(kc, c);
+  for (int c0 = 0; c0 < nch; c0 += S) {
+    wait_chunks(c0);
+    gemm_sync(rs);  // chunks c0 .. are in LDS everywhere; every wave is done with the chunks before
 #pragma unroll
-    for (int pass = 0; pass < R / 32; ++pass) {
-      const int r = pass * 32 + grp, jj = c * R + r;
+    for (int u = 0; u < S; ++u)
+      if (c0 + AHEAD + u < nch) issue(kc, c0 + AHEAD + u);
+#pragma unroll 1
+    for (int pass = 0; pass < S * R / 32; ++pass) {
+      const int c = c0 + pass / (R / 32);
+      if (c >= nch) break;  // uniform
+      const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes);
+      const int r = (pass % (R / 32)) * 32 + grp, jj = c * R + r;
       float kv[C];
       lds_read_strided<C, 16 * (BF16KV ? 2 : 4), BF16KV>(st + r * RB + li * (BF16KV ? 2 : 4), kv);
       float acc = 0.0f;
@@ -1380,14 +1392,19 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = w[j] / sum;
   rs.sync();
   // ---- out_d = mul_add(w_j, v_jd, out_d) over keys in order; thread d < HD owns dim d
-  for (int c = 0; c < min(kAttnStages - 1, nch); ++c) issue(vc, c);
+  for (int c = 0; c < min(AHEAD, nch); ++c) issue(vc, c);
   float acc = 0.0f;
   const int d = min((int)threadIdx.x, HD - 1);
-  for (int c = 0; c < nch; ++c) {
-    wait_chunk(c);
+  for (int c0 = 0; c0 < nch; c0 += S) {
+    wait_chunks(c0);
     gemm_sync(rs);
-    if (c + kAttnStages - 1 < nch) issue(vc, c + kAttnStages - 1);
-    if (wave < HD / kWave) {
+#pragma unroll
+    for (int u = 0; u < S; ++u)
+      if (c0 + AHEAD + u < nch) issue(vc, c0 + AHEAD + u);
+#pragma unroll 1
+    for (int u = 0; u < S; ++u) {
+      const int c = c0 + u;
+      if (c >= nch || wave >= HD / kWave) break;  // uniform
       const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes) + d * (BF16KV ? 2 : 4);
 #pragma unroll
       for (int r0 = 0; r0 < R; r0 += 8) {
@@ -1396,8 +1413,8 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
         lds_read8_f32(lds_addr(w + c * R + r0), wv);
         lds_read_strided<8, RB, BF16KV>(st + r0 * RB, vv);
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (c * R + r0 + u < L) acc = fmaf(wv[u], vv[u], acc);
+        for (int k = 0; k < 8; ++k)
+          if (c * R + r0 + k < L) acc = fmaf(wv[k], vv[k], acc);
       }
     }
   }
