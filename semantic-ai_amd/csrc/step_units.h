@@ -1218,8 +1218,7 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
       for (; c < chunks; ++c) acc = fmaf(xs[c * 16 + li], ldg(w + (size_t)c * 16), acc);
     }
     // pairwise lane sum: acc[i] += acc[i + width] for width 8, 4, 2, 1
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
+    acc = row16_pairwise_sum(acc);
     if (li == 0) {
       float tail = 0.0f;
       for (int i = chunks * 16; i < K; ++i) {
@@ -1294,6 +1293,43 @@ __device__ __forceinline__ void lds_read_strided(uint32_t addr, float (&v)[N]) {
   for (int i = 0; i < N; ++i) v[i] = BF16 ? __uint_as_float(r[i] << 16) : __uint_as_float(r[i]);
 }
 
+// The values phase's operands of 16 keys in one round trip: wv = 16 consecutive f32 at waddr
+// (16-byte aligned), vv[i] = the f32 (BF16: the widened bf16) at vaddr + i * STEP.
+template <int STEP, bool BF16>
+__device__ __forceinline__ void lds_read_wv16(uint32_t waddr, uint32_t vaddr, float (&wv)[16], float (&vv)[16]) {
+  float4 w0, w1, w2, w3;
+  uint32_t r[16];
+#define SVL_V16(OP)                                                                                              \
+  asm volatile("ds_read_b128 %0, %20\n\tds_read_b128 %1, %20 offset:16\n\t"                                     \
+               "ds_read_b128 %2, %20 offset:32\n\tds_read_b128 %3, %20 offset:48\n\t"                           \
+               OP " %4, %21\n\t" OP " %5, %21 offset:%22\n\t" OP " %6, %21 offset:%23\n\t"                      \
+               OP " %7, %21 offset:%24\n\t" OP " %8, %21 offset:%25\n\t" OP " %9, %21 offset:%26\n\t"           \
+               OP " %10, %21 offset:%27\n\t" OP " %11, %21 offset:%28\n\t" OP " %12, %21 offset:%29\n\t"        \
+               OP " %13, %21 offset:%30\n\t" OP " %14, %21 offset:%31\n\t" OP " %15, %21 offset:%32\n\t"        \
+               OP " %16, %21 offset:%33\n\t" OP " %17, %21 offset:%34\n\t" OP " %18, %21 offset:%35\n\t"        \
+               OP " %19, %21 offset:%36\n\ts_waitcnt lgkmcnt(0)"                                                  \
+               : "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3), "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]),    \
+                 "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]),       \
+                 "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]), "=&v"(r[15])                            \
+               : "v"(waddr), "v"(vaddr), "i"(STEP), "i"(2 * STEP), "i"(3 * STEP), "i"(4 * STEP), "i"(5 * STEP),  \
+                 "i"(6 * STEP), "i"(7 * STEP), "i"(8 * STEP), "i"(9 * STEP), "i"(10 * STEP), "i"(11 * STEP),      \
+                 "i"(12 * STEP), "i"(13 * STEP), "i"(14 * STEP), "i"(15 * STEP)                                   \
+               : "memory")
+  if constexpr (BF16) SVL_V16("ds_read_u16");
+  else SVL_V16("ds_read_b32");
+#undef SVL_V16
+  const float4 ws[4] = {w0, w1, w2, w3};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wv[4 * i] = ws[i].x;
+    wv[4 * i + 1] = ws[i].y;
+    wv[4 * i + 2] = ws[i].z;
+    wv[4 * i + 3] = ws[i].w;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) vv[i] = BF16 ? __uint_as_float(r[i] << 16) : __uint_as_float(r[i]);
+}
+
 // Eight consecutive f32 at a 16-byte aligned LDS byte address.
 __device__ __forceinline__ void lds_read8_f32(uint32_t addr, float (&v)[8]) {
   float4 x, y;
@@ -1353,6 +1389,7 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
   // the query has arrived and no older store interleaves with the counted loads
   __builtin_amdgcn_s_waitcnt(kVmWait0);
+  float mx = -__builtin_huge_valf();  // running maximum of this thread's scores
   for (int c = 0; c < min(AHEAD, nch); ++c) issue(kc, c);
   for (int c0 = 0; c0 < nch; c0 += S) {
     wait_chunks(c0);
@@ -1371,22 +1408,25 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
       float acc = 0.0f;
 #pragma unroll
       for (int cc = 0; cc < C; ++cc) acc = fmaf(q[cc], kv[cc], acc);
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, 16);
-      if (jj < L && li == 0) lds_write_f32(lds_addr(w + jj), scale * (acc + 0.0f));
+      acc = row16_pairwise_sum(acc);
+      if (jj < L && li == 0) {
+        const float sc = scale * (acc + 0.0f);
+        lds_write_f32(lds_addr(w + jj), sc);
+        mx = fmaxf(mx, sc);
+      }
     }
   }
+  // ---- softmax: max (exact in any order), e_j = exp(w_j - max), the sum of e_j in key order,
+  // e_j / sum
+  mx = wave_max(mx);
+  if (lane == 0) lds_write_f32(lds_addr(sum_slot + 4 + wave), mx);
   __builtin_amdgcn_s_waitcnt(kVmWait0);
   gemm_sync(rs);
-  // ---- softmax: max, e_j = exp(w_j - max), the sum of e_j in key order, e_j / sum
-  if (wave == 0) {
-    float mx = -__builtin_huge_valf();
-    for (int j = lane; j < L; j += kWave) mx = fmaxf(mx, w[j]);
-    mx = wave_max(mx);
-    for (int j = lane; j < L; j += kWave) w[j] = ref_exp(w[j] - mx);
-    wave_lds_fence();
-    if (lane == 0) sum_slot[0] = ordered_sum(w, L);
-  }
+#pragma unroll
+  for (int v = 0; v < kRowWaves; ++v) mx = fmaxf(mx, sum_slot[4 + v]);
+  for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = ref_exp(w[j] - mx);
+  rs.sync();
+  if (threadIdx.x == 0) sum_slot[0] = ordered_sum(w, L);
   rs.sync();
   const float sum = sum_slot[0];
   for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = w[j] / sum;
@@ -1407,13 +1447,12 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
       if (c >= nch || wave >= HD / kWave) break;  // uniform
       const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes) + d * (BF16KV ? 2 : 4);
 #pragma unroll
-      for (int r0 = 0; r0 < R; r0 += 8) {
+      for (int r0 = 0; r0 < R; r0 += 16) {
         if (c * R + r0 >= L) break;  // uniform
-        float wv[8], vv[8];
-        lds_read8_f32(lds_addr(w + c * R + r0), wv);
-        lds_read_strided<8, RB, BF16KV>(st + r0 * RB, vv);
+        float wv[16], vv[16];
+        lds_read_wv16<RB, BF16KV>(lds_addr(w + c * R + r0), st + r0 * RB, wv, vv);
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < 16; ++k)
           if (c * R + r0 + k < L) acc = fmaf(wv[k], vv[k], acc);
       }
     }
