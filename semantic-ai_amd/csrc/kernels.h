@@ -6,12 +6,16 @@
 
 namespace svl {
 
-enum WeightFmt { FMT_F32 = 0, FMT_BF16 = 1, FMT_Q8_0 = 3, FMT_Q4K = 4 };
+enum WeightFmt { FMT_F32 = 0, FMT_BF16 = 1, FMT_Q8_0 = 3, FMT_Q4K = 4, FMT_F32C = 5, FMT_BF16C = 6 };
 enum NormKind { NORM_NONE = 0, NORM_LAYER = 1, NORM_RMS = 2 };
 enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 3, EPI_GELU = 4 };
 
 // One linear layer as held on the device.
 //   FMT_F32 / FMT_BF16: w = [out][in] row-major.
+//   FMT_F32C / FMT_BF16C: chain-packed dense weights, for in % (16 E) == 0 with E = 4 (f32) or
+//     8 (bf16) elements per 16 bytes: element (row, 16 c + l) is at
+//     ((row * in / (16 E) + c / E) * 16 + l) * E + c % E, i.e. the 16 lane chains of a row are
+//     interleaved 16 bytes at a time.
 //   FMT_Q8_0: w = int8 quants [out][in]; scale = f16 block scales [out][in/32].
 //   FMT_Q4K: w = 144-byte super-blocks [out][in/256]: f16 d, f16 dmin and the 12 bytes of packed
 //     6-bit sub-block scales and mins exactly as candle's BlockQ4K holds them, then the 128 quant
@@ -161,6 +165,7 @@ constexpr int kStepThreads = 1024;                       // workgroup of the ste
 constexpr int kRowThreads = 512;                         // row waves: threads [0, 512)
 constexpr int kWeightThreads = kStepThreads - kRowThreads;  // weight waves: threads [512, 1024)
 constexpr int kWBlocks = 6;                              // Q8_0 blocks per weight-wave thread and unit
+constexpr int kDenseBatch = 16;                          // 16-byte loads in flight per dense weight-wave thread
 constexpr int kQ4Blocks = 2;                             // Q4K super-blocks per weight-wave thread and unit
 constexpr int kQ4Terms = 9;   // f32 terms per Q4K super-block and row: 8 lane sums and the min term
 constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8_0 linears as MFMA GEMMs
@@ -210,6 +215,8 @@ hipError_t launch_q8_to_blocks(const int8_t* qs, const uint16_t* d, int rows, in
 hipError_t launch_q4k_quantize(const float* w, int rows, int K, uint8_t* blocks, hipStream_t s);
 hipError_t launch_q4k_from_blocks(const uint8_t* candle, int rows, int K, uint8_t* blocks, hipStream_t s);
 hipError_t launch_q4k_to_blocks(const uint8_t* blocks, int rows, int K, uint8_t* candle, hipStream_t s);
+// Row-major [rows][K] f32 or bf16 (src_bf16) -> chain-packed FMT_F32C (dst_bf16 = 0) or FMT_BF16C.
+hipError_t launch_chain_pack(const void* src, int src_bf16, int rows, int K, void* dst, int dst_bf16, hipStream_t s);
 hipError_t launch_dequant(const LinearDev& L, float* out, hipStream_t s);
 hipError_t launch_f16_to_f32(const uint16_t* x, float* y, size_t n, hipStream_t s);
 hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, size_t n, hipStream_t s);

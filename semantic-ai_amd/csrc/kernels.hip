@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) {
-    if constexpr ((F & (FAM_Q8 | FAM_Q4K)) != 0) weight_waves<F>(P, &ws, smem);
+    if constexpr ((F & (FAM_Q8 | FAM_Q4K | FAM_DENSE)) != 0) weight_waves<F>(P, &ws, smem);
     return;
   }
   RowSync rs{&ws, 0u};
@@ -122,7 +122,12 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, 
   if (threadIdx.x >= kRowThreads) {
     if (is_split_gemv(d_ph)) {
       if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
-      if (ld_const(&d_ph->g.L.fmt) == FMT_Q4K) {
+      const int fmt = ld_const(&d_ph->g.L.fmt);
+      if (is_chained_dense(fmt)) {
+        const bool ok = fmt == FMT_BF16C ? w_dense<true>(d_ph, blockIdx.x, &ws, smem, 0)
+                                         : w_dense<false>(d_ph, blockIdx.x, &ws, smem, 0);
+        if (!ok) return;
+      } else if (fmt == FMT_Q4K) {
         WItemQ4 it;
         w_issue_q4k(d_ph, blockIdx.x, it);
         if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
@@ -208,6 +213,14 @@ void plan_gemv(GemvArgs& g, int grid, int* units) {
     g.ipw = ipw;
     g.maxb = (per_row * ipw * nb + kWeightThreads - 1) / kWeightThreads;
     if (g.maxb > kQ4Blocks) g.maxb = kQ4Blocks;
+  } else if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C) {
+    // About one unit per workgroup and batch row, at most 64 rows (two weight-wave passes).
+    const int per_row = silu ? 2 : 1;
+    int ipw = (items + grid - 1) / grid;
+    if (g.epi == EPI_QKV_ROPE && (ipw & 1)) ++ipw;
+    if (ipw > 64 / per_row) ipw = 64 / per_row;
+    g.ipw = ipw;
+    g.maxb = 0;
   } else {
     g.ipw = silu ? kRowThreads / 32 : kRowThreads / 16;
     g.maxb = 0;
@@ -239,6 +252,8 @@ size_t phase_smem(const Phase& ph) {
         return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
                (size_t)nb * kQ4Terms * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
+      if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C)
+        return (size_t)K * 4 + (size_t)16 * (K / 16 + 4) * 4 + (size_t)2 * g.ipw * 4 + 64;
       return (size_t)K * 4 + (kRowThreads / 16) * 4 + 64;
     }
     case PH_ATTN:
@@ -493,6 +508,33 @@ __device__ float q4k_value(const uint8_t* b, int e) {
   return t - m1;
 }
 
+// Position of element (row, col) of a [rows][K] matrix in the chain-packed layout with E elements
+// per 16 bytes.
+__host__ __device__ inline size_t chain_index(size_t row, int col, int K, int E) {
+  const int l = col % 16, c = col / 16;
+  return ((row * (K / (16 * E)) + c / E) * 16 + l) * E + c % E;
+}
+
+__global__ void chain_pack_kernel(const void* src, int src_bf16, size_t n, int K, void* dst, int dst_bf16) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const size_t row = i / K;
+  const int col = (int)(i % K);
+  const size_t o = chain_index(row, col, K, dst_bf16 ? 8 : 4);
+  if (dst_bf16) {
+    ((uint16_t*)dst)[o] = src_bf16 ? ((const uint16_t*)src)[i] : f32_to_bf16(((const float*)src)[i]);
+  } else {
+    ((float*)dst)[o] = src_bf16 ? bf16_to_f32(((const uint16_t*)src)[i]) : ((const float*)src)[i];
+  }
+}
+
+hipError_t launch_chain_pack(const void* src, int src_bf16, int rows, int K, void* dst, int dst_bf16, hipStream_t s) {
+  const size_t n = (size_t)rows * K;
+  hipLaunchKernelGGL(chain_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, src_bf16, n, K, dst,
+                     dst_bf16);
+  return hipGetLastError();
+}
+
 // Dequantization: Q8_0 closed form q * f32(d); Q4K closed form; dense bf16 widening; f32 copy.
 __global__ void dequant_kernel(LinearDev L, float* out) {
   size_t n = (size_t)L.out * L.in;
@@ -501,6 +543,8 @@ __global__ void dequant_kernel(LinearDev L, float* out) {
   if (L.fmt == FMT_Q8_0) out[i] = (float)((const int8_t*)L.w)[i] * f16_to_f32(L.scale[i / 32]);
   else if (L.fmt == FMT_Q4K) out[i] = q4k_value((const uint8_t*)L.w + (i / 256) * 144, (int)(i % 256));
   else if (L.fmt == FMT_BF16) out[i] = bf16_to_f32(((const uint16_t*)L.w)[i]);
+  else if (L.fmt == FMT_BF16C) out[i] = bf16_to_f32(((const uint16_t*)L.w)[chain_index(i / L.in, (int)(i % L.in), L.in, 8)]);
+  else if (L.fmt == FMT_F32C) out[i] = ((const float*)L.w)[chain_index(i / L.in, (int)(i % L.in), L.in, 4)];
   else out[i] = ((const float*)L.w)[i];
 }
 

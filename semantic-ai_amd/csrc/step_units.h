@@ -900,7 +900,7 @@ __device__ __forceinline__ void w_terms_q4k(const WItemQ4& it, unsigned char* sm
 __device__ __forceinline__ bool is_split_gemv(const Phase* ph) {
   if (ld_const(&ph->kind) != PH_GEMV) return false;
   const int fmt = ld_const(&ph->g.L.fmt);
-  return fmt == FMT_Q8_0 || fmt == FMT_Q4K;
+  return fmt == FMT_Q8_0 || fmt == FMT_Q4K || fmt == FMT_F32C || fmt == FMT_BF16C;
 }
 
 // ---- batched Q8_0 GEMM (lockstep batches; row waves) ----------------------------------------------
@@ -1233,6 +1233,136 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
   gemv_finish(a, b, part, i0, ni, p, in, Y);
 }
 
+// ---- dense GEMV, chain-packed weights (row waves + weight waves) ---------------------------------
+// The reference's matvec with its 16-lane dot (SVL/nn/kernels/matvec.rs:239-246,
+// kernels/mod.rs:66-91): lane l of a row accumulates x[16 c + l] * w[16 c + l] over c with FMA,
+// then the pairwise lane sum.  The weights are packed so that one weight-wave thread owns one
+// lane chain of one row and reads it with 16-byte loads (FMT_F32C / FMT_BF16C); the row waves
+// put the normalized input into LDS chain-major (xT[l][c], rows padded by 4 floats against bank
+// conflicts).  A unit has up to 2 x 32 rows; the weight waves take them 32 at a time.
+
+__device__ __forceinline__ int dense_chain_stride(int K) { return K / 16 + 4; }
+
+struct DenseLds {
+  float* xs;  // [K] norm scratch
+  float* xT;  // [16][K / 16 + 4]
+  float* Y;   // [2 ipw]
+};
+
+__device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
+  DenseLds l;
+  l.xs = (float*)smem;
+  l.xT = l.xs + K;
+  l.Y = l.xT + 16 * dense_chain_stride(K);
+  return l;
+}
+
+template <int KP>
+__device__ __forceinline__ void store_row_chains(const float (&v)[KP], int K, float* xT) {
+  const int stride = dense_chain_stride(K);
+#pragma unroll
+  for (int u = 0; u < KP; ++u) {
+    const int i = threadIdx.x + u * kRowThreads;
+    if (i < K) xT[(i & 15) * stride + (i >> 4)] = v[u];
+  }
+}
+
+// Row-wave part of dense item `item`: input row, norm, the chain-major copy for the weight waves,
+// then (once they have written the row results) the epilogue.
+template <int KP>
+__device__ __forceinline__ void gemv_dense_rows(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
+                                                RowSync& rs, unsigned item) {
+  const int K = a.L.in;
+  const Q8Geom g = q8_geom(K, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
+  const DenseLds l = dense_lds(smem, K);
+  const int p = spos[g.b];
+  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
+  constexpr bool kNorm = KP <= 8;
+  NormW<kNorm ? KP : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
+  float v[KP];
+  load_row(a.x + (size_t)g.b * a.x_stride, K, v, &rs.ws->r_issued);
+  if constexpr (kNorm) {
+    if (a.norm != NORM_NONE) norm_regs(v, K, a.norm, nwt, a.eps, l.xs, rs);
+  }
+  // the weight waves are done with the previous item's input and results
+  lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
+  store_row_chains(v, K, l.xT);
+  lds_signal(&rs.ws->xq_parts);
+  if ((int)(threadIdx.x & ~(kWave - 1)) >= g.ni && threadIdx.x != 0) return;  // waves without epilogue rows
+  lds_wait(&rs.ws->t_parts, (item + 1) * kWeightWaves, &rs.ws->stop);
+  gemv_finish(a, g.b, g.part, g.i0, g.ni, p, in, l.Y);
+}
+
+// Weight-wave part of a dense item: issue the first loads of the thread's lane chain as soon as
+// the row waves have requested the input row, wait for the chain-major input, then stream the
+// chain (kDenseBatch loads in flight), sum the 16 lanes and write the row result.
+template <bool BF16W>
+__device__ __forceinline__ bool w_dense(const Phase* ph, int unit, WgSync* ws, unsigned char* smem, unsigned item) {
+  constexpr int EPL = BF16W ? 8 : 4;  // elements per 16-byte load
+  const int K = ld_const(&ph->g.L.in);
+  const int epi = ld_const(&ph->g.epi);
+  const int ff_hidden = ld_const(&ph->g.ff_hidden);
+  const int items = epi == EPI_SILU_GATE ? ff_hidden : ld_const(&ph->g.L.out);
+  const int ipw = ld_const(&ph->g.ipw);
+  const Q8Geom g = q8_geom(K, items, ipw, ld_const(&ph->g.parts), epi == EPI_SILU_GATE, unit);
+  const unsigned char* wbase = (const unsigned char*)ld_const(&ph->g.L.w);
+  const DenseLds l = dense_lds(smem, K);
+  const int stride = dense_chain_stride(K);
+  const int NL = K / (16 * EPL);  // loads per chain
+  const int w = threadIdx.x - kRowThreads;
+  const int rr = w / 16, lane16 = w % 16;
+  bool ready = false;
+  for (int r0 = 0; r0 < g.NR; r0 += 32) {
+    const int r = r0 + rr;
+    const size_t row = (size_t)gemv_phys_row(epi, ff_hidden, g.i0, g.ni, min(r, g.NR - 1));
+    const v4i* src = (const v4i*)(wbase + (row * NL * 16 + lane16) * 16);  // load k at src[16 k]
+    v4i buf[kDenseBatch];
+#pragma unroll
+    for (int u = 0; u < kDenseBatch; ++u) buf[u] = ldg_stream(src + 16 * min(u, NL - 1));
+    if (!ready) {
+      if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return false;
+      ready = true;
+    }
+    const float* xc = l.xT + lane16 * stride;
+    float acc = 0.0f;
+    const bool stream = NL > kDenseBatch;  // uniform: more loads than fit in flight
+    for (int k0 = 0; k0 < NL; k0 += kDenseBatch) {
+#pragma unroll
+      for (int u = 0; u < kDenseBatch; ++u) {
+        const int k = k0 + u;
+        if (k < NL) {  // uniform
+        const v4i wv = buf[u];
+        if (stream) buf[u] = ldg_stream(src + 16 * min(k + kDenseBatch, NL - 1));
+        float xv[EPL];
+        if constexpr (BF16W) {
+          const float4 x0 = *(const float4*)(xc + k * 8), x1 = *(const float4*)(xc + k * 8 + 4);
+          xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
+          xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
+          const uint32_t wd[4] = {(uint32_t)wv.x, (uint32_t)wv.y, (uint32_t)wv.z, (uint32_t)wv.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc = fmaf(xv[e], __uint_as_float(e & 1 ? (wd[e / 2] & 0xFFFF0000u) : (wd[e / 2] << 16)), acc);
+        } else {
+          const float4 x0 = *(const float4*)(xc + k * 4);
+          xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w;
+          acc = fmaf(xv[0], __int_as_float(wv.x), acc);
+          acc = fmaf(xv[1], __int_as_float(wv.y), acc);
+          acc = fmaf(xv[2], __int_as_float(wv.z), acc);
+          acc = fmaf(xv[3], __int_as_float(wv.w), acc);
+        }
+        }
+      }
+    }
+    acc = row16_pairwise_sum(acc);
+    if (lane16 == 0 && r < g.NR) l.Y[r] = acc;
+  }
+  if (!ready && !lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return false;
+  return true;
+}
+
+__device__ __forceinline__ bool is_chained_dense(int fmt) { return fmt == FMT_F32C || fmt == FMT_BF16C; }
+
 // ---- attention unit (row waves) ------------------------------------------------------------------
 // One unit per (stream, head).  The query at position p attends to keys
 // max(0, p - window + 1) ..= p (transformer.rs:385) in the ring, in the reference's order
@@ -1451,9 +1581,14 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
         if (c * R + r0 >= L) break;  // uniform
         float wv[16], vv[16];
         lds_read_wv16<RB, BF16KV>(lds_addr(w + c * R + r0), st + r0 * RB, wv, vv);
+        if (c * R + r0 + 16 <= L) {  // uniform
 #pragma unroll
-        for (int k = 0; k < 16; ++k)
-          if (c * R + r0 + k < L) acc = fmaf(wv[k], vv[k], acc);
+          for (int k = 0; k < 16; ++k) acc = fmaf(wv[k], vv[k], acc);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 16; ++k)
+            if (c * R + r0 + k < L) acc = fmaf(wv[k], vv[k], acc);
+        }
       }
     }
   }
@@ -1632,6 +1767,16 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
     ++item;
     return;
   }
+  if ((F & FAM_DENSE) && ph.kind == PH_GEMV && is_chained_dense(ph.g.L.fmt)) {
+    switch (row_slots(ph.g.L.in)) {
+      case 2: gemv_dense_rows<2>(ph.g, unit, spos, smem, rs, item); break;
+      case 4: gemv_dense_rows<4>(ph.g, unit, spos, smem, rs, item); break;
+      case 8: gemv_dense_rows<8>(ph.g, unit, spos, smem, rs, item); break;
+      default: gemv_dense_rows<kMaxSlots>(ph.g, unit, spos, smem, rs, item); break;
+    }
+    ++item;
+    return;
+  }
   if ((F & FAM_Q4K) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q4K) {
     switch (row_slots(ph.g.L.in)) {
       case 2: gemv_q4k_rows<2>(ph.g, unit, spos, smem, rs, item); break;
@@ -1738,12 +1883,17 @@ __device__ __forceinline__ void weight_waves(const StepParams& P, WgSync* ws, un
     // the blocks are requested right after the row waves have requested the item's input row,
     // so that neither the row nor the row waves' stores and barrier traffic queue behind them
     if (!lds_wait<true>(&ws->r_issued, (item + 1) * kRowWaves, &ws->stop)) return;
-    if ((F & FAM_Q4K) && (!(F & FAM_Q8) || ld_const(&P.prog[p].g.L.fmt) == FMT_Q4K)) {
+    const int fmt = ld_const(&P.prog[p].g.L.fmt);
+    if ((F & FAM_DENSE) && is_chained_dense(fmt)) {
+      const bool ok = fmt == FMT_BF16C ? w_dense<true>(P.prog + p, u, ws, smem, item)
+                                       : w_dense<false>(P.prog + p, u, ws, smem, item);
+      if (!ok) return;
+    } else if ((F & FAM_Q4K) && (!(F & FAM_Q8) || fmt == FMT_Q4K)) {
       WItemQ4 it4;
       w_issue_q4k(P.prog + p, u, it4);
       if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return;
       w_terms_q4k(it4, smem);
-    } else {
+    } else if constexpr ((F & FAM_Q8) != 0) {
       WItem it;
       w_issue(P.prog + p, u, it);
       if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return;

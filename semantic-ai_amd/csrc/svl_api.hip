@@ -282,14 +282,39 @@ int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string&
     if (in_f % 8) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: bf16 rows need in %% 8 == 0", name.c_str());
     void* w;
     TRY(m->alloc(&w, count * 2));
-    HIP_TRY(hipMemcpy(w, t->data, count * 2, hipMemcpyHostToDevice));
-    L->fmt = FMT_BF16;
+    if (in_f % 128 == 0) {  // chain-packed for the weight waves
+      void* tmp;
+      HIP_TRY(hipMalloc(&tmp, count * 2));
+      hipError_t e = hipMemcpy(tmp, t->data, count * 2, hipMemcpyHostToDevice);
+      if (e == hipSuccess) e = launch_chain_pack(tmp, 1, out_f, in_f, w, 1, m->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+      hipFree(tmp);
+      HIP_TRY(e);
+      L->fmt = FMT_BF16C;
+    } else {
+      HIP_TRY(hipMemcpy(w, t->data, count * 2, hipMemcpyHostToDevice));
+      L->fmt = FMT_BF16;
+    }
     L->w = w;
     return 0;
   }
   if (in_f % 4) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: f32 rows need in %% 4 == 0", name.c_str());
   float* f = nullptr;
   TRY(upload_f32(m, t, count, &f));
+  if (in_f % 64 == 0) {  // chain-packed for the weight waves
+    void* w;
+    TRY(m->alloc(&w, count * 4));
+    HIP_TRY(launch_chain_pack(f, 0, out_f, in_f, w, 0, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    // the row-major staging copy is released right away
+    m->allocs.pop_back();
+    m->allocs.pop_back();
+    hipFree(f);
+    m->allocs.push_back(w);
+    L->fmt = FMT_F32C;
+    L->w = w;
+    return 0;
+  }
   L->fmt = FMT_F32;
   L->w = f;
   return 0;
