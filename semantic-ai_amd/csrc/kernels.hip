@@ -43,10 +43,10 @@ __device__ __forceinline__ bool grid_barrier(SyncState* s, unsigned gen, unsigne
   bool ok = true;
   unsigned spins = 0;
   for (;;) {
+    // lanes < ngroups read the group counters, the others the abort flag
     const unsigned v = __hip_atomic_load(gbl(ctr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned ab = __hip_atomic_load(gbl(&s->abort_flag[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool waiting = lane < (int)ngroups && (int)(v - target) < 0;
-    if (ab || lds_ld(&ws->stop)) {
+    if (__any(lane >= (int)ngroups && v != 0u) || lds_ld(&ws->stop)) {
       ok = false;
       break;
     }
