@@ -446,7 +446,7 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, 
 __device__ __forceinline__ int term_stride(int ipw) { return 2 * ipw + 1; }
 
 // acc = 0; acc += T[blk * ts + r] for blk = 0 .. nb-1 in order; each batch of 32 terms is
-// read before its additions.
+// read before its additions, the last partial batch too.
 __device__ __forceinline__ float ordered_row_sum(const float* T, int ts, int r, int nb) {
   constexpr int U = 32;
   const float* t = T + r;
@@ -460,7 +460,14 @@ __device__ __forceinline__ float ordered_row_sum(const float* T, int ts, int r, 
 #pragma unroll
     for (int u = 0; u < U; ++u) acc = acc + v[u];
   }
-  for (; blk < nb; ++blk) acc = acc + t[blk * ts];
+  if (blk < nb) {  // the last partial batch, read at once (indices past nb read the last term)
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = t[min(blk + u, nb - 1) * ts];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = blk + u < nb ? acc + v[u] : acc;
+  }
   return acc;
 }
 
