@@ -169,7 +169,7 @@ constexpr int kDenseBatch = 16;                          // 16-byte loads in fli
 constexpr int kQ4Blocks = 2;                             // Q4K super-blocks per weight-wave thread and unit
 constexpr int kQ4Terms = 9;   // f32 terms per Q4K super-block and row: 8 lane sums and the min term
 constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8_0 linears as MFMA GEMMs
-constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit
+constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit (or 16)
 constexpr int kTileBatch = 64;   // batch rows of a GEMM unit
 constexpr int kMaxBatch = 1024;
 constexpr int kGemmChunk = 4;    // Q8_0 blocks (128 bytes of K) per LDS stage of a GEMM unit
@@ -185,6 +185,7 @@ constexpr int kSyncChunks = 2;   // stages consumed between two row-wave barrier
 constexpr int vm_wait_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 2 * kSyncChunks));
 constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 2 * kSyncChunks));
+constexpr int kVmWait1 = vm_wait_imm(1 * (kGemmStages - 2 * kSyncChunks));
 constexpr int kVmWait0 = vm_wait_imm(0);
 constexpr int kAttnChunkBytes = 16384;  // K or V rows per LDS stage of an attention unit
 constexpr int kAttnStages = 6;
@@ -206,8 +207,9 @@ int step_program_grid(int device);
 size_t phase_smem(const Phase& ph);
 // Fills the unit layout of a GEMV phase (ipw, parts, maxb, units) for `grid` workgroups.
 void plan_gemv(GemvArgs& g, int grid, int* units);
-// Unit layout of a batched Q8_0 GEMM phase (units = row tiles x batch tiles; parts = row tiles).
-void plan_qgemm(GemvArgs& g, int* units);
+// Unit layout of a batched Q8_0 GEMM phase (units = row tiles x batch tiles; parts = row tiles):
+// 32-row tiles, or 16-row tiles when they put no more units on the busiest of `grid` workgroups.
+void plan_qgemm(GemvArgs& g, int grid, int* units);
 
 hipError_t launch_q8_quantize(const float* w, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_from_blocks(const uint8_t* blocks, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);

@@ -229,13 +229,22 @@ void plan_gemv(GemvArgs& g, int grid, int* units) {
   *units = g.parts * g.B;
 }
 
-void plan_qgemm(GemvArgs& g, int* units) {
+void plan_qgemm(GemvArgs& g, int grid, int* units) {
   const bool silu = g.epi == EPI_SILU_GATE;
   const int items = silu ? g.ff_hidden : g.L.out;
-  g.ipw = silu ? kTileRows / 2 : kTileRows;
+  const int btiles = (g.B + kTileBatch - 1) / kTileBatch;
+  // a unit's time depends little on its rows (it is bound by the per-chunk latency), so 16-row
+  // tiles are used only when they add no unit to the busiest workgroup
+  auto busiest_units = [&](int tr) {
+    const int ipw = silu ? tr / 2 : tr;
+    const int u = (items + ipw - 1) / ipw * btiles;
+    return (u + grid - 1) / grid;
+  };
+  const int tr = busiest_units(kTileRows / 2) <= busiest_units(kTileRows) ? kTileRows / 2 : kTileRows;
+  g.ipw = silu ? tr / 2 : tr;
   g.parts = (items + g.ipw - 1) / g.ipw;
   g.maxb = 0;
-  *units = g.parts * ((g.B + kTileBatch - 1) / kTileBatch);
+  *units = g.parts * btiles;
 }
 
 size_t phase_smem(const Phase& ph) {

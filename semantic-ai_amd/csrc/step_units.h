@@ -1068,6 +1068,7 @@ __device__ __forceinline__ void gemm_read(const GemmStage& st, int ja, int jb, i
       : "memory");
 }
 
+template <int TR>  // tile rows: 32 (waves 0-7 compute) or 16 (waves 0-3 compute)
 __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
                                            RowSync& rs) {
   const int K = a.L.in, nb = K / 32;
@@ -1080,17 +1081,18 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
   const int nbat = min(kTileBatch, a.B - b0);
   float* Y = (float*)smem;            // [kTileRows][kTileBatch]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
-  // ---- loads of one chunk: wave w brings X rows 8w..8w+7; waves 0-3 W rows 8w..8w+7, waves 4-5
-  // the weight scales of rows 16 (w - 4) .., waves 6-7 the activation scales of batch rows
-  // 32 (w - 6) .. (two loads).  Rows past the tile load the last row in use; blocks past K load
-  // the last block (their results are never used).
+  // ---- loads of one chunk: wave w brings X rows 8w..8w+7.  TR = 32: waves 0-3 W rows 8w..8w+7,
+  // waves 4-5 the weight scales of rows 16 (w - 4) .., waves 6-7 the activation scales of batch
+  // rows 32 (w - 6) .. (two loads).  TR = 16: waves 0-1 W rows 8w..8w+7, wave 2 the weight
+  // scales, waves 4-7 the activation scales of batch rows 16 (w - 4) ...  Rows past the tile load
+  // the last row in use; blocks past K load the last block (their results are never used).
   const int lrow = 8 * wave + lane / 8, lslot = lane % 8;
   const int8_t* xsrc = a.xq + (size_t)(b0 + min(lrow, nbat - 1)) * K;
   const int8_t* wsrc = (const int8_t*)a.L.w +
-                       (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(wave < 4 ? lrow : 0, NR - 1)) * K;
-  const int srow = 16 * (wave & 1) + lane / 4, sblk = lane % 4;
+                       (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(wave < TR / 8 ? lrow : 0, NR - 1)) * K;
+  const int srow = (TR == 32 ? 16 * (wave & 1) : 0) + lane / 4, sblk = lane % 4;
   const uint16_t* dwsrc = a.L.scale + (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(srow, NR - 1)) * nb;
-  const int xrow0 = 32 * (wave & 1) + lane / 4;
+  const int xrow0 = (TR == 32 ? 32 * (wave & 1) : 16 * (wave & 3)) + lane / 4;
   const float* dxsrc0 = a.xdq + (size_t)(b0 + min(xrow0, nbat - 1)) * nb;
   const float* dxsrc1 = a.xdq + (size_t)(b0 + min(xrow0 + 16, nbat - 1)) * nb;
   auto issue = [&](int c) {
@@ -1099,13 +1101,19 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
     const int off = min(128 * c + 16 * seg, K - 16);
     lds_dma<16, true>(xsrc + off, st.x + wave * 1024);
     const int k = min(kGemmChunk * c + sblk, nb - 1);
-    if (wave < 4) {
-      lds_dma<16, false>(wsrc + off, st.w + wave * 1024);
-    } else if (wave < 6) {
-      lds_dma<2, false>(dwsrc + k, (unsigned char*)st.dw + (wave - 4) * 256);
+    if constexpr (TR == 32) {
+      if (wave < 4) {
+        lds_dma<16, false>(wsrc + off, st.w + wave * 1024);
+      } else if (wave < 6) {
+        lds_dma<2, false>(dwsrc + k, (unsigned char*)st.dw + (wave - 4) * 256);
+      } else {
+        lds_dma<4, true>(dxsrc0 + k, (unsigned char*)st.dx + (wave - 6) * 512);
+        lds_dma<4, true>(dxsrc1 + k, (unsigned char*)st.dx + (wave - 6) * 512 + 256);
+      }
     } else {
-      lds_dma<4, true>(dxsrc0 + k, (unsigned char*)st.dx + (wave - 6) * 512);
-      lds_dma<4, true>(dxsrc1 + k, (unsigned char*)st.dx + (wave - 6) * 512 + 256);
+      if (wave < 2) lds_dma<16, false>(wsrc + off, st.w + wave * 1024);
+      else if (wave == 2) lds_dma<2, false>(dwsrc + k, (unsigned char*)st.dw);
+      else if (wave >= 4) lds_dma<4, true>(dxsrc0 + k, (unsigned char*)st.dx + (wave - 4) * 256);
     }
   };
   const int nch = (nb + kGemmChunk - 1) / kGemmChunk;
@@ -1118,8 +1126,9 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
   for (int c = 0; c < nch; c += S) {
     // this wave's loads of chunks c .. c + S - 1 have landed (later chunks may still be in flight)
     if (c + AHEAD <= nch) {
-      if (wave < 6) __builtin_amdgcn_s_waitcnt(kVmWait2);
-      else __builtin_amdgcn_s_waitcnt(kVmWait3);
+      if (TR == 32 && wave >= 6) __builtin_amdgcn_s_waitcnt(kVmWait3);
+      else if (TR == 16 && wave == 3) __builtin_amdgcn_s_waitcnt(kVmWait1);
+      else __builtin_amdgcn_s_waitcnt(kVmWait2);
     } else {
       __builtin_amdgcn_s_waitcnt(kVmWait0);
     }
@@ -1129,7 +1138,7 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
       if (c + AHEAD + u < nch) issue(c + AHEAD + u);
 #pragma unroll 1
     for (int u = 0; u < S; ++u) {
-      if (c + u >= nch) break;  // uniform
+      if (c + u >= nch || wave >= TR / 4) break;  // uniform
       GemmOps o;
       gemm_read(gemm_stage(smem, (c + u) % kGemmStages), ja, jb, g, r0, o);
       const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
@@ -1148,8 +1157,10 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
       }
     }
   }
+  if (wave < TR / 4) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) Y[(r0 + 4 * g + i) * kTileBatch + jb] = acc[i];
+    for (int i = 0; i < 4; ++i) Y[(r0 + 4 * g + i) * kTileBatch + jb] = acc[i];
+  }
   rs.sync();
   // epilogues: item t of the tile for batch row b0 + j
   for (int e = threadIdx.x; e < ni * nbat; e += kRowThreads) {
@@ -1840,7 +1851,8 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       break;
     case PH_QGEMM:
       if constexpr (!(F & FAM_BATCH)) break;
-      qgemm_unit(ph.g, unit, spos, smem, rs);
+      if ((ph.g.epi == EPI_SILU_GATE ? 2 * ph.g.ipw : ph.g.ipw) == kTileRows) qgemm_unit<kTileRows>(ph.g, unit, spos, smem, rs);
+      else qgemm_unit<kTileRows / 2>(ph.g, unit, spos, smem, rs);
       break;
     case PH_ARGMAX:
       argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem, rs);

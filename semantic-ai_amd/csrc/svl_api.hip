@@ -510,7 +510,7 @@ void add_gemv(const svl_state* s, std::vector<Phase>& out, Phase ph) {
     q.units = s->B;
     out.push_back(q);
     ph.kind = PH_QGEMM;
-    plan_qgemm(ph.g, &ph.units);
+    plan_qgemm(ph.g, s->grid, &ph.units);
     out.push_back(ph);
     return;
   }

@@ -223,10 +223,15 @@ def test_lockstep_batch_equals_independent_streams():
         assert np.array_equal(g.recognize(audio[b][:, None, :], one)[:, 0], batched[:, b]), b
 
 
-def test_mfma_batch_equals_independent_streams():
+# text vocabulary 8000: text_linear runs in 32-row GEMM tiles, the other linears in 16-row tiles
+S1_SMALL_VOCAB = W.stt_shape("stt-small-vocab", 256, 2, 4, 4.125, 24, card=64, n_q=4, text_card=8000)
+
+
+@pytest.mark.parametrize("shape", [W.S1_SMALL, S1_SMALL_VOCAB], ids=["small", "vocab8000"])
+def test_mfma_batch_equals_independent_streams(shape):
     """A lockstep batch large enough for the MFMA GEMM path (20 streams at different positions):
     logits and tokens bit-identical to each stream stepped alone through the GEMV path."""
-    s = W.S1_SMALL
+    s = shape
     _, g, _ = build(s, "q8_0", seed=24)
     B, n = 20, 10
     audio = W.audio_tokens(s, n, seed=25, batch=B)
