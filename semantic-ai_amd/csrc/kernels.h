@@ -73,6 +73,7 @@ struct AttnArgs {
   int kv_bf16;
   float scale;
   float* out;          // [B][H*hd]
+  int hpu;             // heads per unit (1 or 2); units = B * H / hpu
 };
 
 struct EmbedArgs {

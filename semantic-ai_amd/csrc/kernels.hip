@@ -266,7 +266,7 @@ size_t phase_smem(const Phase& ph) {
       return (size_t)K * 4 + (kRowThreads / 16) * 4 + 64;
     }
     case PH_ATTN:
-      return (size_t)kAttnStages * kAttnChunkBytes + (size_t)(((ph.at.cap + 7) & ~7) + 8 + 4 + kRowThreads / 64) * 4 + 64;
+      return (size_t)kAttnStages * kAttnChunkBytes + (size_t)(ph.at.hpu * (((ph.at.cap + 7) & ~7) + 8) + 4 + 32) * 4 + 64;
     case PH_ARGMAX:
       return 32 * 4 + 64;
     case PH_NORM:

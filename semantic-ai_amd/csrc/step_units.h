@@ -1489,40 +1489,46 @@ __device__ __forceinline__ void lds_read8_f32(uint32_t addr, float (&v)[8]) {
   v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
 }
 
-template <int HD, bool BF16KV>
+// HPU heads of one stream per unit (1, or 2 for large batches): chunk row r holds head r % HPU,
+// key r / HPU of the chunk, so that a thread's scores stay with one head; the weighted sums of
+// head hh run on waves [hh HD / 64, (hh + 1) HD / 64).
+template <int HD, bool BF16KV, int HPU>
 __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int* spos, unsigned char* smem, RowSync& rs) {
   constexpr int RB = HD * (BF16KV ? 2 : 4);   // bytes of a K or V row
   constexpr int R = kAttnChunkBytes / RB;     // rows per stage
+  constexpr int RH = R / HPU;                 // keys per stage and head
   constexpr int C = HD / 16;
+  static_assert(RH % 16 == 0 && HPU * HD <= kRowThreads, "stage rows per head");
   // the descriptor's fields are read once: the written-out LDS accesses below count as memory
   // clobbers, after which the compiler would read the descriptor again (and wait for every load
   // in flight before using the value)
-  const int cap = a.cap, H = a.H;
+  const int cap = a.cap, H = a.H, KVH = a.KVH;
   const float scale = a.scale;
   const void* kc = a.kc;
   const void* vc = a.vc;
   float* out = a.out;
-  float* w = (float*)(smem + kAttnStages * kAttnChunkBytes);  // L weights (16-byte aligned)
-  float* sum_slot = w + ((cap + 7) & ~7) + 8;  // reads of w run up to 7 past the last key
-  const int h = unit % H, b = unit / H;
+  const int wstride = ((cap + 7) & ~7) + 8;  // reads of w run up to 7 past the last key
+  float* w = (float*)(smem + kAttnStages * kAttnChunkBytes);  // HPU x L weights (16-byte aligned)
+  float* slot = w + HPU * wstride;  // [0, HPU): sums; [4, 4 + 32): score maxima of the 32 groups
+  const int h0 = (unit % (H / HPU)) * HPU, b = unit / (H / HPU);
   const int p = spos[b];
   const int L = visible_keys(a, p);
   const int first = p + 1 - L;
-  const int kvh = h / (H / a.KVH);
-  const size_t head_base = ((size_t)b * a.KVH + kvh) * (size_t)cap;
-  const float* qp = a.q + (size_t)b * H * HD + (size_t)h * HD + threadIdx.x % 16;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
-  const int nch = (L + R - 1) / R;
+  const int nch = (L + RH - 1) / RH;
   // This thread's two 16-byte pieces of every chunk: piece o is byte o * 8192 + 1024 wave + 16 lane
-  // of the chunk, i.e. row (that / RB), column (that % RB).
+  // of the chunk, i.e. row (that / RB), column (that % RB); the row is key (row / HPU) of head
+  // h0 + row % HPU.
   const int off0 = wave * 1024 + lane * 16, off1 = off0 + 8192;
   const int row0 = off0 / RB, col0 = off0 % RB, row1 = off1 / RB, col1 = off1 % RB;
+  const size_t base0 = ((size_t)b * KVH + (h0 + row0 % HPU) / (H / KVH)) * (size_t)cap;
+  const size_t base1 = ((size_t)b * KVH + (h0 + row1 % HPU) / (H / KVH)) * (size_t)cap;
   auto issue = [&](const void* kv, int c) {
     unsigned char* st = smem + (c % kAttnStages) * kAttnChunkBytes;
-    const int j0 = min(c * R + row0, L - 1), j1 = min(c * R + row1, L - 1);
+    const int j0 = min(c * RH + row0 / HPU, L - 1), j1 = min(c * RH + row1 / HPU, L - 1);
     const unsigned char* g = (const unsigned char*)kv;
-    lds_dma<16, true>(g + (head_base + (size_t)((first + j0) % cap)) * RB + col0, st + wave * 1024);
-    lds_dma<16, true>(g + (head_base + (size_t)((first + j1) % cap)) * RB + col1, st + 8192 + wave * 1024);
+    lds_dma<16, true>(g + (base0 + (size_t)((first + j0) % cap)) * RB + col0, st + wave * 1024);
+    lds_dma<16, true>(g + (base1 + (size_t)((first + j1) % cap)) * RB + col1, st + 8192 + wave * 1024);
   };
   constexpr int S = kSyncChunks, AHEAD = kAttnStages - kSyncChunks;  // chunks per sync, chunks issued ahead
   auto wait_chunks = [&](int c) {  // this wave's pieces of chunks c .. c + S - 1 have landed
@@ -1530,8 +1536,11 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
     else __builtin_amdgcn_s_waitcnt(kVmWait0);
   };
   // ---- scores w_j = scale * dot16(q, k_j): 16 threads per key (thread i accumulating dims
-  // i, i + 16, ... with FMA, then the pairwise lane sum), keys j0 + 32 pass + group
+  // i, i + 16, ... with FMA, then the pairwise lane sum); group grp takes rows grp, grp + 32, ...
   const int li = threadIdx.x % 16, grp = threadIdx.x / 16;
+  const int hs = grp % HPU;  // this thread's head for the scores
+  float* ws = w + hs * wstride;
+  const float* qp = a.q + (size_t)b * H * HD + (size_t)(h0 + hs) * HD + li;
   float q[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
@@ -1550,7 +1559,7 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
       const int c = c0 + pass / (R / 32);
       if (c >= nch) break;  // uniform
       const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes);
-      const int r = (pass % (R / 32)) * 32 + grp, jj = c * R + r;
+      const int r = (pass % (R / 32)) * 32 + grp, jj = c * RH + r / HPU;
       float kv[C];
       lds_read_strided<C, 16 * (BF16KV ? 2 : 4), BF16KV>(st + r * RB + li * (BF16KV ? 2 : 4), kv);
       float acc = 0.0f;
@@ -1559,30 +1568,41 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
       acc = row16_pairwise_sum(acc);
       if (jj < L && li == 0) {
         const float sc = scale * (acc + 0.0f);
-        lds_write_f32(lds_addr(w + jj), sc);
+        lds_write_f32(lds_addr(ws + jj), sc);
         mx = fmaxf(mx, sc);
       }
     }
   }
   // ---- softmax: max (exact in any order), e_j = exp(w_j - max), the sum of e_j in key order,
   // e_j / sum
-  mx = wave_max(mx);
-  if (lane == 0) lds_write_f32(lds_addr(sum_slot + 4 + wave), mx);
+  if (li == 0) lds_write_f32(lds_addr(slot + 4 + grp), mx);
   __builtin_amdgcn_s_waitcnt(kVmWait0);
   gemm_sync(rs);
+  float mxh[HPU];
 #pragma unroll
-  for (int v = 0; v < kRowWaves; ++v) mx = fmaxf(mx, sum_slot[4 + v]);
-  for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = ref_exp(w[j] - mx);
+  for (int hh = 0; hh < HPU; ++hh) {
+    mxh[hh] = -__builtin_huge_valf();
+#pragma unroll
+    for (int gg = hh; gg < 32; gg += HPU) mxh[hh] = fmaxf(mxh[hh], slot[4 + gg]);
+  }
+#pragma unroll
+  for (int hh = 0; hh < HPU; ++hh)
+    for (int j = threadIdx.x; j < L; j += kRowThreads) w[hh * wstride + j] = ref_exp(w[hh * wstride + j] - mxh[hh]);
   rs.sync();
-  if (threadIdx.x == 0) sum_slot[0] = ordered_sum(w, L);
+  if (lane == 0 && wave < HPU) slot[wave] = ordered_sum(w + wave * wstride, L);
   rs.sync();
-  const float sum = sum_slot[0];
-  for (int j = threadIdx.x; j < L; j += kRowThreads) w[j] = w[j] / sum;
+#pragma unroll
+  for (int hh = 0; hh < HPU; ++hh) {
+    const float sum = slot[hh];
+    for (int j = threadIdx.x; j < L; j += kRowThreads) w[hh * wstride + j] = w[hh * wstride + j] / sum;
+  }
   rs.sync();
-  // ---- out_d = mul_add(w_j, v_jd, out_d) over keys in order; thread d < HD owns dim d
+  // ---- out_d = mul_add(w_j, v_jd, out_d) over keys in order; thread hh HD + d owns dim d of
+  // head h0 + hh
   for (int c = 0; c < min(AHEAD, nch); ++c) issue(vc, c);
   float acc = 0.0f;
-  const int d = min((int)threadIdx.x, HD - 1);
+  const int hv = min((int)threadIdx.x / HD, HPU - 1), d = threadIdx.x % HD;
+  const float* wv_h = w + hv * wstride;
   for (int c0 = 0; c0 < nch; c0 += S) {
     wait_chunks(c0);
     gemm_sync(rs);
@@ -1592,35 +1612,43 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
 #pragma unroll 1
     for (int u = 0; u < S; ++u) {
       const int c = c0 + u;
-      if (c >= nch || wave >= HD / kWave) break;  // uniform
-      const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes) + d * (BF16KV ? 2 : 4);
+      if (c >= nch || wave >= HPU * HD / kWave) break;  // uniform
+      const uint32_t st = lds_addr(smem + (c % kAttnStages) * kAttnChunkBytes) + hv * RB + d * (BF16KV ? 2 : 4);
 #pragma unroll
-      for (int r0 = 0; r0 < R; r0 += 16) {
-        if (c * R + r0 >= L) break;  // uniform
+      for (int r0 = 0; r0 < RH; r0 += 16) {
+        if (c * RH + r0 >= L) break;  // uniform
         float wv[16], vv[16];
-        lds_read_wv16<RB, BF16KV>(lds_addr(w + c * R + r0), st + r0 * RB, wv, vv);
-        if (c * R + r0 + 16 <= L) {  // uniform
+        lds_read_wv16<HPU * RB, BF16KV>(lds_addr(wv_h + c * RH + r0), st + r0 * HPU * RB, wv, vv);
+        if (c * RH + r0 + 16 <= L) {  // uniform
 #pragma unroll
           for (int k = 0; k < 16; ++k) acc = fmaf(wv[k], vv[k], acc);
         } else {
 #pragma unroll
           for (int k = 0; k < 16; ++k)
-            if (c * R + r0 + k < L) acc = fmaf(wv[k], vv[k], acc);
+            if (c * RH + r0 + k < L) acc = fmaf(wv[k], vv[k], acc);
         }
       }
     }
   }
-  if ((int)threadIdx.x < HD) st_co(out + (size_t)b * H * HD + (size_t)h * HD + threadIdx.x, acc);
+  if ((int)threadIdx.x < HPU * HD) st_co(out + (size_t)b * H * HD + (size_t)(h0 + hv) * HD + d, acc);
 }
 
 __device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const int* spos, unsigned char* smem,
                                               RowSync& rs) {
-  if (a.hd == 128) {
-    if (a.kv_bf16) attn_unit<128, true>(a, unit, spos, smem, rs);
-    else attn_unit<128, false>(a, unit, spos, smem, rs);
+  if (a.hpu == 2) {
+    if (a.hd == 128) {
+      if (a.kv_bf16) attn_unit<128, true, 2>(a, unit, spos, smem, rs);
+      else attn_unit<128, false, 2>(a, unit, spos, smem, rs);
+    } else {
+      if (a.kv_bf16) attn_unit<64, true, 2>(a, unit, spos, smem, rs);
+      else attn_unit<64, false, 2>(a, unit, spos, smem, rs);
+    }
+  } else if (a.hd == 128) {
+    if (a.kv_bf16) attn_unit<128, true, 1>(a, unit, spos, smem, rs);
+    else attn_unit<128, false, 1>(a, unit, spos, smem, rs);
   } else {
-    if (a.kv_bf16) attn_unit<64, true>(a, unit, spos, smem, rs);
-    else attn_unit<64, false>(a, unit, spos, smem, rs);
+    if (a.kv_bf16) attn_unit<64, true, 1>(a, unit, spos, smem, rs);
+    else attn_unit<64, false, 1>(a, unit, spos, smem, rs);
   }
 }
 
@@ -1835,7 +1863,7 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       }
       break;
     case PH_ATTN: {
-      const int heads = ph.at.B * ph.at.H;
+      const int heads = ph.at.B * ph.at.H / ph.at.hpu;
       if (unit < heads) attn_dispatch(ph.at, unit, spos, smem, rs);
       else if (step + 1 < P.n_steps && !P.text) gather_unit(ph.e, P.audio + (size_t)(step + 1) * P.audio_stride, unit - heads);
       break;

@@ -562,8 +562,12 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     a.at.kv_bf16 = kv_bf16;
     a.at.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
     a.at.out = s->att;
+    // two heads per unit once the batch has at least two units per workgroup without pairing
+    // (SVL_ATTN_PAIRS=1 forces pairs, for tests)
+    const char* pairs = getenv("SVL_ATTN_PAIRS");
+    a.at.hpu = H % 2 == 0 && (s->B * H >= 2 * s->grid || (pairs && !strcmp(pairs, "1"))) ? 2 : 1;
     a.kind = PH_ATTN;
-    a.units = s->B * H;
+    a.units = s->B * H / a.at.hpu;
     out.push_back(a);
     // out_proj + residual (layer scale if any)
     Phase o = gemv_phase(s, L.out_proj);

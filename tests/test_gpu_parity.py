@@ -391,6 +391,38 @@ def test_t1_f32_prefilled_256_within_f32_bar():
         assert np.array_equal(z, zo), (i, float(np.max(np.abs(z - zo))))
 
 
+S_HD128 = W.stt_shape("stt-small-hd128", 512, 2, 4, 4.125, 24, card=64, n_q=4, text_card=100)
+
+
+@pytest.mark.parametrize("kv", [svl.F32, svl.BF16], ids=["f32kv", "bf16kv"])
+@pytest.mark.parametrize("shape", [W.S1_SMALL, S_HD128, W.T1_SMALL], ids=["hd64", "hd128", "tts-hd64"])
+def test_attention_head_pairs_equal_single_heads(monkeypatch, shape, kv):
+    """Two heads per attention unit (the schedule of large batches) gives the same bits as one
+    head per unit: STT logits over 40 steps through a wrapping window, TTS z over 12 steps."""
+    t = W.make_weights(shape, "q8_0" if shape.kind == W.MODEL_STT else "f32", seed=41)
+    q = W.Q8_0 if shape.kind == W.MODEL_STT else 0
+    results = []
+    for pairs in ("0", "1"):
+        monkeypatch.setenv("SVL_ATTN_PAIRS", pairs)
+        g = svl.Model(shape.config(q), t, kv_dtype=kv)
+        if shape.kind == W.MODEL_STT:
+            st = g.init_state(batch=3)
+            audio = W.audio_tokens(shape, 40, seed=42, batch=3)
+            text = np.full(3, shape.text_card, dtype=np.uint32)
+            logits = []
+            for i in range(40):
+                tok, lg = g.step(text, audio[:, i], st, want_logits=True)
+                logits.append(lg)
+                text = tok.astype(np.uint32)
+            results.append(np.stack(logits))
+        else:
+            ks, vs = W.prefill_caches(shape, 20, seed=43)
+            st = g.state_from_layer_caches(ks, vs, capacity=64)
+            lat = W.latents(shape, 12, seed=44)
+            results.append(np.stack([g.backbone_step(lat[i][None], st) for i in range(12)]))
+    assert np.array_equal(results[0].view(np.uint32), results[1].view(np.uint32))
+
+
 def test_persistent_and_per_phase_launches_agree(monkeypatch):
     """The persistent step kernel and one launch per phase run the same units: same bits."""
     s = W.S1_SMALL
