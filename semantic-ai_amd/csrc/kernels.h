@@ -74,6 +74,7 @@ struct AttnArgs {
   float scale;
   float* out;          // [B][H*hd]
   int hpu;             // heads per unit (1 or 2); units = B * H / hpu
+  const int* order;    // [B] the stream of units k H / hpu .. (k + 1) H / hpu - 1
 };
 
 struct EmbedArgs {

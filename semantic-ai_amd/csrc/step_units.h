@@ -1510,7 +1510,7 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   const int wstride = ((cap + 7) & ~7) + 8;  // reads of w run up to 7 past the last key
   float* w = (float*)(smem + kAttnStages * kAttnChunkBytes);  // HPU x L weights (16-byte aligned)
   float* slot = w + HPU * wstride;  // [0, HPU): sums; [4, 4 + 32): score maxima of the 32 groups
-  const int h0 = (unit % (H / HPU)) * HPU, b = unit / (H / HPU);
+  const int h0 = (unit % (H / HPU)) * HPU, b = ldg(a.order + unit / (H / HPU));
   const int p = spos[b];
   const int L = visible_keys(a, p);
   const int first = p + 1 - L;

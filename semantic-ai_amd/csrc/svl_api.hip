@@ -12,6 +12,7 @@
 // is the ring's content.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -131,6 +132,8 @@ struct svl_state {
   std::vector<void*> kc, vc;  // per layer [B][KVH][slots][hd]
   int* pos = nullptr;
   std::vector<int64_t> pos_host;
+  int* attn_order = nullptr;     // [B] streams by visible keys, longest first (attention units)
+  std::vector<int> order_host;
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
   float* in = nullptr;        // TTS latent staging [B][latent_dim]
@@ -562,6 +565,7 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     a.at.kv_bf16 = kv_bf16;
     a.at.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
     a.at.out = s->att;
+    a.at.order = s->attn_order;
     // two heads per unit once the batch has at least two units per workgroup without pairing
     // (SVL_ATTN_PAIRS=1 forces pairs, for tests)
     const char* pairs = getenv("SVL_ATTN_PAIRS");
@@ -767,9 +771,26 @@ int check_room(const svl_state* s, int64_t steps) {
   return ensure_rope(s->m, top);
 }
 
+// Attention units take the streams longest first, so that the workgroups that get a second
+// round of units get short ones (visible keys grow with the position up to the window; the
+// order of the streams does not change while they step together).
+int refresh_attn_order(svl_state* s) {
+  const int64_t window = s->m->cfg.context;
+  std::vector<int> order(s->B);
+  for (int b = 0; b < s->B; ++b) order[b] = b;
+  auto visible = [&](int b) { return window > 0 ? std::min(s->pos_host[b] + 1, window) : s->pos_host[b] + 1; };
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return visible(x) > visible(y); });
+  if (order == s->order_host) return 0;
+  s->order_host = order;
+  HIP_TRY(hipMemcpyAsync(s->attn_order, s->order_host.data(), (size_t)s->B * sizeof(int), hipMemcpyHostToDevice,
+                         s->stream));
+  return 0;
+}
+
 // Runs `n_steps` steps of program `p` on the state's stream: one persistent launch, or one
 // launch per phase.
 int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
+  TRY(refresh_attn_order(s));
   const float* rope;
   {
     std::lock_guard<std::mutex> lock(s->m->rope_mu);
@@ -849,6 +870,7 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   const int width = std::max(std::max(c.d_model, qdim), c.ff_hidden);
   void* p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * sizeof(int)), s->pos = (int*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * sizeof(int)), s->attn_order = (int*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->fb_tok = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * c.d_model * 4), s->x = (float*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * qdim * 4), s->q = (float*)p;
