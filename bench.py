@@ -18,11 +18,13 @@ Other workloads (one JSON line each, same fields):
                  (the reference returns to the host every frame).
 
 Prints ONE JSON line (rank 0).  `value` is decode steps/s; `roofline` prices the dominant
-kernel -- the persistent step-program kernel, one launch of which runs all the timed steps --
-against MI355X HBM bandwidth with the algorithmic bytes of the steps it ran; its `traffic` is the
-HBM bytes of that launch as measured by rocprofv3 counters (profiles/), when the profiled launch
-had the same workload and number of steps; `cpu_baseline` is the oracle (this repository's C
-restatement of the reference's CPU path) on the host cores.
+kernel -- phase_kernel, launched once per phase of every step (83 launches per STT-1B step, 148
+at B=64) -- against MI355X HBM bandwidth: `achieved` = algorithmic bytes per launch / average
+launch time, i.e. the algorithmic bytes of the timed steps over their HIP-event time (which
+also counts the gaps between launches); `traffic` is the HBM bytes per launch measured by
+rocprofv3 counters on a run of the same workload (profiles/; `traffic_counter_steps` says how
+many steps that run had); `cpu_baseline` is the oracle (this repository's C restatement of the
+reference's CPU path) on the host cores.
 
 `--calibrate-copy BYTES` instead runs the plain copy kernel of libsvl three times over BYTES
 (the known-size reference that scales the traffic counters) and prints one JSON line.
@@ -46,27 +48,25 @@ WORKLOADS = ["stt1b-q8-b1", "stt1b-q8-b64", "stt1b-bf16-b1", "stt2.6b-q4k-b1", "
 
 
 def traffic_file(workload):
-    return os.path.join(ROOT, "profiles", f"step_program_kernel.{workload.replace('-', '_')}.traffic.txt")
+    return os.path.join(ROOT, "profiles", f"phase_kernel.{workload.replace('-', '_')}.traffic.txt")
 
 
-def read_traffic(workload, steps):
-    """HBM bytes of one step-program launch of `steps` steps, from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel calibration), or
-    None when no summary for that launch exists."""
+def read_traffic(workload):
+    """(HBM bytes per phase_kernel launch, steps of the counter run) from the committed counter
+    summary of this workload (FETCH_SIZE + WRITE_SIZE summed over the run's dispatches, scaled
+    by the copy-kernel calibration, divided by the dispatches), or (None, None)."""
     path = traffic_file(workload)
     if not os.path.exists(path):
-        return None
+        return None, None
     kv = {}
     for line in open(path):
         if ":" in line and not line.lstrip().startswith("#"):
             k, v = line.split(":", 1)
             kv[k.strip()] = v.strip()
     try:
-        if int(kv["steps_per_dispatch"]) != steps:
-            return None
-        return int(float(kv["hbm_bytes_per_dispatch"]))
+        return int(float(kv["hbm_bytes_per_launch"])), int(kv["steps"])
     except (KeyError, ValueError):
-        return None
+        return None, None
 
 
 def step_bytes(shape, dtype, kv_bytes, visible):
@@ -82,6 +82,15 @@ def step_bytes(shape, dtype, kv_bytes, visible):
     norms = (2 * L + 1) * d * 4 * (2 if shape.norm_kind == W.NORM_LAYER else 1)
     per_stream = [L * (2 * v * kvw * kv_bytes + 2 * kvw * kv_bytes) + emb + norms for v in visible]
     return w + float(sum(per_stream))
+
+
+def stt_phases_per_step(shape, B, dtype):
+    """Launches per STT step: embedding; per layer QKV, attention, out, FF-in, FF-out (each
+    Q8_0 linear of a batch of 16 or more streams is an activation-quantization launch and a GEMM
+    launch); text_linear (+ quantization) and argmax."""
+    batched = dtype == "q8_0" and B >= 16
+    per_layer = 5 + (4 if batched else 0)
+    return 1 + shape.num_layers * per_layer + (2 if batched else 1) + 1
 
 
 def calibrate_copy(nbytes):
@@ -178,10 +187,15 @@ def bench_stt(args, wl, steps, warmup):
           "bf16": "bf16 weights, f32 arithmetic (16-lane FMA dot)"}[dtype]
     line = base_line(steps / (gpu_ms / 1e3), steps, warmup, gpu_ms / steps, dt,
                      "synthetic (seeded N(0, 0.02) weights, uniform audio ids, greedy text feedback)", config)
+    launches = steps * stt_phases_per_step(shape, B, dtype)
+    traffic, traffic_steps = read_traffic(wl)
     line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(wl, steps),
-                        "kernel": "step_program_kernel (one launch = all timed steps)",
-                        "algorithmic_bytes_per_launch": int(bytes_launch), "launch_ms": round(gpu_ms, 4)}
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                        "traffic_counter_steps": traffic_steps,
+                        "kernel": "phase_kernel (one launch per phase of each step)",
+                        "launches": launches,
+                        "algorithmic_bytes_per_launch": int(bytes_launch / launches),
+                        "avg_launch_us": round(gpu_ms * 1e3 / launches, 3), "timed_ms": round(gpu_ms, 4)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_stt(args, shape, dtype, tensors, audio, fills, d_out, steps, B)
     return line
@@ -251,8 +265,8 @@ def bench_tts(args, steps, warmup):
                      "synthetic (seeded N(0, 0.02) weights, N(0, 1) latents, seeded prefilled K/V)", config)
     line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                        "kernel": "step_program_kernel (one launch per step)",
-                        "algorithmic_bytes_per_launch": int(bytes_total / steps)}
+                        "kernel": "phase_kernel (one launch per phase; one call = one step)",
+                        "algorithmic_bytes_per_step": int(bytes_total / steps)}
     if not args.no_cpu_baseline:
         import oracle
 

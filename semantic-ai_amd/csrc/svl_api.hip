@@ -848,7 +848,9 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   s->slots = slots;
   s->grid = step_program_grid(m->device);
   const char* mode = getenv("SVL_STEP_LAUNCH");
-  s->persistent = !(mode && !strcmp(mode, "phases"));
+  // one launch per phase by default (kernel boundaries order the phases); SVL_STEP_LAUNCH=persistent
+  // runs the steps of a call in one cooperative launch with grid barriers instead
+  s->persistent = mode && !strcmp(mode, "persistent");
   auto fail = [&](int rc) {
     delete s;
     return rc;

@@ -429,6 +429,7 @@ def test_persistent_and_per_phase_launches_agree(monkeypatch):
     t = W.make_weights(s, "q8_0", seed=19)
     g = svl.Model(s.config(W.Q8_0), t)
     audio = W.audio_tokens(s, 30, seed=20)[0][:, None, :]
+    monkeypatch.setenv("SVL_STEP_LAUNCH", "persistent")
     a = g.recognize(audio, g.init_state())
     monkeypatch.setenv("SVL_STEP_LAUNCH", "phases")
     st = g.init_state()
