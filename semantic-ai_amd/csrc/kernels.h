@@ -148,7 +148,7 @@ struct StepParams {
   const Phase* prog;
   int nphase;
   int n_steps;
-  int* pos;                      // [B] stream positions (cached per step in LDS)
+  int* pos;                      // [B] stream positions (the persistent kernel caches them per step in LDS)
   int B;
   SyncState* sync;
   unsigned gen0;                 // barriers completed by earlier launches on this state

@@ -116,7 +116,6 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
 
 __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, StepParams P, int step) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int spos[kMaxBatch];
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) {
@@ -143,10 +142,10 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, 
     return;
   }
   RowSync rs{&ws, 0u};
-  load_positions(P, spos);
-  rs.sync();
   unsigned item = 0;
-  run_unit<FAM_ALL>(phase_at(d_ph, 0), P, step, blockIdx.x, spos, smem, rs, item);
+  // Units read the positions from memory where they need them: only the step's last phase that
+  // reads them advances them, and launches are ordered on the stream.
+  run_unit<FAM_ALL>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
 }
 
 unsigned program_families(const Phase* phases, int n) {

@@ -521,14 +521,14 @@ __device__ __forceinline__ void gemv_q8_rows(const GemvArgs& a, int unit, const 
                                              RowSync& rs, unsigned item) {
   const Q8Geom g = q8_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
   const Q8Lds l = q8_lds(smem, g.K, g.nb, a.ipw, g.ts);
-  const int p = spos[g.b];
-  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   // rows wider than 4096 (row_slots 16) are never normalized (d_model <= 4096)
   constexpr bool kNorm = KP <= 8;
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, g.K, nwt);
   float v[KP];
   load_row(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
+  const int p = (a.epi == EPI_QKV_ROPE || a.advance_pos ? spos[g.b] : 0);
+  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   if constexpr (kNorm) {
     if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
   }
@@ -759,13 +759,13 @@ __device__ __forceinline__ void gemv_q4k_rows(const GemvArgs& a, int unit, const
                                               RowSync& rs, unsigned item) {
   const Q8Geom g = q4_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
   const Q4Lds l = q4_lds(smem, g.K, g.nb, g.ts);
-  const int p = spos[g.b];
-  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   constexpr bool kNorm = KP <= 8;
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, g.K, nwt);
   float v[KP];
   load_row(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
+  const int p = (a.epi == EPI_QKV_ROPE || a.advance_pos ? spos[g.b] : 0);
+  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   if constexpr (kNorm) {
     if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
   }
@@ -1165,7 +1165,7 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
   // epilogues: item t of the tile for batch row b0 + j
   for (int e = threadIdx.x; e < ni * nbat; e += kRowThreads) {
     const int t = e % ni, j = e / ni;
-    const int b = b0 + j, row = i0 + t, p = spos[b];
+    const int b = b0 + j, row = i0 + t, p = a.epi == EPI_QKV_ROPE ? spos[b] : 0;
     const float y = Y[t * kTileBatch + j];
     const float yp = a.epi == EPI_QKV_ROPE ? Y[(t ^ 1) * kTileBatch + j] : 0.0f;
     const float yv = silu ? Y[(ni + t) * kTileBatch + j] : 0.0f;
@@ -1191,15 +1191,15 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
   const int i0 = part * a.ipw;
   const int ni = min(a.ipw, gemv_items(a) - i0);
   const int NR = silu ? 2 * ni : ni;
-  const int p = spos[b];
   float* xs = (float*)smem;   // K
   float* Y = xs + K;          // kRowThreads / 16
-  const EpiIn in = gemv_epi_prefetch(a, b, i0 + min((int)threadIdx.x, ni - 1), p);
   constexpr bool kNorm = KP <= 8;  // rows wider than 4096 are never normalized (d_model <= 4096)
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
   float v[KP];
   load_row(a.x + (size_t)b * a.x_stride, K, v);
+  const int p = a.epi == EPI_QKV_ROPE || a.advance_pos ? spos[b] : 0;
+  const EpiIn in = gemv_epi_prefetch(a, b, i0 + min((int)threadIdx.x, ni - 1), p);
   if constexpr (kNorm) {
     if (a.norm != NORM_NONE) {
       norm_regs(v, K, a.norm, nwt, a.eps, xs, rs);
@@ -1293,13 +1293,13 @@ __device__ __forceinline__ void gemv_dense_rows(const GemvArgs& a, int unit, con
   const int K = a.L.in;
   const Q8Geom g = q8_geom(K, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
   const DenseLds l = dense_lds(smem, K);
-  const int p = spos[g.b];
-  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   constexpr bool kNorm = KP <= 8;
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
   float v[KP];
   load_row(a.x + (size_t)g.b * a.x_stride, K, v, &rs.ws->r_issued);
+  const int p = (a.epi == EPI_QKV_ROPE || a.advance_pos ? spos[g.b] : 0);
+  const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   if constexpr (kNorm) {
     if (a.norm != NORM_NONE) norm_regs(v, K, a.norm, nwt, a.eps, l.xs, rs);
   }
@@ -1511,6 +1511,16 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   float* w = (float*)(smem + kAttnStages * kAttnChunkBytes);  // HPU x L weights (16-byte aligned)
   float* slot = w + HPU * wstride;  // [0, HPU): sums; [4, 4 + 32): score maxima of the 32 groups
   const int h0 = (unit % (H / HPU)) * HPU, b = ldg(a.order + unit / (H / HPU));
+  // the query is requested with the position (the prologue needs only the position)
+  const int li = threadIdx.x % 16, grp = threadIdx.x / 16;
+  const int hs = grp % HPU;  // this thread's head for the scores
+  float q[C];
+  {
+    const float* qp = a.q + (size_t)b * H * HD + (size_t)(h0 + hs) * HD + li;
+    __builtin_amdgcn_s_waitcnt(kVmWait0);  // no older store interleaves with the counted loads
+#pragma unroll
+    for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
+  }
   const int p = spos[b];
   const int L = visible_keys(a, p);
   const int first = p + 1 - L;
@@ -1537,15 +1547,7 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   };
   // ---- scores w_j = scale * dot16(q, k_j): 16 threads per key (thread i accumulating dims
   // i, i + 16, ... with FMA, then the pairwise lane sum); group grp takes rows grp, grp + 32, ...
-  const int li = threadIdx.x % 16, grp = threadIdx.x / 16;
-  const int hs = grp % HPU;  // this thread's head for the scores
   float* ws = w + hs * wstride;
-  const float* qp = a.q + (size_t)b * H * HD + (size_t)(h0 + hs) * HD + li;
-  float q[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) q[c] = ld_co(qp + c * 16);
-  // the query has arrived and no older store interleaves with the counted loads
-  __builtin_amdgcn_s_waitcnt(kVmWait0);
   float mx = -__builtin_huge_valf();  // running maximum of this thread's scores
   for (int c = 0; c < min(AHEAD, nch); ++c) issue(kc, c);
   for (int c0 = 0; c0 < nch; c0 += S) {
