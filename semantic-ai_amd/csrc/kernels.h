@@ -204,7 +204,7 @@ enum UnitFamily : unsigned {
 };
 unsigned program_families(const Phase* phases, int n);
 hipError_t launch_step_program(const StepParams& p, unsigned families, int grid, size_t smem, hipStream_t s);
-hipError_t launch_phase(const Phase* d_ph, int units, const StepParams& p, int step, size_t smem, hipStream_t s);
+hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s);
 int step_program_grid(int device);
 size_t phase_smem(const Phase& ph);
 // Fills the unit layout of a GEMV phase (ipw, parts, maxb, units) for `grid` workgroups.

@@ -114,30 +114,38 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
   }
 }
 
-__global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, StepParams P, int step) {
+// One phase of a step.  The descriptor travels in the kernel arguments: its fields are read from
+// the argument segment, with no dependent load of a descriptor pointer first.  F and KM select
+// the unit code compiled in (one GEMV family, or a group of phase kinds), so that each launch
+// runs a compact kernel.
+template <unsigned F, unsigned KM>
+__global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, StepParams P, int step) {
+  const Phase* d_ph = &ph;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) {
-    if (is_split_gemv(d_ph)) {
-      if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
-      const int fmt = ld_const(&d_ph->g.L.fmt);
-      if (is_chained_dense(fmt)) {
-        const bool ok = fmt == FMT_BF16C ? w_dense<true>(d_ph, blockIdx.x, &ws, smem, 0)
-                                         : w_dense<false>(d_ph, blockIdx.x, &ws, smem, 0);
-        if (!ok) return;
-      } else if (fmt == FMT_Q4K) {
-        WItemQ4 it;
-        w_issue_q4k(d_ph, blockIdx.x, it);
-        if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
-        w_terms_q4k(it, smem);
-      } else {
-        WItem it;
-        w_issue(d_ph, blockIdx.x, it);
-        if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
-        w_terms(it, smem);
+    if constexpr ((F & (FAM_Q8 | FAM_Q4K | FAM_DENSE)) != 0) {
+      if (is_split_gemv(d_ph)) {
+        if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
+        if constexpr (F == FAM_DENSE) {
+          const int fmt = ld_const(&d_ph->g.L.fmt);
+          const bool ok = fmt == FMT_BF16C ? w_dense<true>(d_ph, blockIdx.x, &ws, smem, 0)
+                                           : w_dense<false>(d_ph, blockIdx.x, &ws, smem, 0);
+          if (!ok) return;
+        } else if constexpr (F == FAM_Q4K) {
+          WItemQ4 it;
+          w_issue_q4k(d_ph, blockIdx.x, it);
+          if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+          w_terms_q4k(it, smem);
+        } else {
+          WItem it;
+          w_issue(d_ph, blockIdx.x, it);
+          if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+          w_terms(it, smem);
+        }
+        lds_signal(&ws.t_parts);
       }
-      lds_signal(&ws.t_parts);
     }
     return;
   }
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase* d_ph, 
   unsigned item = 0;
   // Units read the positions from memory where they need them: only the step's last phase that
   // reads them advances them, and launches are ordered on the stream.
-  run_unit<FAM_ALL>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
+  run_unit<F, KM>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
 }
 
 unsigned program_families(const Phase* phases, int n) {
@@ -170,9 +178,21 @@ hipError_t launch_step_program(const StepParams& p, unsigned families, int grid,
   return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kStepThreads), kargs, (unsigned)smem, s);
 }
 
-hipError_t launch_phase(const Phase* d_ph, int units, const StepParams& p, int step, size_t smem, hipStream_t s) {
-  if (units <= 0) return hipSuccess;
-  hipLaunchKernelGGL(phase_kernel, dim3(units), dim3(kStepThreads), smem, s, d_ph, p, step);
+hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s) {
+  if (ph.units <= 0) return hipSuccess;
+  void (*k)(const Phase, StepParams, int);
+  switch (ph.kind) {
+    case PH_GEMV:
+      if (ph.g.L.fmt == FMT_Q8_0) k = phase_kernel<FAM_Q8, 0u>;
+      else if (ph.g.L.fmt == FMT_Q4K) k = phase_kernel<FAM_Q4K, 0u>;
+      else k = phase_kernel<FAM_DENSE, kind_bit(PH_GEMV)>;
+      break;
+    case PH_QUANT:
+    case PH_QGEMM: k = phase_kernel<FAM_BATCH, kind_bit(PH_QUANT) | kind_bit(PH_QGEMM)>; break;
+    case PH_ATTN: k = phase_kernel<0u, kind_bit(PH_ATTN)>; break;
+    default: k = phase_kernel<0u, kMiscKinds>; break;
+  }
+  hipLaunchKernelGGL(k, dim3(ph.units), dim3(kStepThreads), smem, s, ph, p, step);
   return hipGetLastError();
 }
 

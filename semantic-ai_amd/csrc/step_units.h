@@ -1802,7 +1802,13 @@ __device__ __forceinline__ void copy_unit(const float* x, int x_stride, float* y
 // Row-wave part of work unit `unit` of phase `ph` for step `step` of a launch; `spos` holds
 // the streams' positions at the start of the step, `item` counts the workgroup's Q8_0 GEMV
 // units.
-template <unsigned F>
+// Phase kinds compiled into a kernel, one bit per PhaseKind.
+__host__ __device__ constexpr unsigned kind_bit(int k) { return 1u << k; }
+constexpr unsigned kAllKinds = 0x3FFu;
+constexpr unsigned kMiscKinds = kind_bit(PH_EMBED) | kind_bit(PH_ARGMAX) | kind_bit(PH_NORM) | kind_bit(PH_COPY_IN) |
+                                kind_bit(PH_COPY_OUT);
+
+template <unsigned F, unsigned KM = kAllKinds>
 __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
                                          unsigned char* smem, RowSync& rs, unsigned& item) {
   if ((F & FAM_Q8) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
@@ -1838,13 +1844,14 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
   rs.sync();  // the previous unit's readers of LDS are done
   switch (ph.kind) {
     case PH_EMBED: {
+      if constexpr (!(KM & kind_bit(PH_EMBED))) break;
       const uint32_t* text = P.text ? P.text + (size_t)step * P.text_stride : nullptr;
       const bool staged = ph.e.stage != nullptr && step > 0 && !P.text;
       embed_unit(ph.e, text, P.audio + (size_t)step * P.audio_stride, unit, spos, staged, smem, rs);
       break;
     }
     case PH_GEMV:
-      if constexpr (!(F & FAM_DENSE)) break;
+      if constexpr (!(F & FAM_DENSE) || !(KM & kind_bit(PH_GEMV))) break;
       switch (row_slots(ph.g.L.in)) {
         case 2:
           if (ph.g.L.fmt == FMT_BF16) gemv_dense_unit<true, 2>(ph.g, unit, spos, smem, rs);
@@ -1865,13 +1872,14 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       }
       break;
     case PH_ATTN: {
+      if constexpr (!(KM & kind_bit(PH_ATTN))) break;
       const int heads = ph.at.B * ph.at.H / ph.at.hpu;
       if (unit < heads) attn_dispatch(ph.at, unit, spos, smem, rs);
       else if (step + 1 < P.n_steps && !P.text) gather_unit(ph.e, P.audio + (size_t)(step + 1) * P.audio_stride, unit - heads);
       break;
     }
     case PH_QUANT:
-      if constexpr (!(F & FAM_BATCH)) break;
+      if constexpr (!(F & FAM_BATCH) || !(KM & kind_bit(PH_QUANT))) break;
       switch (row_slots(ph.g.L.in)) {
         case 2: quant_unit<2>(ph.g, unit, smem, rs); break;
         case 4: quant_unit<4>(ph.g, unit, smem, rs); break;
@@ -1880,14 +1888,16 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       }
       break;
     case PH_QGEMM:
-      if constexpr (!(F & FAM_BATCH)) break;
+      if constexpr (!(F & FAM_BATCH) || !(KM & kind_bit(PH_QGEMM))) break;
       if ((ph.g.epi == EPI_SILU_GATE ? 2 * ph.g.ipw : ph.g.ipw) == kTileRows) qgemm_unit<kTileRows>(ph.g, unit, spos, smem, rs);
       else qgemm_unit<kTileRows / 2>(ph.g, unit, spos, smem, rs);
       break;
     case PH_ARGMAX:
+      if constexpr (!(KM & kind_bit(PH_ARGMAX))) break;
       argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem, rs);
       break;
     case PH_NORM:
+      if constexpr (!(KM & kind_bit(PH_NORM))) break;
       switch (row_slots(ph.nm.d)) {  // d_model <= 4096
         case 2: norm_unit<2>(ph.nm, unit, smem, rs); break;
         case 4: norm_unit<4>(ph.nm, unit, smem, rs); break;
@@ -1895,9 +1905,11 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       }
       break;
     case PH_COPY_IN:
+      if constexpr (!(KM & kind_bit(PH_COPY_IN))) break;
       copy_unit(P.fwd_in + (size_t)step * ph.cp.n, ph.cp.x_stride, ph.cp.y, ph.cp.y_stride, ph.cp.n, unit);
       break;
     case PH_COPY_OUT:
+      if constexpr (!(KM & kind_bit(PH_COPY_OUT))) break;
       copy_unit(ph.cp.x, ph.cp.x_stride, P.fwd_out + (size_t)step * ph.cp.n, ph.cp.y_stride, ph.cp.n, unit);
       break;
   }

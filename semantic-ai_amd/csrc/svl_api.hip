@@ -816,7 +816,7 @@ int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
     P.n_steps = (int)n_steps;  // the units see the launch's step count (next-step gathers)
     for (int64_t step = 0; step < n_steps; ++step)
       for (int i = 0; i < P.nphase; ++i)
-        HIP_TRY(launch_phase(p.dev + i, p.phases[i].units, P, (int)step, p.smem, s->stream));
+        HIP_TRY(launch_phase(p.phases[i], P, (int)step, p.smem, s->stream));
   }
   for (auto& q : s->pos_host) q += n_steps;
   return 0;
