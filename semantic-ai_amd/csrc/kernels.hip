@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
 // the argument segment, with no dependent load of a descriptor pointer first.  F and KM select
 // the unit code compiled in (one GEMV family, or a group of phase kinds), so that each launch
 // runs a compact kernel.
-template <unsigned F, unsigned KM>
+template <unsigned F, unsigned KM, int V>
 __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, StepParams P, int step) {
   const Phase* d_ph = &ph;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, Ste
   unsigned item = 0;
   // Units read the positions from memory where they need them: only the step's last phase that
   // reads them advances them, and launches are ordered on the stream.
-  run_unit<F, KM>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
+  run_unit<F, KM, V>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
 }
 
 unsigned program_families(const Phase* phases, int n) {
@@ -178,19 +178,45 @@ hipError_t launch_step_program(const StepParams& p, unsigned families, int grid,
   return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kStepThreads), kargs, (unsigned)smem, s);
 }
 
+// The kernel of a GEMV family for inputs of `slots` row slots (2, 4, 8 or 16).
+template <unsigned F, unsigned KM>
+void (*slots_kernel(int slots))(const Phase, StepParams, int) {
+  switch (slots) {
+    case 2: return phase_kernel<F, KM, 2>;
+    case 4: return phase_kernel<F, KM, 4>;
+    case 8: return phase_kernel<F, KM, 8>;
+    default: return phase_kernel<F, KM, kMaxSlots>;
+  }
+}
+
+template <int AV>
+void (*attn_kernel_at(int v))(const Phase, StepParams, int) {
+  if constexpr (AV > 8) {
+    return nullptr;
+  } else {
+    return v == AV ? phase_kernel<0u, kind_bit(PH_ATTN), AV> : attn_kernel_at<AV + 1>(v);
+  }
+}
+
 hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s) {
   if (ph.units <= 0) return hipSuccess;
   void (*k)(const Phase, StepParams, int);
   switch (ph.kind) {
     case PH_GEMV:
-      if (ph.g.L.fmt == FMT_Q8_0) k = phase_kernel<FAM_Q8, 0u>;
-      else if (ph.g.L.fmt == FMT_Q4K) k = phase_kernel<FAM_Q4K, 0u>;
-      else k = phase_kernel<FAM_DENSE, kind_bit(PH_GEMV)>;
+      if (ph.g.L.fmt == FMT_Q8_0) k = slots_kernel<FAM_Q8, 0u>(row_slots(ph.g.L.in));
+      else if (ph.g.L.fmt == FMT_Q4K) k = slots_kernel<FAM_Q4K, 0u>(row_slots(ph.g.L.in));
+      else k = slots_kernel<FAM_DENSE, kind_bit(PH_GEMV)>(row_slots(ph.g.L.in));
       break;
     case PH_QUANT:
-    case PH_QGEMM: k = phase_kernel<FAM_BATCH, kind_bit(PH_QUANT) | kind_bit(PH_QGEMM)>; break;
-    case PH_ATTN: k = phase_kernel<0u, kind_bit(PH_ATTN)>; break;
-    default: k = phase_kernel<0u, kMiscKinds>; break;
+    case PH_QGEMM:
+      k = slots_kernel<FAM_BATCH, kind_bit(PH_QUANT) | kind_bit(PH_QGEMM)>(row_slots(ph.g.L.in));
+      break;
+    case PH_ATTN: {
+      const int hd = ph.at.hd == 128 ? 128 : 64;
+      k = attn_kernel_at<1>(attn_variant(hd, ph.at.kv_bf16, ph.at.hpu));
+      break;
+    }
+    default: k = phase_kernel<0u, kMiscKinds, 0>; break;
   }
   hipLaunchKernelGGL(k, dim3(ph.units), dim3(kStepThreads), smem, s, ph, p, step);
   return hipGetLastError();

@@ -1635,8 +1635,19 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   if ((int)threadIdx.x < HPU * HD) st_co(out + (size_t)b * H * HD + (size_t)(h0 + hv) * HD + d, acc);
 }
 
+// Compile-time attention variant of (head_dim, bf16 cache, heads per unit); 0 = chosen at run time.
+__host__ __device__ constexpr int attn_variant(int hd, int kv_bf16, int hpu) {
+  return 1 + (hd == 128 ? 1 : 0) + (kv_bf16 ? 2 : 0) + (hpu == 2 ? 4 : 0);
+}
+
+template <int AV>
 __device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const int* spos, unsigned char* smem,
                                               RowSync& rs) {
+  if constexpr (AV != 0) {
+    constexpr int c = AV - 1;
+    attn_unit<(c & 1) ? 128 : 64, (c & 2) != 0, (c & 4) ? 2 : 1>(a, unit, spos, smem, rs);
+    return;
+  }
   if (a.hpu == 2) {
     if (a.hd == 128) {
       if (a.kv_bf16) attn_unit<128, true, 2>(a, unit, spos, smem, rs);
@@ -1808,11 +1819,12 @@ constexpr unsigned kAllKinds = 0x3FFu;
 constexpr unsigned kMiscKinds = kind_bit(PH_EMBED) | kind_bit(PH_ARGMAX) | kind_bit(PH_NORM) | kind_bit(PH_COPY_IN) |
                                 kind_bit(PH_COPY_OUT);
 
-template <unsigned F, unsigned KM = kAllKinds>
+template <unsigned F, unsigned KM = kAllKinds, int V = 0>
 __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
                                          unsigned char* smem, RowSync& rs, unsigned& item) {
   if ((F & FAM_Q8) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
-    switch (row_slots(ph.g.L.in)) {
+    if constexpr (V != 0) gemv_q8_rows<V>(ph.g, unit, spos, smem, rs, item);
+    else switch (row_slots(ph.g.L.in)) {
       case 2: gemv_q8_rows<2>(ph.g, unit, spos, smem, rs, item); break;
       case 4: gemv_q8_rows<4>(ph.g, unit, spos, smem, rs, item); break;
       case 8: gemv_q8_rows<8>(ph.g, unit, spos, smem, rs, item); break;
@@ -1822,7 +1834,8 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
     return;
   }
   if ((F & FAM_DENSE) && ph.kind == PH_GEMV && is_chained_dense(ph.g.L.fmt)) {
-    switch (row_slots(ph.g.L.in)) {
+    if constexpr (V != 0) gemv_dense_rows<V>(ph.g, unit, spos, smem, rs, item);
+    else switch (row_slots(ph.g.L.in)) {
       case 2: gemv_dense_rows<2>(ph.g, unit, spos, smem, rs, item); break;
       case 4: gemv_dense_rows<4>(ph.g, unit, spos, smem, rs, item); break;
       case 8: gemv_dense_rows<8>(ph.g, unit, spos, smem, rs, item); break;
@@ -1832,7 +1845,8 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
     return;
   }
   if ((F & FAM_Q4K) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q4K) {
-    switch (row_slots(ph.g.L.in)) {
+    if constexpr (V != 0) gemv_q4k_rows<V>(ph.g, unit, spos, smem, rs, item);
+    else switch (row_slots(ph.g.L.in)) {
       case 2: gemv_q4k_rows<2>(ph.g, unit, spos, smem, rs, item); break;
       case 4: gemv_q4k_rows<4>(ph.g, unit, spos, smem, rs, item); break;
       case 8: gemv_q4k_rows<8>(ph.g, unit, spos, smem, rs, item); break;
@@ -1874,13 +1888,14 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
     case PH_ATTN: {
       if constexpr (!(KM & kind_bit(PH_ATTN))) break;
       const int heads = ph.at.B * ph.at.H / ph.at.hpu;
-      if (unit < heads) attn_dispatch(ph.at, unit, spos, smem, rs);
+      if (unit < heads) attn_dispatch<V>(ph.at, unit, spos, smem, rs);
       else if (step + 1 < P.n_steps && !P.text) gather_unit(ph.e, P.audio + (size_t)(step + 1) * P.audio_stride, unit - heads);
       break;
     }
     case PH_QUANT:
       if constexpr (!(F & FAM_BATCH) || !(KM & kind_bit(PH_QUANT))) break;
-      switch (row_slots(ph.g.L.in)) {
+      if constexpr (V != 0) quant_unit<V>(ph.g, unit, smem, rs);
+      else switch (row_slots(ph.g.L.in)) {
         case 2: quant_unit<2>(ph.g, unit, smem, rs); break;
         case 4: quant_unit<4>(ph.g, unit, smem, rs); break;
         case 8: quant_unit<8>(ph.g, unit, smem, rs); break;
