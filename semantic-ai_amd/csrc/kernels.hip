@@ -298,8 +298,9 @@ size_t phase_smem(const Phase& ph) {
       const GemvArgs& g = ph.g;
       const int K = g.L.in;
       if (g.L.fmt == FMT_Q8_0) {
-        const int nb = K / 32, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
-        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)nb * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
+        const int nb = K / 32, nb4 = (nb + 3) & ~3;
+        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
+               (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_Q4K) {
         const int nb = K / 256, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;

@@ -440,33 +440,48 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs& a, int b, int part, 
   if (a.advance_pos && part == 0 && t == 0) st_co(a.pos + b, p + 1);
 }
 
-// Terms are stored block-major, T[blk * ts + r] with an odd stride ts = 2 ipw + 1, so that the
-// row threads (consecutive r) and the weight-wave threads (consecutive blk) both access LDS
+// Q4K terms are stored block-major, T[blk * ts + r] with an odd stride ts = 2 ipw + 1, so that
+// the row threads (consecutive r) and the weight-wave threads (consecutive blk) both access LDS
 // without bank conflicts.
 __device__ __forceinline__ int term_stride(int ipw) { return 2 * ipw + 1; }
 
-// acc = 0; acc += T[blk * ts + r] for blk = 0 .. nb-1 in order; each batch of 32 terms is
-// read before its additions, the last partial batch too.
-__device__ __forceinline__ float ordered_row_sum(const float* T, int ts, int r, int nb) {
-  constexpr int U = 32;
-  const float* t = T + r;
+// Q8_0 terms are stored row-major, T[r * rs + blk] with rs = q8_row_stride(nb): a multiple of 4
+// (16-byte rows) with 4 words of padding, so that the rows' 16-byte reads fall in different banks.
+__host__ __device__ inline int q8_row_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+
+// acc = 0; acc += T[r * rs + blk] for blk = 0 .. nb-1 in order; each batch of 32 terms is read
+// (as 16-byte vectors) before its additions, the last partial batch too.
+__device__ __forceinline__ float ordered_row_sum(const float* T, int rs, int r, int nb) {
+  typedef float v4f_t __attribute__((ext_vector_type(4)));
+  const v4f_t* t4 = (const v4f_t*)(T + r * rs);
   float acc = 0.0f;
   int blk = 0;
-  for (; blk + U <= nb; blk += U) {
-    float v[U];
+  for (; blk + 32 <= nb; blk += 32) {
+    v4f_t v[8];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = t[(blk + u) * ts];
+    for (int u = 0; u < 8; ++u) v[u] = t4[blk / 4 + u];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc = acc + v[u];
+    for (int u = 0; u < 8; ++u) {
+      acc = acc + v[u].x;
+      acc = acc + v[u].y;
+      acc = acc + v[u].z;
+      acc = acc + v[u].w;
+    }
   }
-  if (blk < nb) {  // the last partial batch, read at once (indices past nb read the last term)
-    float v[U];
+  if (blk < nb) {  // the last partial batch (vectors past the row's last read its last vector)
+    v4f_t v[8];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = t[min(blk + u, nb - 1) * ts];
+    for (int u = 0; u < 8; ++u) v[u] = t4[min(blk / 4 + u, (nb - 1) / 4)];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc = blk + u < nb ? acc + v[u] : acc;
+    for (int u = 0; u < 8; ++u) {
+      const int b0 = blk + 4 * u;
+      acc = b0 < nb ? acc + v[u].x : acc;
+      acc = b0 + 1 < nb ? acc + v[u].y : acc;
+      acc = b0 + 2 < nb ? acc + v[u].z : acc;
+      acc = b0 + 3 < nb ? acc + v[u].w : acc;
+    }
   }
   return acc;
 }
@@ -494,8 +509,8 @@ __device__ __forceinline__ Q8Geom q8_geom(int K, int items, int ipw, int parts, 
   return g;
 }
 
-// LDS of a Q8_0 unit: xs [K] f32 | xq [K] int8 | xdq [nb, padded to 4] f32 | T [nb][ts] f32 |
-// Y [2 ipw] f32.
+// LDS of a Q8_0 unit: xs [K] f32 | xq [K] int8 | xdq [nb, padded to 4] f32 |
+// T [2 ipw][q8_row_stride(nb)] f32 | Y [2 ipw] f32.
 struct Q8Lds {
   float* xs;
   int8_t* xq;
@@ -504,13 +519,13 @@ struct Q8Lds {
   float* Y;
 };
 
-__device__ __forceinline__ Q8Lds q8_lds(unsigned char* smem, int K, int nb, int ipw, int ts) {
+__device__ __forceinline__ Q8Lds q8_lds(unsigned char* smem, int K, int nb, int ipw) {
   Q8Lds l;
   l.xs = (float*)smem;
   l.xq = (int8_t*)(l.xs + K);
   l.xdq = (float*)(l.xq + K);
   l.T = l.xdq + ((nb + 3) & ~3);
-  l.Y = l.T + nb * ts;
+  l.Y = l.T + 2 * ipw * q8_row_stride(nb);
   return l;
 }
 
@@ -520,7 +535,7 @@ template <int KP>
 __device__ __forceinline__ void gemv_q8_rows(const GemvArgs& a, int unit, const int* spos, unsigned char* smem,
                                              RowSync& rs, unsigned item) {
   const Q8Geom g = q8_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
-  const Q8Lds l = q8_lds(smem, g.K, g.nb, a.ipw, g.ts);
+  const Q8Lds l = q8_lds(smem, g.K, g.nb, a.ipw);
   // rows wider than 4096 (row_slots 16) are never normalized (d_model <= 4096)
   constexpr bool kNorm = KP <= 8;
   NormW<kNorm ? KP : 1> nwt;
@@ -540,7 +555,7 @@ __device__ __forceinline__ void gemv_q8_rows(const GemvArgs& a, int unit, const 
   const bool many = g.NR > kWave;  // uniform
   if (many || threadIdx.x < kWave) {
     lds_wait(&rs.ws->t_parts, (item + 1) * kWeightWaves, &rs.ws->stop);
-    if ((int)threadIdx.x < g.NR) l.Y[threadIdx.x] = ordered_row_sum(l.T, g.ts, threadIdx.x, g.nb);
+    if ((int)threadIdx.x < g.NR) l.Y[threadIdx.x] = ordered_row_sum(l.T, q8_row_stride(g.nb), threadIdx.x, g.nb);
   }
   if (many) {
     rs.sync();
@@ -599,7 +614,8 @@ __device__ __forceinline__ void w_issue(const Phase* ph, int unit, WItem& it) {
 
 // The item's block terms T[r][blk] = ((f32)(sum qw * qx) * d_w) * d_x into LDS.
 __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
-  const Q8Lds l = q8_lds(smem, it.g.K, it.g.nb, it.ipw, it.g.ts);
+  const Q8Lds l = q8_lds(smem, it.g.K, it.g.nb, it.ipw);
+  const int rs = q8_row_stride(it.g.nb);
   const int nb = it.g.nb;
   const int w = threadIdx.x - kRowThreads;
   int r = w / nb, blk = w - r * nb;
@@ -619,7 +635,7 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
       s = sdot4(it.wb[k].z, xb.z, s);
       s = sdot4(it.wb[k].w, xb.w, s);
       const float t = (float)s * f16_to_f32((uint16_t)it.wd[k]);
-      l.T[blk * it.g.ts + r] = t * l.xdq[blk];
+      l.T[r * rs + blk] = t * l.xdq[blk];
     }
     r += dr;
     blk += db;
