@@ -1683,6 +1683,36 @@ __device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const
 
 // ---- embedding, argmax, norm, copies (row waves) -------------------------------------------------
 
+__device__ __forceinline__ float table_f32(uint16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ float table_f32(float v) { return v; }
+
+// Element i of the text token's row plus the rows of the n_q codebooks' tokens, added in that
+// order.  The raw elements (bf16 bits or f32) of the text row and of 32 codebooks are requested
+// before any is used, so that no load waits for another.  Past n_q the last codebook's row is read
+// again.
+template <typename E>
+__device__ __forceinline__ float embed_sum(const EmbedArgs& a, const uint32_t* stok, int b, int i, bool staged) {
+  constexpr int G = 32;
+  const size_t rows = (size_t)a.card + 1;
+  const E te = ldg((const E*)a.text_emb + (size_t)stok[0] * a.d + i);
+  const E* base = (const E*)(staged ? a.stage : a.emb);
+  float x = 0.0f;
+  for (int c0 = 0; c0 < a.n_q; c0 += G) {
+    E e[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int c = min(c0 + u, a.n_q - 1);
+      // staged: the rows were copied next to each other during the previous step
+      const size_t row = staged ? (size_t)b * a.n_q + c : (size_t)c * rows + stok[1 + c];
+      e[u] = ld_co(base + row * a.d + i);
+    }
+    if (c0 == 0) x = table_f32(te);
+#pragma unroll
+    for (int u = 0; u < G; ++u) x = c0 + u < a.n_q ? x + table_f32(e[u]) : x;
+  }
+  return a.n_q > 0 ? x : table_f32(te);
+}
+
 // SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
 // ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 512.
 // The stream's tokens are staged in LDS first, then every table row is requested at once.  When
@@ -1690,7 +1720,6 @@ __device__ __forceinline__ void attn_dispatch(const AttnArgs& a, int unit, const
 // table rows cost an address-translation miss each; the copies are contiguous).
 __device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* text, const uint32_t* audio, int unit,
                                            const int* spos, bool staged, unsigned char* smem, RowSync& rs) {
-  constexpr int G = 32;  // table rows in flight per round
   uint32_t* stok = (uint32_t*)smem;  // [0]: text token, [1 + c]: token of codebook c
   const int chunks = (a.d + kRowThreads - 1) / kRowThreads;
   const int b = unit / chunks;
@@ -1709,27 +1738,7 @@ __device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* t
   rs.sync();
   const int i = (unit % chunks) * kRowThreads + threadIdx.x;
   if (i >= a.d) return;
-  const size_t rows = (size_t)a.card + 1;
-  const uint32_t t = stok[0];
-  float x = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.text_emb + (size_t)t * a.d + i))
-                          : ldg((const float*)a.text_emb + (size_t)t * a.d + i);
-  for (int c0 = 0; c0 < a.n_q; c0 += G) {
-    // every load is issued (past n_q: the last codebook's row again), so none waits for another
-    float e[G];
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const int c = min(c0 + u, a.n_q - 1);
-      if (staged) {  // the rows were copied next to each other during the previous step
-        const size_t idx = ((size_t)b * a.n_q + c) * a.d + i;
-        e[u] = a.tables_bf16 ? bf16_to_f32(ld_co((const uint16_t*)a.stage + idx)) : ld_co((const float*)a.stage + idx);
-      } else {
-        const size_t idx = ((size_t)c * rows + stok[1 + c]) * a.d + i;
-        e[u] = a.tables_bf16 ? bf16_to_f32(ldg((const uint16_t*)a.emb + idx)) : ldg((const float*)a.emb + idx);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < G; ++u) x = c0 + u < a.n_q ? x + e[u] : x;
-  }
+  const float x = a.tables_bf16 ? embed_sum<uint16_t>(a, stok, b, i, staged) : embed_sum<float>(a, stok, b, i, staged);
   st_co(a.x + (size_t)b * a.d + i, x);
 }
 
