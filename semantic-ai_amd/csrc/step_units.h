@@ -290,24 +290,39 @@ __device__ __forceinline__ void norm_regs(float (&v)[KP], int K, int norm, const
 // q_i = round(x_i * id).  The 32 elements of a block are held by the 32 lanes of a half-wave;
 // after the half-wave maximum, lane u of each half computes d and id of the block of element
 // group u, and every lane takes id back from that lane.
+// The KP half-wave maxima run step by step side by side (each cross-lane step of every slot before
+// the next step), so that the lane exchanges of different slots overlap.
 template <int KP>
 __device__ __forceinline__ void quantize_regs(const float (&v)[KP], int K, int8_t* xq, float* xdq) {
   const int hl = threadIdx.x & 31;
+  uint32_t m[KP];
+#pragma unroll
+  for (int u = 0; u < KP; ++u) m[u] = __float_as_uint(fmaxf(fabsf(v[u]), 0.0f));
+#pragma unroll
+  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0xB1, 0xf, 0xf, false));
+#pragma unroll
+  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x4E, 0xf, 0xf, false));
+#pragma unroll
+  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x141, 0xf, 0xf, false));
+#pragma unroll
+  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x140, 0xf, 0xf, false));
+  uint32_t o[KP];
+#pragma unroll
+  for (int u = 0; u < KP; ++u) o[u] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)m[u], 0x401F);  // lane ^ 16
   float mine = 0.0f;
 #pragma unroll
-  for (int u = 0; u < KP; ++u) {
-    const float m = __uint_as_float(half_max_bits(__float_as_uint(fmaxf(fabsf(v[u]), 0.0f))));
-    mine = hl == u ? m : mine;
-  }
+  for (int u = 0; u < KP; ++u) mine = hl == u ? __uint_as_float(max(m[u], o[u])) : mine;
   const float dm = mine / 127.0f;
   const float idm = dm != 0.0f ? 1.0f / dm : 0.0f;
   const int own = (threadIdx.x & ~31) + hl * kRowThreads;  // first element of lane hl's block
   if (hl < KP && own < K) xdq[own / 32] = f16_to_f32(f32_to_f16(dm));
+  float id[KP];
+#pragma unroll
+  for (int u = 0; u < KP; ++u) id[u] = half_lane(idm, u);
 #pragma unroll
   for (int u = 0; u < KP; ++u) {
-    const float id = half_lane(idm, u);
     const int i = threadIdx.x + u * kRowThreads;
-    if (i < K) xq[i] = (int8_t)sat_i8(roundf(v[u] * id));
+    if (i < K) xq[i] = (int8_t)sat_i8(roundf(v[u] * id[u]));
   }
 }
 
