@@ -110,28 +110,6 @@ __device__ __forceinline__ uint32_t half_max_bits(uint32_t v) {
   return v;
 }
 
-// x of lane u (u < 16, known after unrolling) of the calling lane's 32-lane half.
-__device__ __forceinline__ float half_lane(float x, int u) {
-  switch (u) {
-    case 0: return swizzle<0 << 5>(x);
-    case 1: return swizzle<1 << 5>(x);
-    case 2: return swizzle<2 << 5>(x);
-    case 3: return swizzle<3 << 5>(x);
-    case 4: return swizzle<4 << 5>(x);
-    case 5: return swizzle<5 << 5>(x);
-    case 6: return swizzle<6 << 5>(x);
-    case 7: return swizzle<7 << 5>(x);
-    case 8: return swizzle<8 << 5>(x);
-    case 9: return swizzle<9 << 5>(x);
-    case 10: return swizzle<10 << 5>(x);
-    case 11: return swizzle<11 << 5>(x);
-    case 12: return swizzle<12 << 5>(x);
-    case 13: return swizzle<13 << 5>(x);
-    case 14: return swizzle<14 << 5>(x);
-    default: return swizzle<15 << 5>(x);
-  }
-}
-
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its
 // outstanding global loads (which __syncthreads would wait for).
 __device__ __forceinline__ void lds_barrier() {

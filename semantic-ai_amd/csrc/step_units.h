@@ -285,44 +285,129 @@ __device__ __forceinline__ void norm_regs(float (&v)[KP], int K, int norm, const
   }
 }
 
-// candle BlockQ8_0::from_float of the row in v into xq (int8, LDS) and xdq (the f16-rounded
+// ---- rows in 4-element chunks (Q8_0 activation quantization) -------------------------------------
+// The Q8_0 paths hold the input row as 4-element chunks: thread t owns elements 4 c .. 4 c + 3 of
+// chunks c = t + 512 u, u < KU = chunk_slots(K); a Q8_0 block (32 elements) is the chunks of 8
+// consecutive lanes, so that its maximum takes three lane exchanges and each element costs a few
+// instructions.  Chunks past K / 4 hold 0.
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr int chunk_slots(int K) { return (K + 4 * kRowThreads - 1) / (4 * kRowThreads); }
+
+// v[u] = the chunk's four elements: one 16-byte coherent (agent scope, the sc1 cache policy)
+// buffer load per chunk over the row x (16-byte aligned), all in flight together.  When `issued`
+// is given, the wave counts itself there once its loads are requested.
+template <int KU>
+__device__ __forceinline__ void load_row4(const float* x, int K, v4f (&v)[KU], unsigned* issued = nullptr) {
+  const int nc = K / 4;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, K * 4, 0x00020000);
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int c = min((int)threadIdx.x + u * kRowThreads, nc - 1);
+    v[u] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, 16 * c, 0, 16));
+  }
+  if (issued) {
+    __builtin_amdgcn_sched_barrier(0);
+    lds_signal(issued);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int u = 0; u < KU; ++u)
+    if ((int)threadIdx.x + u * kRowThreads >= nc) v[u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+template <int KU>
+struct NormW4 {
+  v4f w[KU], b[KU];
+};
+
+template <int KU>
+__device__ __forceinline__ void load_norm_weights4(int norm, const float* nw, const float* nb, int K, NormW4<KU>& o) {
+  const int nc = K / 4;
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int c = min((int)threadIdx.x + u * kRowThreads, nc - 1);
+    o.w[u] = ldg((const v4f*)nw + c);
+    o.b[u] = norm == NORM_LAYER ? ldg((const v4f*)nb + c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+}
+
+// norm_regs on the chunked row: the same statistics over xs in the blocked order, the same
+// per-element arithmetic.
+template <int KU>
+__device__ __forceinline__ void norm_row4(v4f (&v)[KU], int K, int norm, const NormW4<KU>& nw, float eps, float* xs,
+                                          RowSync& rs) {
+  const int nc = K / 4;
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int c = threadIdx.x + u * kRowThreads;
+    if (c < nc) ((v4f*)xs)[c] = v[u];
+  }
+  rs.sync();
+  float s, s2;
+  if (norm == NORM_LAYER) blocked_sums<true>(xs, K, s, s2);
+  else blocked_sums<false>(xs, K, s, s2);
+  s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));
+  s2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s2)));
+  if (norm == NORM_RMS) {
+    const float s0 = sqrtf(s2 / (float)K + eps);
+#pragma unroll
+    for (int u = 0; u < KU; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float t = v[u][e] / s0;
+        v[u][e] = t * nw.w[u][e];
+      }
+  } else {
+    const float mean = s / (float)K;
+    const float mm = mean * mean;
+    const float var = s2 / (float)K - mm;
+    const float s1 = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int u = 0; u < KU; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = (v[u][e] - mean) * s1;
+        t = t * nw.w[u][e];
+        v[u][e] = t + nw.b[u][e];
+      }
+  }
+}
+
+// candle BlockQ8_0::from_float of the chunked row into xq (int8, LDS) and xdq (the f16-rounded
 // block scales as f32, LDS): amax = max(0, |x_i|...), d = amax / 127, id = 1 / d (0 if d = 0),
-// q_i = round(x_i * id).  The 32 elements of a block are held by the 32 lanes of a half-wave;
-// after the half-wave maximum, lane u of each half computes d and id of the block of element
-// group u, and every lane takes id back from that lane.
-// The KP half-wave maxima run step by step side by side (each cross-lane step of every slot before
-// the next step), so that the lane exchanges of different slots overlap.
-template <int KP>
-__device__ __forceinline__ void quantize_regs(const float (&v)[KP], int K, int8_t* xq, float* xdq) {
-  const int hl = threadIdx.x & 31;
-  uint32_t m[KP];
+// q_i = round(x_i * id).  The block maximum runs over 8 lanes (after each lane's maximum of its
+// four elements); every lane then computes its block's d and id and writes its four quantized
+// elements as one word; lane 0 of the 8 writes the block scale.
+template <int KU>
+__device__ __forceinline__ void quantize_row4(const v4f (&v)[KU], int K, int8_t* xq, float* xdq) {
+  const int nc = K / 4;
+  uint32_t m[KU];
 #pragma unroll
-  for (int u = 0; u < KP; ++u) m[u] = __float_as_uint(fmaxf(fabsf(v[u]), 0.0f));
+  for (int u = 0; u < KU; ++u) {
+    const uint32_t a0 = __float_as_uint(fmaxf(fabsf(v[u].x), 0.0f)), a1 = __float_as_uint(fmaxf(fabsf(v[u].y), 0.0f));
+    const uint32_t a2 = __float_as_uint(fmaxf(fabsf(v[u].z), 0.0f)), a3 = __float_as_uint(fmaxf(fabsf(v[u].w), 0.0f));
+    m[u] = max(max(a0, a1), max(a2, a3));
+  }
 #pragma unroll
-  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0xB1, 0xf, 0xf, false));
+  for (int u = 0; u < KU; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0xB1, 0xf, 0xf, false));
 #pragma unroll
-  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x4E, 0xf, 0xf, false));
+  for (int u = 0; u < KU; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x4E, 0xf, 0xf, false));
 #pragma unroll
-  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x141, 0xf, 0xf, false));
+  for (int u = 0; u < KU; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x141, 0xf, 0xf, false));
 #pragma unroll
-  for (int u = 0; u < KP; ++u) m[u] = max(m[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m[u], 0x140, 0xf, 0xf, false));
-  uint32_t o[KP];
-#pragma unroll
-  for (int u = 0; u < KP; ++u) o[u] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)m[u], 0x401F);  // lane ^ 16
-  float mine = 0.0f;
-#pragma unroll
-  for (int u = 0; u < KP; ++u) mine = hl == u ? __uint_as_float(max(m[u], o[u])) : mine;
-  const float dm = mine / 127.0f;
-  const float idm = dm != 0.0f ? 1.0f / dm : 0.0f;
-  const int own = (threadIdx.x & ~31) + hl * kRowThreads;  // first element of lane hl's block
-  if (hl < KP && own < K) xdq[own / 32] = f16_to_f32(f32_to_f16(dm));
-  float id[KP];
-#pragma unroll
-  for (int u = 0; u < KP; ++u) id[u] = half_lane(idm, u);
-#pragma unroll
-  for (int u = 0; u < KP; ++u) {
-    const int i = threadIdx.x + u * kRowThreads;
-    if (i < K) xq[i] = (int8_t)sat_i8(roundf(v[u] * id[u]));
+  for (int u = 0; u < KU; ++u) {
+    const int c = threadIdx.x + u * kRowThreads;
+    if (c >= nc) continue;  // uniform per 8 lanes (nc is a multiple of 8)
+    const float dm = __uint_as_float(m[u]) / 127.0f;
+    const float idm = dm != 0.0f ? 1.0f / dm : 0.0f;
+    if ((c & 7) == 0) xdq[c / 8] = f16_to_f32(f32_to_f16(dm));
+    const uint32_t q0 = (uint32_t)sat_i8(roundf(v[u].x * idm)) & 0xffu;
+    const uint32_t q1 = (uint32_t)sat_i8(roundf(v[u].y * idm)) & 0xffu;
+    const uint32_t q2 = (uint32_t)sat_i8(roundf(v[u].z * idm)) & 0xffu;
+    const uint32_t q3 = (uint32_t)sat_i8(roundf(v[u].w * idm)) & 0xffu;
+    ((uint32_t*)xq)[c] = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
   }
 }
 
@@ -551,20 +636,21 @@ __device__ __forceinline__ void gemv_q8_rows(const GemvArgs& a, int unit, const 
                                              RowSync& rs, unsigned item) {
   const Q8Geom g = q8_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
   const Q8Lds l = q8_lds(smem, g.K, g.nb, a.ipw);
+  constexpr int KU = chunk_slots(KP * kRowThreads);
   // rows wider than 4096 (row_slots 16) are never normalized (d_model <= 4096)
   constexpr bool kNorm = KP <= 8;
-  NormW<kNorm ? KP : 1> nwt;
-  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, g.K, nwt);
-  float v[KP];
-  load_row(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
+  NormW4<kNorm ? KU : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights4(a.norm, a.nw, a.nb, g.K, nwt);
+  v4f v[KU];
+  load_row4(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
   const int p = (a.epi == EPI_QKV_ROPE || a.advance_pos ? spos[g.b] : 0);
   const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   if constexpr (kNorm) {
-    if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
+    if (a.norm != NORM_NONE) norm_row4(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
   }
   // the weight waves have read the previous item's quantized row
   lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
-  quantize_regs(v, g.K, l.xq, l.xdq);
+  quantize_row4(v, g.K, l.xq, l.xdq);
   lds_signal(&rs.ws->xq_parts);
   // one thread per row adds the row's terms in block order once every term is written
   const bool many = g.NR > kWave;  // uniform
@@ -959,15 +1045,16 @@ __device__ __forceinline__ void quant_unit(const GemvArgs& a, int b, unsigned ch
   float* xs = (float*)smem;
   int8_t* xq = (int8_t*)(xs + K);
   float* xdq = (float*)(xq + K);
+  constexpr int KU = chunk_slots(KP * kRowThreads);
   constexpr bool kNorm = KP <= 8;
-  NormW<kNorm ? KP : 1> nwt;
-  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
-  float v[KP];
-  load_row(a.x + (size_t)b * a.x_stride, K, v);
+  NormW4<kNorm ? KU : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights4(a.norm, a.nw, a.nb, K, nwt);
+  v4f v[KU];
+  load_row4(a.x + (size_t)b * a.x_stride, K, v);
   if constexpr (kNorm) {
-    if (a.norm != NORM_NONE) norm_regs(v, K, a.norm, nwt, a.eps, xs, rs);
+    if (a.norm != NORM_NONE) norm_row4(v, K, a.norm, nwt, a.eps, xs, rs);
   }
-  quantize_regs(v, K, xq, xdq);
+  quantize_row4(v, K, xq, xdq);
   rs.sync();
   uint32_t* dq = (uint32_t*)(a.xq + (size_t)b * K);
   for (int i = threadIdx.x; i < K / 4; i += kRowThreads) st_co(dq + i, ((const uint32_t*)xq)[i]);
