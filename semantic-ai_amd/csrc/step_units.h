@@ -1260,16 +1260,20 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
       GemmOps o;
       gemm_read(gemm_stage(smem, (c + u) % kGemmStages), ja, jb, g, r0, o);
       const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
+      // the chunk's block products first (independent), then their terms added in block order
+      const int nk = min(kGemmChunk, nb - kGemmChunk * (c + u));  // uniform: 4 except in a last partial chunk
+      v4i cc[kGemmChunk];
+#pragma unroll
+      for (int kk = 0; kk < kGemmChunk; ++kk)
+        cc[kk] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
       for (int kk = 0; kk < kGemmChunk; ++kk) {
-        if (kGemmChunk * (c + u) + kk >= nb) break;  // uniform
-        v4i cc = {0, 0, 0, 0};
-        cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], cc, 0, 0, 0);
+        if (kk >= nk) break;  // uniform
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t dwp = kk == 0 ? o.dw[i].x : (kk == 1 ? o.dw[i].y : (kk == 2 ? o.dw[i].z : o.dw[i].w));
           const float dw = f16_to_f32((uint16_t)(dwp & 0xFFFF));
-          const float t = (float)cc[i] * dw;
+          const float t = (float)cc[kk][i] * dw;
           acc[i] = acc[i] + t * dxs[kk];
         }
       }
