@@ -63,6 +63,10 @@ typedef struct {
     int32_t card, n_q, text_card;    /* STT */
     int32_t latent_dim, z_dim;       /* TTS (z_dim 0: no z_proj) */
     int32_t kv_dtype;      /* SVL_F32 (default) or SVL_BF16: element type of the KV ring buffers */
+    int32_t extra_heads_num, extra_heads_dim;  /* STT extra (VAD) heads, SttConfig's
+                              extra_heads_num_heads / extra_heads_dim (SVL/stt/model.rs:217-222):
+                              dense "extra_heads.{i}.weight" [dim][d_model], never quantized;
+                              0 = none */
 } svl_config;
 
 /* One named tensor (the reference's safetensors names, e.g.
@@ -130,6 +134,14 @@ int svl_transformer_forward(const svl_model* model, svl_state* state, const floa
 int svl_stt_step(const svl_model* model, svl_state* state, const uint32_t* text_tokens,
                  const uint32_t* audio_tokens, uint32_t* out_tokens, float* out_logits);
 
+/* LanguageModel::step with its Prediction (SVL/stt/model.rs:189-193, 239-276): as svl_stt_step,
+ * and out_probs [batch][extra_heads_num] receives, per extra head, the probability of its first
+ * class (softmax of the head's logits over the out_norm'ed output, index 0; the VAD heads'
+ * "no speech").  out_probs may be NULL. */
+int svl_stt_step_heads(const svl_model* model, svl_state* state, const uint32_t* text_tokens,
+                       const uint32_t* audio_tokens, uint32_t* out_tokens, float* out_logits,
+                       float* out_probs);
+
 /* Recognizer::step's token loop (SVL/stt/mod.rs:551-566) for n_steps steps with no host round
  * trip: the text token of a step is the previous step's argmax (text_card before the first
  * step of a stream), and a stream's first step (position 0) sees `card` for every audio
@@ -139,6 +151,16 @@ int svl_stt_recognize(const svl_model* model, svl_state* state, int64_t n_steps,
 /* The same, enqueued on the state's stream; device pointers; returns without waiting. */
 int svl_stt_recognize_async(const svl_model* model, svl_state* state, int64_t n_steps,
                             const uint32_t* d_audio_tokens, uint32_t* d_out_tokens);
+/* svl_stt_recognize with the extra heads' first-class probabilities of every step
+ * (Prediction::extra_head_probabilities, SVL/stt/model.rs:259-271, as the recognizer's turn
+ * detection reads them, SVL/stt/mod.rs:327-350): out_probs [n_steps][batch][extra_heads_num].
+ * Host pointers. */
+int svl_stt_recognize_heads(const svl_model* model, svl_state* state, int64_t n_steps,
+                            const uint32_t* audio_tokens, uint32_t* out_tokens, float* out_probs);
+/* The same with device pointers, enqueued on the state's stream; d_out_probs may be NULL. */
+int svl_stt_recognize_heads_async(const svl_model* model, svl_state* state, int64_t n_steps,
+                                  const uint32_t* d_audio_tokens, uint32_t* d_out_tokens,
+                                  float* d_out_probs);
 
 /* FlowLm::step's backbone (SVL/tts/flow_lm.rs:169-180) for every stream: latent
  * [batch][latent_dim] f32, or NULL for the learnt `bos_emb` -> z [batch][z_dim or d_model]. */

@@ -51,6 +51,7 @@ class Config(C.Structure):
         ("quantize", C.c_int32),
         ("card", C.c_int32), ("n_q", C.c_int32), ("text_card", C.c_int32),
         ("latent_dim", C.c_int32), ("z_dim", C.c_int32),
+        ("extra_heads_num", C.c_int32), ("extra_heads_dim", C.c_int32),
     ]
 
 
@@ -122,9 +123,11 @@ def lib():
             L.svlo_state_from_layer_caches.restype = vp
             L.svlo_transformer_forward.argtypes = [vp, vp, vp, C.c_int64, vp]
             L.svlo_transformer_forward.restype = C.c_int
-            L.svlo_stt_step.argtypes = [vp, vp, C.c_uint32, vp, C.POINTER(C.c_uint32), vp]
+            L.svlo_stt_step.argtypes = [vp, vp, C.c_uint32, vp, C.POINTER(C.c_uint32), vp, vp]
             L.svlo_stt_step.restype = C.c_int
-            L.svlo_stt_greedy.argtypes = [vp, vp, C.c_int64, vp, vp, vp]
+            L.svlo_stt_greedy.argtypes = [vp, vp, C.c_int64, vp, vp, vp, vp]
+            L.svlo_softmax_first.argtypes = [vp, sz]
+            L.svlo_softmax_first.restype = C.c_float
             L.svlo_stt_greedy.restype = C.c_int
             L.svlo_tts_backbone_step.argtypes = [vp, vp, vp, vp]
             L.svlo_tts_backbone_step.restype = C.c_int
@@ -317,6 +320,12 @@ def rope_i(x, cos_t, sin_t) -> np.ndarray:
     return y
 
 
+def softmax_first(x) -> float:
+    """Element 0 of softmax(x) (the oracle's restatement of candle's softmax_last_dim)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return float(lib().svlo_softmax_first(_p(x), x.size))
+
+
 def argmax(x) -> int:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return int(lib().svlo_argmax(_p(x), x.size))
@@ -415,27 +424,36 @@ class State:
             raise ValueError(lib().svlo_last_error().decode())
         return ys
 
-    def stt_step(self, text_token: int, audio, want_logits: bool = False):
+    def stt_step(self, text_token: int, audio, want_logits: bool = False, want_probs: bool = False):
         audio = np.ascontiguousarray(audio, dtype=np.uint32)
         tok = C.c_uint32()
         logits = np.empty(self.model.cfg["text_card"], dtype=np.float32) if want_logits else None
+        probs = (np.empty(self.model.cfg.get("extra_heads_num", 0), dtype=np.float32)
+                 if want_probs else None)
         rc = lib().svlo_stt_step(self.model.h, self.h, text_token, _p(audio), C.byref(tok),
-                                 None if logits is None else _p(logits))
+                                 None if logits is None else _p(logits),
+                                 None if probs is None else _p(probs))
         if rc:
             raise ValueError(lib().svlo_last_error().decode())
-        return (tok.value, logits) if want_logits else tok.value
+        res = (tok.value,) + ((logits,) if want_logits else ()) + ((probs,) if want_probs else ())
+        return res if len(res) > 1 else tok.value
 
-    def stt_greedy(self, audio, n: int | None = None, want_logits: bool = False):
+    def stt_greedy(self, audio, n: int | None = None, want_logits: bool = False,
+                   want_probs: bool = False):
         audio = np.ascontiguousarray(audio, dtype=np.uint32)
         nq = self.model.cfg["n_q"]
         n = audio.size // nq if n is None else n
         out = np.empty(n, dtype=np.uint32)
         logits = np.empty(self.model.cfg["text_card"], dtype=np.float32) if want_logits else None
+        probs = (np.empty((n, self.model.cfg.get("extra_heads_num", 0)), dtype=np.float32)
+                 if want_probs else None)
         rc = lib().svlo_stt_greedy(self.model.h, self.h, n, _p(audio), _p(out),
-                                   None if logits is None else _p(logits))
+                                   None if logits is None else _p(logits),
+                                   None if probs is None else _p(probs))
         if rc:
             raise ValueError(lib().svlo_last_error().decode())
-        return (out, logits) if want_logits else out
+        res = (out,) + ((logits,) if want_logits else ()) + ((probs,) if want_probs else ())
+        return res if len(res) > 1 else out
 
     def tts_step(self, latent=None) -> np.ndarray:
         cfg = self.model.cfg

@@ -289,3 +289,19 @@ uint32_t svlo_argmax(const float* x, size_t n) {
         }
     return best;
 }
+
+/* [candle hypothesis] candle-nn ops::softmax_last_dim on the CPU, as LanguageModel::step applies it
+ * to each extra head's logits (SVL/stt/model.rs:262-268): the maximum in index order starting
+ * from x[0], exp(x_i - max) with the C library's expf (Rust's f32::exp), their sum in index
+ * order from zero, then element 0 divided by the sum (the step keeps only `.i(0)`). */
+float svlo_softmax_first(const float* x, size_t n) {
+    float mx = x[0];
+    for (size_t i = 1; i < n; ++i) mx = fmaxf(mx, x[i]);
+    float sum = 0.0f, first = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        const float e = expf(x[i] - mx);
+        if (i == 0) first = e;
+        sum += e;
+    }
+    return first / sum;
+}

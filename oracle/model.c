@@ -179,6 +179,7 @@ struct svlo_model {
     float* out_norm_w;
     float* out_norm_b;
     linear_t text_linear;
+    linear_t* extra_heads; /* extra_heads_num dense [extra_heads_dim, d] */
     /* TTS */
     linear_t input_linear, z_proj;
     float* bos;
@@ -203,6 +204,10 @@ void svlo_model_destroy(svlo_model* m) {
     free(m->out_norm_w);
     free(m->out_norm_b);
     linear_free(&m->text_linear);
+    if (m->extra_heads) {
+        for (int i = 0; i < m->cfg.extra_heads_num; ++i) linear_free(&m->extra_heads[i]);
+        free(m->extra_heads);
+    }
     linear_free(&m->input_linear);
     linear_free(&m->z_proj);
     free(m->bos);
@@ -281,6 +286,19 @@ int svlo_model_create(const svlo_config* cfg, const svlo_tensor* tensors, size_t
         m->out_norm_w = load_f32(&ts, "out_norm.alpha", d, &rc);
         if (!m->out_norm_w) goto done;
         if ((rc = load_linear(&ts, "text_linear.weight", (size_t)c->text_card, d, c->quantize, &m->text_linear))) goto done;
+        /* SVL/stt/model.rs:217-222: extra_heads.{i} are dense Linear [extra_heads_dim, d]
+         * without bias, never quantized */
+        if (c->extra_heads_num < 0 || (c->extra_heads_num > 0 && c->extra_heads_dim <= 0)) {
+            rc = fail("invalid extra heads config");
+            goto done;
+        }
+        if (c->extra_heads_num > 0) {
+            m->extra_heads = (linear_t*)calloc((size_t)c->extra_heads_num, sizeof(linear_t));
+            for (int i = 0; i < c->extra_heads_num; ++i) {
+                snprintf(name, sizeof(name), "extra_heads.%d.weight", i);
+                if ((rc = load_linear(&ts, name, (size_t)c->extra_heads_dim, d, 0, &m->extra_heads[i]))) goto done;
+            }
+        }
     } else if (c->kind == SVLO_MODEL_TTS) {
         /* SVL/tts/flow_lm.rs:72-74, 97-115: these linears are always dense (Linear::new) */
         if (c->latent_dim <= 0) { rc = fail("invalid TTS config"); goto done; }
@@ -562,9 +580,9 @@ int svlo_transformer_forward(const svlo_model* m, svlo_state* s, const float* xs
     return 0;
 }
 
-/* LanguageModel::step, SVL/stt/model.rs:239-276 (extra heads omitted: none in these shapes). */
+/* LanguageModel::step, SVL/stt/model.rs:239-276. */
 int svlo_stt_step(const svlo_model* m, svlo_state* s, uint32_t text_token, const uint32_t* audio,
-                  uint32_t* out_token, float* out_logits) {
+                  uint32_t* out_token, float* out_logits, float* out_probs) {
     const svlo_config* c = &m->cfg;
     if (c->kind != SVLO_MODEL_STT) return fail("not an STT model");
     if (s->b != 1) return fail("stt_step: batch 1 only");
@@ -588,6 +606,15 @@ int svlo_stt_step(const svlo_model* m, svlo_state* s, uint32_t text_token, const
         linear_forward(&m->text_linear, x, 1, logits);
         *out_token = svlo_argmax(logits, (size_t)c->text_card);
         if (out_logits) memcpy(out_logits, logits, sizeof(float) * (size_t)c->text_card);
+        /* SVL/stt/model.rs:259-271: per extra head, softmax of its logits, probability 0 */
+        if (out_probs && c->extra_heads_num > 0) {
+            float* hl = (float*)malloc(sizeof(float) * (size_t)c->extra_heads_dim);
+            for (int h = 0; h < c->extra_heads_num; ++h) {
+                linear_forward(&m->extra_heads[h], x, 1, hl);
+                out_probs[h] = svlo_softmax_first(hl, (size_t)c->extra_heads_dim);
+            }
+            free(hl);
+        }
     }
     free(x); free(y); free(logits);
     return rc;
@@ -595,7 +622,7 @@ int svlo_stt_step(const svlo_model* m, svlo_state* s, uint32_t text_token, const
 
 /* Recognizer::step token feedback, SVL/stt/mod.rs:551-566. */
 int svlo_stt_greedy(const svlo_model* m, svlo_state* s, int64_t n, const uint32_t* audio,
-                    uint32_t* out_tokens, float* out_last_logits) {
+                    uint32_t* out_tokens, float* out_last_logits, float* out_probs) {
     const svlo_config* c = &m->cfg;
     uint32_t* initial = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)c->n_q);
     for (int i = 0; i < c->n_q; ++i) initial[i] = (uint32_t)c->card;
@@ -604,7 +631,8 @@ int svlo_stt_greedy(const svlo_model* m, svlo_state* s, int64_t n, const uint32_
     for (int64_t i = 0; i < n && rc == 0; ++i) {
         const uint32_t* a = (s->position == 0) ? initial : audio + (size_t)i * (size_t)c->n_q;
         uint32_t tok = 0;
-        rc = svlo_stt_step(m, s, text, a, &tok, (i == n - 1) ? out_last_logits : NULL);
+        rc = svlo_stt_step(m, s, text, a, &tok, (i == n - 1) ? out_last_logits : NULL,
+                           out_probs ? out_probs + (size_t)i * (size_t)c->extra_heads_num : NULL);
         out_tokens[i] = tok;
         text = tok;
     }

@@ -80,6 +80,8 @@ void svlo_rope_i(float* x, const float* cos_t, const float* sin_t, size_t bh, si
 void svlo_rope_tables(size_t position, size_t t, size_t head_dim, double max_period, float* cos_t,
                       float* sin_t);
 uint32_t svlo_argmax(const float* x, size_t n);
+/* softmax over x[0..n) (candle-nn softmax_last_dim), returning its first element */
+float svlo_softmax_first(const float* x, size_t n);
 
 /* ---- model ------------------------------------------------------------------------------ */
 
@@ -102,6 +104,7 @@ typedef struct {
     int32_t card, n_q, text_card;
     /* TTS */
     int32_t latent_dim, z_dim; /* z_dim 0 = no z_proj */
+    int32_t extra_heads_num, extra_heads_dim; /* STT VAD heads (0: none) */
 } svlo_config;
 
 typedef struct {
@@ -135,13 +138,14 @@ svlo_state* svlo_state_from_layer_caches(const svlo_model* m, int32_t batch, int
 
 /* xs [b, t, d] -> ys [b, t, d] */
 int svlo_transformer_forward(const svlo_model* m, svlo_state* s, const float* xs, int64_t t, float* ys);
-/* batch 1: text token + n_q audio tokens -> argmax; logits (text_card) optional */
+/* batch 1: text token + n_q audio tokens -> argmax; logits (text_card) and the extra heads'
+ * first-class probabilities (extra_heads_num) optional */
 int svlo_stt_step(const svlo_model* m, svlo_state* s, uint32_t text_token, const uint32_t* audio,
-                  uint32_t* out_token, float* out_logits);
+                  uint32_t* out_token, float* out_logits, float* out_probs);
 /* Recognizer loop: n steps, audio [n * n_q]; step 0 of a fresh state sees `card` tokens; text
  * token = previous argmax, initially text_card. */
 int svlo_stt_greedy(const svlo_model* m, svlo_state* s, int64_t n, const uint32_t* audio,
-                    uint32_t* out_tokens, float* out_last_logits);
+                    uint32_t* out_tokens, float* out_last_logits, float* out_probs /* [n][heads] */);
 /* latent [latent_dim] or NULL (bos) -> z [z_dim or d_model] */
 int svlo_tts_backbone_step(const svlo_model* m, svlo_state* s, const float* latent, float* out_z);
 

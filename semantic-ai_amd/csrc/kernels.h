@@ -97,6 +97,10 @@ struct ArgmaxArgs {
   int B, V;
   uint32_t* fb_tok;         // [B]
   uint32_t* out;            // [B] or null
+  // STT extra heads: softmax over each head's hd logits, element 0 (nh = 0: none)
+  const float* xlogits;     // [B][nh * hd]
+  int nh, hd;
+  float* xprob;             // [B][nh], the last step's probabilities
 };
 
 struct NormArgs {           // y[b] = norm(x[b]) (TTS out_norm without z_proj)
@@ -158,6 +162,8 @@ struct StepParams {
   size_t text_stride;
   uint32_t* out_tok;             // step s: out_tok + s * out_stride, or null
   size_t out_stride;
+  float* out_prob;               // step s: out_prob + s * prob_stride (extra heads), or null
+  size_t prob_stride;
   const float* fwd_in;           // [B][T][d], step s reads column s
   float* fwd_out;
   int fwd_T;

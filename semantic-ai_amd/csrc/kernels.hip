@@ -123,29 +123,30 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
 // going to memory one after another.
 __device__ __forceinline__ void touch_kernel_args() {
   const void* k = (const void*)__builtin_amdgcn_kernarg_segment_ptr();
-  unsigned d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10;
+  unsigned d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11;
   asm volatile(
-      "s_load_dword %0, %11, 0x0\n\t"
-      "s_load_dword %1, %11, 0x40\n\t"
-      "s_load_dword %2, %11, 0x80\n\t"
-      "s_load_dword %3, %11, 0xc0\n\t"
-      "s_load_dword %4, %11, 0x100\n\t"
-      "s_load_dword %5, %11, 0x140\n\t"
-      "s_load_dword %6, %11, 0x180\n\t"
-      "s_load_dword %7, %11, 0x1c0\n\t"
-      "s_load_dword %8, %11, 0x200\n\t"
-      "s_load_dword %9, %11, 0x240\n\t"
-      "s_load_dword %10, %11, 0x280\n\t"
+      "s_load_dword %0, %12, 0x0\n\t"
+      "s_load_dword %1, %12, 0x40\n\t"
+      "s_load_dword %2, %12, 0x80\n\t"
+      "s_load_dword %3, %12, 0xc0\n\t"
+      "s_load_dword %4, %12, 0x100\n\t"
+      "s_load_dword %5, %12, 0x140\n\t"
+      "s_load_dword %6, %12, 0x180\n\t"
+      "s_load_dword %7, %12, 0x1c0\n\t"
+      "s_load_dword %8, %12, 0x200\n\t"
+      "s_load_dword %9, %12, 0x240\n\t"
+      "s_load_dword %10, %12, 0x280\n\t"
+      "s_load_dword %11, %12, 0x2c0\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7), "=&s"(d8),
-        "=&s"(d9), "=&s"(d10)
+        "=&s"(d9), "=&s"(d10), "=&s"(d11)
       : "s"(k)
       : "memory");
 }
 
 template <unsigned F, unsigned KM, int V>
 __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, StepParams P, int step) {
-  static_assert(sizeof(Phase) + sizeof(StepParams) + sizeof(int) <= 0x2c0, "kernel arguments past the touched lines");
+  static_assert(sizeof(Phase) + sizeof(StepParams) + sizeof(int) <= 0x300, "kernel arguments past the touched lines");
   touch_kernel_args();
   const Phase* d_ph = &ph;
   extern __shared__ __align__(16) unsigned char smem[];

@@ -1862,8 +1862,8 @@ __device__ __forceinline__ void gather_unit(const EmbedArgs& a, const uint32_t* 
 }
 
 // argmax over logits[b] (first index of the maximum); unit = stream.
-__device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, int unit, unsigned char* smem,
-                                            RowSync& rs) {
+__device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, float* out_prob, int unit,
+                                            unsigned char* smem, RowSync& rs) {
   float* sv = (float*)smem;
   int* si = (int*)(sv + kRowWaves);
   const int b = unit;
@@ -1914,6 +1914,24 @@ __device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, 
     if (bi == 0x7fffffff) bi = 0;
     st_co(a.fb_tok + b, (uint32_t)bi);
     if (out) st_co(out + b, (uint32_t)bi);
+  }
+  // Extra heads (SVL/stt/model.rs:259-271): thread kWave + h takes head h's logits through
+  // candle-nn's softmax_last_dim as the oracle restates it -- the maximum in index order from
+  // element 0, exp(l_i - max), their sum in index order from zero -- and keeps element 0.
+  const int h = (int)threadIdx.x - kWave;
+  if (h >= 0 && h < a.nh) {
+    const float* l = a.xlogits + ((size_t)b * a.nh + h) * a.hd;
+    float mx = ld_co(l);
+    for (int i = 1; i < a.hd; ++i) mx = fmaxf(mx, ld_co(l + i));
+    float sum = 0.0f, first = 0.0f;
+    for (int i = 0; i < a.hd; ++i) {
+      const float e = expf(ld_co(l + i) - mx);
+      if (i == 0) first = e;
+      sum = sum + e;
+    }
+    const float p = first / sum;
+    st_co(a.xprob + (size_t)b * a.nh + h, p);
+    if (out_prob) st_co(out_prob + (size_t)b * a.nh + h, p);
   }
 }
 
@@ -2040,7 +2058,8 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
       break;
     case PH_ARGMAX:
       if constexpr (!(KM & kind_bit(PH_ARGMAX))) break;
-      argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr, unit, smem, rs);
+      argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr,
+                  P.out_prob ? P.out_prob + (size_t)step * P.prob_stride : nullptr, unit, smem, rs);
       break;
     case PH_NORM:
       if constexpr (!(KM & kind_bit(PH_NORM))) break;

@@ -97,6 +97,7 @@ struct svl_model {
   float* out_norm_w = nullptr;
   float* out_norm_b = nullptr;
   LinearDev text_linear;
+  LinearDev extra_heads;  // the extra heads' weights stacked: [extra_heads_num * extra_heads_dim][d]
   // TTS
   LinearDev input_linear, z_proj;
   float* bos = nullptr;
@@ -137,6 +138,8 @@ struct svl_state {
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
   float* in = nullptr;        // TTS latent staging [B][latent_dim]
+  float* xlogits = nullptr;   // STT extra heads: logits [B][nh * hd]
+  float* xprob = nullptr;     //                  first-class probabilities [B][nh]
   float* fwd = nullptr;       // transformer forward staging (input then output)
   size_t fwd_cap = 0;
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
@@ -382,6 +385,44 @@ int ensure_rope(const svl_model* m, int64_t needed) {
   return 0;
 }
 
+// LanguageModel::new's extra heads (SVL/stt/model.rs:217-222): extra_heads.{i}.weight, dense
+// [extra_heads_dim][d] without bias, loaded unquantized (Linear::load(.., false)).  The heads are
+// stacked into one linear of extra_heads_num * extra_heads_dim rows: each output row is its own
+// dot product, so stacking changes no arithmetic.
+int load_extra_heads(svl_model* m, const svl_tensor* ts, size_t n) {
+  const svl_config& c = m->cfg;
+  const int nh = c.extra_heads_num, hd = c.extra_heads_dim, d = c.d_model;
+  if (nh == 0) return 0;
+  if (nh < 0 || nh > 256 || hd <= 0 || hd > 4096)
+    return set_error(SVL_ERR_CONFIG, "extra heads: need 0 <= extra_heads_num <= 256 and 1 <= extra_heads_dim <= 4096");
+  int dtype = -1;
+  std::vector<const svl_tensor*> parts(nh);
+  for (int i = 0; i < nh; ++i) {
+    const std::string name = "extra_heads." + std::to_string(i) + ".weight";
+    const svl_tensor* t = find_tensor(ts, n, name);
+    if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", name.c_str());
+    if (t->ndim != 2 || t->shape[0] != hd || t->shape[1] != d)
+      return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: shape mismatch (expected [%d, %d])", name.c_str(), hd, d);
+    if (t->dtype != SVL_F32 && t->dtype != SVL_BF16 && t->dtype != SVL_F16)
+      return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: the extra heads are dense (f32, bf16 or f16)", name.c_str());
+    if (dtype >= 0 && t->dtype != dtype)
+      return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: the extra heads must share one dtype", name.c_str());
+    dtype = t->dtype;
+    parts[i] = t;
+  }
+  const size_t esz = dtype == SVL_F32 ? 4 : 2, one = (size_t)hd * d * esz;
+  std::vector<unsigned char> stacked(one * nh);
+  for (int i = 0; i < nh; ++i) memcpy(stacked.data() + one * i, parts[i]->data, one);
+  svl_tensor all{};
+  all.name = "extra_heads";
+  all.dtype = dtype;
+  all.ndim = 2;
+  all.shape[0] = (int64_t)nh * hd;
+  all.shape[1] = d;
+  all.data = stacked.data();
+  return load_linear(m, &all, 1, "extra_heads", nh * hd, d, 0, &m->extra_heads);
+}
+
 int check_config(const svl_config* c) {
   if (c->d_model <= 0 || c->num_layers <= 0 || c->num_heads <= 0 || c->num_kv_heads <= 0 || c->head_dim <= 0)
     return set_error(SVL_ERR_CONFIG, "invalid transformer dimensions");
@@ -464,6 +505,7 @@ int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_mode
       TRY(load_table(m, ts, n, "emb." + std::to_string(i) + ".weight", rows, (char*)m->emb + rows * i * esz));
     TRY(load_vec(m, ts, n, "out_norm.alpha", d, &m->out_norm_w));
     TRY(load_linear(m, ts, n, "text_linear.weight", c.text_card, d, c.quantize, &m->text_linear));
+    TRY(load_extra_heads(m, ts, n));
   } else if (c.kind == SVL_MODEL_TTS) {
     // input_linear, z_proj: always dense (Linear::new, SVL/tts/flow_lm.rs:72-74)
     TRY(load_linear(m, ts, n, "input_linear.weight", d, c.latent_dim, 0, &m->input_linear));
@@ -478,6 +520,7 @@ int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_mode
 
 const LinearDev* find_linear(const svl_model* m, const char* name) {
   if (!strcmp(name, "text_linear")) return m->cfg.kind == SVL_MODEL_STT ? &m->text_linear : nullptr;
+  if (!strcmp(name, "extra_heads")) return m->cfg.kind == SVL_MODEL_STT && m->cfg.extra_heads_num > 0 ? &m->extra_heads : nullptr;
   if (!strcmp(name, "input_linear")) return m->cfg.kind == SVL_MODEL_TTS ? &m->input_linear : nullptr;
   if (!strcmp(name, "z_proj")) return m->cfg.z_dim > 0 ? &m->z_proj : nullptr;
   int layer = -1;
@@ -683,12 +726,29 @@ int build_programs(const svl_model* m, svl_state* s) {
     t.g.y = s->logits;
     t.g.y_stride = c.text_card;
     add_gemv(s, P, t);
+    if (c.extra_heads_num > 0) {
+      // the extra heads' logits from the same normalized output (SVL/stt/model.rs:259-266)
+      Phase xh = gemv_phase(s, m->extra_heads);
+      xh.g.x = s->x;
+      xh.g.x_stride = d;
+      xh.g.norm = NORM_RMS;
+      xh.g.nw = m->out_norm_w;
+      xh.g.eps = 1e-8f;
+      xh.g.epi = EPI_STORE;
+      xh.g.y = s->xlogits;
+      xh.g.y_stride = c.extra_heads_num * c.extra_heads_dim;
+      add_gemv(s, P, xh);
+    }
     Phase am{};
     am.kind = PH_ARGMAX;
     am.am.logits = s->logits;
     am.am.B = s->B;
     am.am.V = c.text_card;
     am.am.fb_tok = s->fb_tok;
+    am.am.xlogits = s->xlogits;
+    am.am.nh = c.extra_heads_num;
+    am.am.hd = c.extra_heads_dim;
+    am.am.xprob = s->xprob;
     am.units = s->B;
     P.push_back(am);
     TRY(upload_program(s, s->stt));
@@ -884,6 +944,10 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
   if (!rc && c.kind == SVL_MODEL_STT)
     rc = s->alloc(&p, (size_t)batch * c.n_q * c.d_model * (m->tables_bf16 ? 2 : 4)), s->stage = p;
+  if (!rc && c.kind == SVL_MODEL_STT && c.extra_heads_num > 0) {
+    rc = s->alloc(&p, (size_t)batch * c.extra_heads_num * c.extra_heads_dim * 4), s->xlogits = (float*)p;
+    if (!rc) rc = s->alloc(&p, (size_t)batch * c.extra_heads_num * 4), s->xprob = (float*)p;
+  }
   if (!rc && batch >= kBatchMfma) {
     const int wmax = std::max(std::max(c.d_model, c.num_heads * c.head_dim), c.ff_hidden);
     rc = s->alloc(&p, (size_t)batch * wmax), s->xqb = (int8_t*)p;
@@ -903,8 +967,11 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   return 0;
 }
 
-StepParams stt_params(const svl_state* s, const uint32_t* d_audio, const uint32_t* d_text, uint32_t* d_out) {
+StepParams stt_params(const svl_state* s, const uint32_t* d_audio, const uint32_t* d_text, uint32_t* d_out,
+                       float* d_prob = nullptr) {
   StepParams P{};
+  P.out_prob = d_prob;
+  P.prob_stride = (size_t)s->B * std::max(s->m->cfg.extra_heads_num, 0);
   P.audio = d_audio;
   P.audio_stride = (size_t)s->B * s->m->cfg.n_q;
   P.text = d_text;
@@ -1168,6 +1235,11 @@ int svl_transformer_forward(const svl_model* m, svl_state* s, const float* xs, i
 
 int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
                  uint32_t* out_tokens, float* out_logits) {
+  return svl_stt_step_heads(m, s, text_tokens, audio_tokens, out_tokens, out_logits, nullptr);
+}
+
+int svl_stt_step_heads(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
+                       uint32_t* out_tokens, float* out_logits, float* out_probs) {
   if (!m || !s || !text_tokens || !audio_tokens || !out_tokens) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
   const svl_config& c = m->cfg;
@@ -1195,12 +1267,20 @@ int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, 
   HIP_TRY(hipMemcpyAsync(out_tokens, s->tok_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
   if (out_logits)
     HIP_TRY(hipMemcpyAsync(out_logits, s->logits, (size_t)s->B * c.text_card * 4, hipMemcpyDeviceToHost, s->stream));
+  if (out_probs && c.extra_heads_num > 0)
+    HIP_TRY(hipMemcpyAsync(out_probs, s->xprob, (size_t)s->B * c.extra_heads_num * 4, hipMemcpyDeviceToHost,
+                           s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
   return check_abort(s);
 }
 
 int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
                             uint32_t* d_out_tokens) {
+  return svl_stt_recognize_heads_async(m, s, n_steps, d_audio_tokens, d_out_tokens, nullptr);
+}
+
+int svl_stt_recognize_heads_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+                                  uint32_t* d_out_tokens, float* d_out_probs) {
   if (!m || !s || (n_steps > 0 && (!d_audio_tokens || !d_out_tokens)))
     return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
@@ -1209,11 +1289,18 @@ int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, c
   if (n_steps == 0) return 0;
   TRY(check_room(s, n_steps));
   HIP_TRY(hipSetDevice(m->device));
-  return run_program(s, s->stt, stt_params(s, d_audio_tokens, nullptr, d_out_tokens), n_steps);
+  return run_program(s, s->stt,
+                     stt_params(s, d_audio_tokens, nullptr, d_out_tokens, m->cfg.extra_heads_num > 0 ? d_out_probs : nullptr),
+                     n_steps);
 }
 
 int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                       uint32_t* out_tokens) {
+  return svl_stt_recognize_heads(m, s, n_steps, audio_tokens, out_tokens, nullptr);
+}
+
+int svl_stt_recognize_heads(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                            uint32_t* out_tokens, float* out_probs) {
   if (!m || !s || (n_steps > 0 && (!audio_tokens || !out_tokens))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
   const svl_config& c = m->cfg;
@@ -1225,21 +1312,29 @@ int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const u
     if (audio_tokens[i] > (uint32_t)c.card) return set_error(SVL_ERR_INVALID_INPUT, "audio token %u out of range", audio_tokens[i]);
   TRY(check_room(s, n_steps));
   HIP_TRY(hipSetDevice(m->device));
+  const size_t np = out_probs ? (size_t)n_steps * s->B * std::max(c.extra_heads_num, 0) : 0;
   uint32_t *da, *dout;
+  float* dprob = nullptr;
   HIP_TRY(hipMalloc(&da, na * 4));
   hipError_t e = hipMalloc(&dout, (size_t)n_steps * s->B * 4);
+  if (e == hipSuccess && np) {
+    e = hipMalloc(&dprob, np * 4);
+    if (e != hipSuccess) hipFree(dout);
+  }
   if (e != hipSuccess) {
     hipFree(da);
     HIP_TRY(e);
   }
   int rc = 0;
   e = hipMemcpyAsync(da, audio_tokens, na * 4, hipMemcpyHostToDevice, s->stream);
-  if (e == hipSuccess) rc = run_program(s, s->stt, stt_params(s, da, nullptr, dout), n_steps);
+  if (e == hipSuccess) rc = run_program(s, s->stt, stt_params(s, da, nullptr, dout, dprob), n_steps);
   if (e == hipSuccess && rc == 0)
     e = hipMemcpyAsync(out_tokens, dout, (size_t)n_steps * s->B * 4, hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess && rc == 0 && np) e = hipMemcpyAsync(out_probs, dprob, np * 4, hipMemcpyDeviceToHost, s->stream);
   hipError_t e2 = hipStreamSynchronize(s->stream);
   hipFree(da);
   hipFree(dout);
+  if (dprob) hipFree(dprob);
   if (rc) return rc;
   HIP_TRY(e);
   HIP_TRY(e2);

@@ -39,7 +39,8 @@ EXPORTS = [
     "svl_model_linear_weight", "svl_state_create", "svl_state_duplicate", "svl_state_load_stream",
     "svl_state_layer_cache", "svl_state_positions", "svl_state_reset", "svl_state_destroy",
     "svl_state_synchronize", "svl_state_stream", "svl_transformer_forward", "svl_stt_step",
-    "svl_stt_recognize", "svl_stt_recognize_async", "svl_tts_backbone_step",
+    "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
+    "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
     "svl_bench_copy",
 ]
 
@@ -62,6 +63,7 @@ class Config(C.Structure):
         ("card", C.c_int32), ("n_q", C.c_int32), ("text_card", C.c_int32),
         ("latent_dim", C.c_int32), ("z_dim", C.c_int32),
         ("kv_dtype", C.c_int32),
+        ("extra_heads_num", C.c_int32), ("extra_heads_dim", C.c_int32),
     ]
 
 
@@ -104,6 +106,9 @@ def load_library(path: str = LIB_PATH):
     L.svl_transformer_forward.argtypes = [vp, vp, vp, i64, vp]
     L.svl_stt_step.argtypes = [vp, vp, vp, vp, vp, vp]
     L.svl_stt_recognize.argtypes = [vp, vp, i64, vp, vp]
+    L.svl_stt_step_heads.argtypes = [vp, vp, vp, vp, vp, vp, vp]
+    L.svl_stt_recognize_heads.argtypes = [vp, vp, i64, vp, vp, vp]
+    L.svl_stt_recognize_heads_async.argtypes = [vp, vp, i64, vp, vp, vp]
     L.svl_stt_recognize_async.argtypes = [vp, vp, i64, vp, vp]
     L.svl_tts_backbone_step.argtypes = [vp, vp, vp, vp]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
@@ -221,22 +226,34 @@ class Model:
         _check(load_library().svl_transformer_forward(self.h, state.h, _p(xs), xs.shape[1], _p(ys)))
         return ys
 
-    def step(self, text_tokens, audio_tokens, state: "State", want_logits: bool = False):
+    def step(self, text_tokens, audio_tokens, state: "State", want_logits: bool = False,
+             want_probs: bool = False):
+        """LanguageModel::step for every stream -> tokens [batch] (+ logits [batch, text_card])
+        (+ the extra heads' first-class probabilities [batch, extra_heads_num])."""
         t = np.ascontiguousarray(np.atleast_1d(text_tokens), dtype=np.uint32)
         a = np.ascontiguousarray(audio_tokens, dtype=np.uint32)
         out = np.empty(state.batch, dtype=np.uint32)
         logits = np.empty((state.batch, self.cfg["text_card"]), dtype=np.float32) if want_logits else None
-        _check(load_library().svl_stt_step(self.h, state.h, _p(t), _p(a), _p(out),
-                                           None if logits is None else _p(logits)))
-        return (out, logits) if want_logits else out
+        probs = (np.empty((state.batch, self.cfg.get("extra_heads_num", 0)), dtype=np.float32)
+                 if want_probs else None)
+        _check(load_library().svl_stt_step_heads(self.h, state.h, _p(t), _p(a), _p(out),
+                                                 None if logits is None else _p(logits),
+                                                 None if probs is None else _p(probs)))
+        res = (out,) + ((logits,) if want_logits else ()) + ((probs,) if want_probs else ())
+        return res if len(res) > 1 else out
 
-    def recognize(self, audio_tokens, state: "State") -> np.ndarray:
-        """audio_tokens [n_steps, batch, n_q] -> tokens [n_steps, batch]."""
+    def recognize(self, audio_tokens, state: "State", want_probs: bool = False):
+        """audio_tokens [n_steps, batch, n_q] -> tokens [n_steps, batch] (+ the extra heads'
+        probabilities [n_steps, batch, extra_heads_num])."""
         a = np.ascontiguousarray(audio_tokens, dtype=np.uint32)
         n = a.shape[0]
         out = np.empty((n, state.batch), dtype=np.uint32)
-        _check(load_library().svl_stt_recognize(self.h, state.h, n, _p(a), _p(out)))
-        return out
+        if not want_probs:
+            _check(load_library().svl_stt_recognize(self.h, state.h, n, _p(a), _p(out)))
+            return out
+        probs = np.empty((n, state.batch, self.cfg.get("extra_heads_num", 0)), dtype=np.float32)
+        _check(load_library().svl_stt_recognize_heads(self.h, state.h, n, _p(a), _p(out), _p(probs)))
+        return out, probs
 
     def recognize_async(self, n_steps: int, d_audio: int, d_out: int, state: "State") -> None:
         """Device-pointer variant: enqueues on the state's stream and returns."""

@@ -49,6 +49,8 @@ class Shape:
     text_card: int = 0
     latent_dim: int = 0
     z_dim: int = 0
+    extra_heads_num: int = 0   # STT VAD heads (SVL/stt/model.rs:217-222)
+    extra_heads_dim: int = 0
 
     def config(self, quantize: int = 0) -> dict:
         return dict(kind=self.kind, d_model=self.d_model, num_layers=self.num_layers,
@@ -58,7 +60,8 @@ class Shape:
                     layer_scale=self.layer_scale, context=self.context,
                     max_period=self.max_period, quantize=quantize, card=self.card,
                     n_q=self.n_q, text_card=self.text_card, latent_dim=self.latent_dim,
-                    z_dim=self.z_dim)
+                    z_dim=self.z_dim, extra_heads_num=self.extra_heads_num,
+                    extra_heads_dim=self.extra_heads_dim)
 
 
 def stt_shape(name, dim, layers, heads, hidden_scale, context, card=2048, n_q=32, text_card=8000):
@@ -143,6 +146,9 @@ def tensor_names(s: Shape):
         out += [(f"emb.{i}.weight", (s.card + 1, d), "emb") for i in range(s.n_q)]
         out.append(("out_norm.alpha", (1, 1, d), "norm_w"))
         out.append(("text_linear.weight", (s.text_card, d), "linear"))
+        # dense, never quantized (Linear::load(.., false), SVL/stt/model.rs:219)
+        out += [(f"extra_heads.{i}.weight", (s.extra_heads_dim, d), "dense_linear")
+                for i in range(s.extra_heads_num)]
     elif s.kind == MODEL_TTS:
         out.append(("input_linear.weight", (d, s.latent_dim), "dense_linear"))
         out += [("out_norm.weight", (d,), "norm_w"), ("out_norm.bias", (d,), "norm_b")]

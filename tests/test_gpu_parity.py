@@ -196,6 +196,56 @@ def test_stt_small_steps_match_oracle(dtype):
     print(f"{dtype}: max |logit diff| over 64 steps = {worst:.3g}")
 
 
+def _with_heads(shape, nh=4, hd=6):
+    """The shape with extra (VAD) heads, 4 x 6 as in the reference's STT configs."""
+    return W.Shape(**{**shape.__dict__, "extra_heads_num": nh, "extra_heads_dim": hd})
+
+
+PROB_TOL = 1e-6  # the GPU's expf and the C library's differ by a few ulp at most
+
+
+@pytest.mark.parametrize("dtype", ["q8_0", "bf16", "f32"])
+def test_stt_extra_heads_match_oracle(dtype):
+    """Extra heads (SVL/stt/model.rs:259-271): per step the first-class probabilities within
+    PROB_TOL of the oracle's, logits bit-exact and tokens equal (the heads change neither); the
+    recognize loop returns every step's probabilities."""
+    s = _with_heads(W.S1_SMALL)
+    _, g, o = build(s, dtype, seed=41)
+    gs, os_ = g.init_state(), o.new_state()
+    audio = W.audio_tokens(s, 40, seed=42)[0]
+    text = s.text_card
+    worst = 0.0
+    for i in range(40):
+        tg, lg, pg = g.step([text], audio[i][None], gs, want_logits=True, want_probs=True)
+        to, lo, po = os_.stt_step(text, audio[i], want_logits=True, want_probs=True)
+        assert tg[0] == to, f"step {i}"
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), f"step {i}"
+        worst = max(worst, float(np.max(np.abs(pg[0] - po))))
+        assert worst < PROB_TOL, f"step {i}: {pg[0]} vs {po}"
+        text = int(tg[0])
+    toks, probs = g.recognize(audio[:, None, :], g.init_state(), want_probs=True)
+    otoks, oprobs = o.new_state().stt_greedy(audio, want_probs=True)
+    assert np.array_equal(toks[:, 0], otoks)
+    assert float(np.max(np.abs(probs[:, 0] - oprobs))) < PROB_TOL
+    print(f"{dtype}: max |probability diff| = {worst:.3g}")
+
+
+@pytest.mark.parametrize("B", [3, 17])
+def test_stt_extra_heads_batch_matches_oracle(B):
+    """Lockstep batches (GEMV path at 3 streams, MFMA GEMMs at 17): each stream's tokens equal the
+    oracle's independent greedy run and its probabilities are within PROB_TOL."""
+    s = _with_heads(W.S1_SMALL)
+    _, g, o = build(s, "q8_0", seed=43)
+    n = 24
+    audio = W.audio_tokens(s, n, seed=44, batch=B)
+    toks, probs = g.recognize(np.ascontiguousarray(audio.transpose(1, 0, 2)), g.init_state(batch=B),
+                              want_probs=True)
+    for b in range(B):
+        ot, op = o.new_state().stt_greedy(audio[b], want_probs=True)
+        assert np.array_equal(toks[:, b], ot), f"stream {b}"
+        assert float(np.max(np.abs(probs[:, b] - op))) < PROB_TOL, f"stream {b}"
+
+
 def test_stt_small_recognize_matches_oracle_greedy():
     s = W.S1_SMALL
     _, g, o = build(s, "q8_0", seed=5)

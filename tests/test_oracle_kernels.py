@@ -163,3 +163,22 @@ def test_argmax_first_index_on_ties():
     x = np.array([0.5, 2.0, -1.0, 2.0, 2.0], dtype=np.float32)
     assert oracle.argmax(x) == 1
     assert oracle.argmax(np.full(7, -3.0, np.float32)) == 0
+
+
+def test_softmax_first_against_float64():
+    """softmax_last_dim's element 0 (SVL/stt/model.rs:267-269) against the float64 definition,
+    including the reductions' special cases: equal logits give 1/n, one dominant logit gives ~1
+    or ~0, a single class gives exactly 1, and shifting every logit leaves the result unchanged
+    to rounding (the maximum is subtracted first)."""
+    rng = np.random.default_rng(11)
+    for n in (1, 2, 6, 7, 33):
+        for scale in (0.1, 3.0, 40.0):
+            x = (rng.standard_normal(n) * scale).astype(np.float32)
+            x64 = x.astype(np.float64)
+            e = np.exp(x64 - x64.max())
+            assert abs(oracle.softmax_first(x) - e[0] / e.sum()) <= 4e-7 * max(1.0, e[0] / e.sum()), (n, scale)
+            assert abs(oracle.softmax_first(x + np.float32(1000.0)) - oracle.softmax_first(x)) < 1e-4
+    assert oracle.softmax_first(np.zeros(6, np.float32)) == np.float32(1.0) / np.float32(6.0)
+    assert oracle.softmax_first(np.array([5.0], np.float32)) == 1.0
+    assert oracle.softmax_first(np.array([100.0, 0.0, 0.0], np.float32)) == 1.0
+    assert oracle.softmax_first(np.array([0.0, 100.0], np.float32)) < 1e-40

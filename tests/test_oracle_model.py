@@ -184,6 +184,42 @@ def test_stt_step_brute_force():
         text = tok
 
 
+def test_stt_extra_heads_brute_force():
+    """LanguageModel::step's extra heads (SVL/stt/model.rs:217-222, 259-271): per head, the dense
+    [dim, d] linear over the out_norm'ed output, softmax, probability of class 0 -- against float64.
+    The heads leave the text tokens and logits unchanged."""
+    base = W.stt_shape("stt-tiny", 64, 2, 2, 4.125, 6, card=10, n_q=3, text_card=20)
+    s = W.Shape(**{**base.__dict__, "extra_heads_num": 4, "extra_heads_dim": 6})
+    tensors = W.make_weights(s, "f32", seed=13)
+    assert tensors["extra_heads.3.weight"][1] == (6, 64)
+    m = oracle.Model(s.config(0), tensors)
+    plain = oracle.Model(base.config(0), {k: v for k, v in tensors.items() if not k.startswith("extra_heads")})
+    st, sp = m.new_state(), plain.new_state()
+    audio = W.audio_tokens(s, 8, seed=2)[0]
+    get = lambda n: tensors[n][2].astype(np.float64).reshape(tensors[n][1])
+    xs, text = [], s.text_card
+    for i in range(8):
+        tok, logits, probs = st.stt_step(text, audio[i], want_logits=True, want_probs=True)
+        tok_p, logits_p = sp.stt_step(text, audio[i], want_logits=True)
+        assert tok == tok_p and np.array_equal(logits, logits_p)
+        xs.append(get("text_emb.weight")[text] + sum(get(f"emb.{c}.weight")[audio[i][c]] for c in range(s.n_q)))
+        y = np_transformer(s, tensors, np.array(xs))[-1]
+        y = y / np.sqrt((y ** 2).mean() + 1e-8) * get("out_norm.alpha").reshape(-1)
+        for h in range(4):
+            lg = get(f"extra_heads.{h}.weight") @ y
+            e = np.exp(lg - lg.max())
+            assert abs(probs[h] - e[0] / e.sum()) < 1e-5, (i, h)
+        text = tok
+    # the greedy loop returns every step's probabilities, equal to the single steps'
+    toks, pr = m.new_state().stt_greedy(audio, want_probs=True)
+    st2, text = m.new_state(), s.text_card
+    for i in range(8):
+        a = np.full(s.n_q, s.card, np.uint32) if i == 0 else audio[i]
+        t, p1 = st2.stt_step(text, a, want_probs=True)
+        assert t == toks[i] and np.array_equal(p1, pr[i])
+        text = t
+
+
 def test_stt_greedy_initial_tokens_and_feedback():
     """Recognizer::step: step 0 sees `card` audio tokens and text_card; then the previous argmax."""
     s = W.S1_SMALL
