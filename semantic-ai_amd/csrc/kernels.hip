@@ -184,6 +184,44 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, Ste
   run_unit<F, KM, V>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
 }
 
+// A Q8_0 GEMV phase launched with the fields its first loads depend on as leading scalar
+// arguments, which the hardware preloads into SGPRs (-amdgpu-kernarg-preload-count): the input
+// row and the weight requests go out at wave start instead of after a scalar load of the
+// argument segment.  `hx` input rows, `hw` / `hsc` quants and block scales, `hnw` norm weights,
+// `hepn` = epilogue | norm kind << 8 | blocks per weight thread << 16, `hxs` input row stride.
+template <int V>
+__global__ __launch_bounds__(kStepThreads) void q8_phase_kernel(const float* hx, const void* hw, const void* hsc,
+                                                                const float* hnw, int hin, int hipw, int hparts,
+                                                                int hitems, int hepn, int hxs, const Phase ph,
+                                                                StepParams P, int step) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ WgSync ws;
+  init_wg_sync(&ws);
+  const int epi = hepn & 0xff;
+  if (threadIdx.x >= kRowThreads) {
+    if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
+    WItem it;
+    w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, hepn >> 16, epi, blockIdx.x, it);
+    if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+    w_terms(it, smem);
+    lds_signal(&ws.t_parts);
+    return;
+  }
+  RowSync rs{&ws, 0u};
+  GemvArgs a = ph.g;
+  a.x = hx;
+  a.x_stride = hxs;
+  a.L.in = hin;
+  a.ipw = hipw;
+  a.parts = hparts;
+  a.epi = epi;
+  a.norm = (hepn >> 8) & 0xff;
+  a.nw = hnw;
+  if (epi == EPI_SILU_GATE) a.ff_hidden = hitems;
+  else a.L.out = hitems;
+  gemv_q8_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
+}
+
 unsigned program_families(const Phase* phases, int n) {
   unsigned f = 0;
   for (int i = 0; i < n; ++i) {
@@ -229,6 +267,22 @@ void (*attn_kernel_at(int v))(const Phase, StepParams, int) {
 hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s) {
   if (ph.units <= 0) return hipSuccess;
   void (*k)(const Phase, StepParams, int);
+  if (ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
+    const GemvArgs& g = ph.g;
+    void (*kq)(const float*, const void*, const void*, const float*, int, int, int, int, int, int, const Phase,
+               StepParams, int);
+    switch (row_slots(g.L.in)) {
+      case 2: kq = q8_phase_kernel<2>; break;
+      case 4: kq = q8_phase_kernel<4>; break;
+      case 8: kq = q8_phase_kernel<8>; break;
+      default: kq = q8_phase_kernel<kMaxSlots>; break;
+    }
+    const int items = g.epi == EPI_SILU_GATE ? g.ff_hidden : g.L.out;
+    const int epn = g.epi | (g.norm << 8) | (g.maxb << 16);
+    hipLaunchKernelGGL(kq, dim3(ph.units), dim3(kStepThreads), smem, s, g.x, (const void*)g.L.w, (const void*)g.L.scale,
+                       g.nw, g.L.in, g.ipw, g.parts, items, epn, g.x_stride, ph, p, step);
+    return hipGetLastError();
+  }
   switch (ph.kind) {
     case PH_GEMV:
       if (ph.g.L.fmt == FMT_Q8_0) k = slots_kernel<FAM_Q8, 0u>(row_slots(ph.g.L.in));

@@ -680,16 +680,14 @@ struct WItem {
 
 // Requests this weight-wave thread's blocks of unit `unit` of GEMV phase `ph` (descriptor read
 // with scalar loads).  Block k of thread w is index w + 512 k = r * nb + blk of the unit.
-__device__ __forceinline__ void w_issue(const Phase* ph, int unit, WItem& it) {
-  const int K = ld_const(&ph->g.L.in);
-  const int epi = ld_const(&ph->g.epi);
-  const int ff_hidden = ld_const(&ph->g.ff_hidden);
-  const int items = epi == EPI_SILU_GATE ? ff_hidden : ld_const(&ph->g.L.out);
-  it.ipw = ld_const(&ph->g.ipw);
-  it.maxb = ld_const(&ph->g.maxb);
-  it.g = q8_geom(K, items, it.ipw, ld_const(&ph->g.parts), epi == EPI_SILU_GATE, unit);
-  const int8_t* wq = (const int8_t*)ld_const(&ph->g.L.w);
-  const uint16_t* sc = (const uint16_t*)ld_const(&ph->g.L.scale);
+// The geometry the requests need: K, items (output rows, or gate/value pairs: then also the offset
+// of the value rows), rows per unit, units per batch row, blocks per thread, the epilogue kind.
+__device__ __forceinline__ void w_issue_at(const int8_t* wq, const uint16_t* sc, int K, int items, int ipw, int parts,
+                                           int maxb, int epi, int unit, WItem& it) {
+  const int ff_hidden = items;  // read by gemv_phys_row for the SiLU gate only, where items = ff_hidden
+  it.ipw = ipw;
+  it.maxb = maxb;
+  it.g = q8_geom(K, items, ipw, parts, epi == EPI_SILU_GATE, unit);
   const int nb = it.g.nb;
   const int w = threadIdx.x - kRowThreads;
   int r = w / nb, blk = w - r * nb;
@@ -711,6 +709,13 @@ __device__ __forceinline__ void w_issue(const Phase* ph, int unit, WItem& it) {
       ++r;
     }
   }
+}
+
+__device__ __forceinline__ void w_issue(const Phase* ph, int unit, WItem& it) {
+  const int epi = ld_const(&ph->g.epi);
+  const int items = epi == EPI_SILU_GATE ? ld_const(&ph->g.ff_hidden) : ld_const(&ph->g.L.out);
+  w_issue_at((const int8_t*)ld_const(&ph->g.L.w), (const uint16_t*)ld_const(&ph->g.L.scale), ld_const(&ph->g.L.in),
+             items, ld_const(&ph->g.ipw), ld_const(&ph->g.parts), ld_const(&ph->g.maxb), epi, unit, it);
 }
 
 // The item's block terms T[r][blk] = ((f32)(sum qw * qx) * d_w) * d_x into LDS.
