@@ -184,26 +184,40 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, Ste
   run_unit<F, KM, V>(phase_at(d_ph, 0), P, step, blockIdx.x, P.pos, smem, rs, item);
 }
 
-// A Q8_0 GEMV phase launched with the fields its first loads depend on as leading scalar
-// arguments, which the hardware preloads into SGPRs (-amdgpu-kernarg-preload-count): the input
-// row and the weight requests go out at wave start instead of after a scalar load of the
-// argument segment.  `hx` input rows, `hw` / `hsc` quants and block scales, `hnw` norm weights,
-// `hepn` = epilogue | norm kind << 8 | blocks per weight thread << 16, `hxs` input row stride.
-template <int V>
-__global__ __launch_bounds__(kStepThreads) void q8_phase_kernel(const float* hx, const void* hw, const void* hsc,
-                                                                const float* hnw, int hin, int hipw, int hparts,
-                                                                int hitems, int hepn, int hxs, const Phase ph,
-                                                                StepParams P, int step) {
+// A GEMV phase whose weight waves stream the weights (Q8_0, Q4K, chain-packed dense) launched
+// with the fields its first loads depend on as leading scalar arguments, which the hardware
+// preloads into SGPRs (-amdgpu-kernarg-preload-count): the input row and the weight requests go
+// out at wave start instead of after a scalar load of the argument segment.  `hx` input rows,
+// `hw` / `hsc` weights and Q8_0 block scales, `hnw` norm weights, `hepn` = epilogue | norm kind
+// << 8 | blocks per weight thread << 16 | bf16 dense weights << 24, `hxs` input row stride.
+template <unsigned F, int V>
+__global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* hx, const void* hw, const void* hsc,
+                                                                  const float* hnw, int hin, int hipw, int hparts,
+                                                                  int hitems, int hepn, int hxs, const Phase ph,
+                                                                  StepParams P, int step) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ WgSync ws;
   init_wg_sync(&ws);
-  const int epi = hepn & 0xff;
+  const int epi = hepn & 0xff, maxb = (hepn >> 16) & 0xff;
   if (threadIdx.x >= kRowThreads) {
     if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
-    WItem it;
-    w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, hepn >> 16, epi, blockIdx.x, it);
-    if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
-    w_terms(it, smem);
+    if constexpr (F == FAM_Q8) {
+      WItem it;
+      w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, maxb, epi, blockIdx.x, it);
+      if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+      w_terms(it, smem);
+    } else if constexpr (F == FAM_Q4K) {
+      WItemQ4 it;
+      w_issue_q4k_at((const unsigned char*)hw, hin, hitems, hipw, hparts, maxb, epi, blockIdx.x, it);
+      if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
+      w_terms_q4k(it, smem);
+    } else {
+      const bool ok = (hepn >> 24) ? w_dense_at<true>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi,
+                                                      blockIdx.x, &ws, smem, 0)
+                                   : w_dense_at<false>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi,
+                                                       blockIdx.x, &ws, smem, 0);
+      if (!ok) return;
+    }
     lds_signal(&ws.t_parts);
     return;
   }
@@ -219,7 +233,9 @@ __global__ __launch_bounds__(kStepThreads) void q8_phase_kernel(const float* hx,
   a.nw = hnw;
   if (epi == EPI_SILU_GATE) a.ff_hidden = hitems;
   else a.L.out = hitems;
-  gemv_q8_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
+  if constexpr (F == FAM_Q8) gemv_q8_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
+  else if constexpr (F == FAM_Q4K) gemv_q4k_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
+  else gemv_dense_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
 }
 
 unsigned program_families(const Phase* phases, int n) {
@@ -242,6 +258,18 @@ hipError_t launch_step_program(const StepParams& p, unsigned families, int grid,
   else if ((families & ~(unsigned)FAM_DENSE) == 0) k = (const void*)step_program_kernel<FAM_DENSE>;
   else k = (const void*)step_program_kernel<FAM_ALL>;
   return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kStepThreads), kargs, (unsigned)smem, s);
+}
+
+// The preloaded-argument GEMV kernel of a family for inputs of `slots` row slots.
+template <unsigned F>
+void (*gemv_slots_kernel(int slots))(const float*, const void*, const void*, const float*, int, int, int, int, int, int,
+                                     const Phase, StepParams, int) {
+  switch (slots) {
+    case 2: return gemv_phase_kernel<F, 2>;
+    case 4: return gemv_phase_kernel<F, 4>;
+    case 8: return gemv_phase_kernel<F, 8>;
+    default: return gemv_phase_kernel<F, kMaxSlots>;
+  }
 }
 
 // The kernel of a GEMV family for inputs of `slots` row slots (2, 4, 8 or 16).
@@ -267,18 +295,16 @@ void (*attn_kernel_at(int v))(const Phase, StepParams, int) {
 hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s) {
   if (ph.units <= 0) return hipSuccess;
   void (*k)(const Phase, StepParams, int);
-  if (ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
+  if (ph.kind == PH_GEMV && (ph.g.L.fmt == FMT_Q8_0 || ph.g.L.fmt == FMT_Q4K || ph.g.L.fmt == FMT_F32C ||
+                             ph.g.L.fmt == FMT_BF16C)) {
     const GemvArgs& g = ph.g;
     void (*kq)(const float*, const void*, const void*, const float*, int, int, int, int, int, int, const Phase,
                StepParams, int);
-    switch (row_slots(g.L.in)) {
-      case 2: kq = q8_phase_kernel<2>; break;
-      case 4: kq = q8_phase_kernel<4>; break;
-      case 8: kq = q8_phase_kernel<8>; break;
-      default: kq = q8_phase_kernel<kMaxSlots>; break;
-    }
+    if (g.L.fmt == FMT_Q8_0) kq = gemv_slots_kernel<FAM_Q8>(row_slots(g.L.in));
+    else if (g.L.fmt == FMT_Q4K) kq = gemv_slots_kernel<FAM_Q4K>(row_slots(g.L.in));
+    else kq = gemv_slots_kernel<FAM_DENSE>(row_slots(g.L.in));
     const int items = g.epi == EPI_SILU_GATE ? g.ff_hidden : g.L.out;
-    const int epn = g.epi | (g.norm << 8) | (g.maxb << 16);
+    const int epn = g.epi | (g.norm << 8) | (g.maxb << 16) | ((g.L.fmt == FMT_BF16C ? 1 : 0) << 24);
     hipLaunchKernelGGL(kq, dim3(ph.units), dim3(kStepThreads), smem, s, g.x, (const void*)g.L.w, (const void*)g.L.scale,
                        g.nw, g.L.in, g.ipw, g.parts, items, epn, g.x_stride, ph, p, step);
     return hipGetLastError();

@@ -921,15 +921,12 @@ struct WItemQ4 {
   v4i q[kQ4Blocks][8];
 };
 
-__device__ __forceinline__ void w_issue_q4k(const Phase* ph, int unit, WItemQ4& it) {
-  const int K = ld_const(&ph->g.L.in);
-  const int epi = ld_const(&ph->g.epi);
-  const int ff_hidden = ld_const(&ph->g.ff_hidden);
-  const int items = epi == EPI_SILU_GATE ? ff_hidden : ld_const(&ph->g.L.out);
-  it.ipw = ld_const(&ph->g.ipw);
-  it.maxb = ld_const(&ph->g.maxb);
-  it.g = q4_geom(K, items, it.ipw, ld_const(&ph->g.parts), epi == EPI_SILU_GATE, unit);
-  const unsigned char* wb = (const unsigned char*)ld_const(&ph->g.L.w);
+__device__ __forceinline__ void w_issue_q4k_at(const unsigned char* wb, int K, int items, int ipw, int parts, int maxb,
+                                               int epi, int unit, WItemQ4& it) {
+  const int ff_hidden = items;  // read by gemv_phys_row for the SiLU gate only, where items = ff_hidden
+  it.ipw = ipw;
+  it.maxb = maxb;
+  it.g = q4_geom(K, items, ipw, parts, epi == EPI_SILU_GATE, unit);
   const int nb = it.g.nb;
   const int w = threadIdx.x - kRowThreads;
   int r = w / nb, blk = w - r * nb;
@@ -951,6 +948,13 @@ __device__ __forceinline__ void w_issue_q4k(const Phase* ph, int unit, WItemQ4& 
       ++r;
     }
   }
+}
+
+__device__ __forceinline__ void w_issue_q4k(const Phase* ph, int unit, WItemQ4& it) {
+  const int epi = ld_const(&ph->g.epi);
+  const int items = epi == EPI_SILU_GATE ? ld_const(&ph->g.ff_hidden) : ld_const(&ph->g.L.out);
+  w_issue_q4k_at((const unsigned char*)ld_const(&ph->g.L.w), ld_const(&ph->g.L.in), items, ld_const(&ph->g.ipw),
+                 ld_const(&ph->g.parts), ld_const(&ph->g.maxb), epi, unit, it);
 }
 
 __device__ __forceinline__ int q4k_lane(const v4i& a, const v4i& b, int l) {
@@ -1443,15 +1447,11 @@ __device__ __forceinline__ void gemv_dense_rows(const GemvArgs& a, int unit, con
 // the row waves have requested the input row, wait for the chain-major input, then stream the
 // chain (kDenseBatch loads in flight), sum the 16 lanes and write the row result.
 template <bool BF16W>
-__device__ __forceinline__ bool w_dense(const Phase* ph, int unit, WgSync* ws, unsigned char* smem, unsigned item) {
+__device__ __forceinline__ bool w_dense_at(const unsigned char* wbase, int K, int items, int ipw, int parts, int epi,
+                                           int unit, WgSync* ws, unsigned char* smem, unsigned item) {
   constexpr int EPL = BF16W ? 8 : 4;  // elements per 16-byte load
-  const int K = ld_const(&ph->g.L.in);
-  const int epi = ld_const(&ph->g.epi);
-  const int ff_hidden = ld_const(&ph->g.ff_hidden);
-  const int items = epi == EPI_SILU_GATE ? ff_hidden : ld_const(&ph->g.L.out);
-  const int ipw = ld_const(&ph->g.ipw);
-  const Q8Geom g = q8_geom(K, items, ipw, ld_const(&ph->g.parts), epi == EPI_SILU_GATE, unit);
-  const unsigned char* wbase = (const unsigned char*)ld_const(&ph->g.L.w);
+  const int ff_hidden = items;  // read by gemv_phys_row for the SiLU gate only, where items = ff_hidden
+  const Q8Geom g = q8_geom(K, items, ipw, parts, epi == EPI_SILU_GATE, unit);
   const DenseLds l = dense_lds(smem, K);
   const int stride = dense_chain_stride(K);
   const int NL = K / (16 * EPL);  // loads per chain
@@ -1504,6 +1504,14 @@ __device__ __forceinline__ bool w_dense(const Phase* ph, int unit, WgSync* ws, u
   }
   if (!ready && !lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return false;
   return true;
+}
+
+template <bool BF16W>
+__device__ __forceinline__ bool w_dense(const Phase* ph, int unit, WgSync* ws, unsigned char* smem, unsigned item) {
+  const int epi = ld_const(&ph->g.epi);
+  const int items = epi == EPI_SILU_GATE ? ld_const(&ph->g.ff_hidden) : ld_const(&ph->g.L.out);
+  return w_dense_at<BF16W>((const unsigned char*)ld_const(&ph->g.L.w), ld_const(&ph->g.L.in), items,
+                           ld_const(&ph->g.ipw), ld_const(&ph->g.parts), epi, unit, ws, smem, item);
 }
 
 __device__ __forceinline__ bool is_chained_dense(int fmt) { return fmt == FMT_F32C || fmt == FMT_BF16C; }
