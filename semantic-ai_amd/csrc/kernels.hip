@@ -238,6 +238,46 @@ __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* h
   else gemv_dense_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
 }
 
+// An attention phase launched like gemv_phase_kernel: the query, K / V ring, position and order
+// pointers, ring slots, window, batch and head units as preloaded scalar arguments.  Units past
+// `hheads` gather the next step's audio embedding rows (the first attention phase of an STT step).
+template <int AV>
+__global__ __launch_bounds__(kStepThreads) void attn_phase_kernel(const float* hq, const void* hkc, const void* hvc,
+                                                                  const int* hpos, const int* horder, int hcap,
+                                                                  int hwindow, int hB, int hheads, const Phase ph,
+                                                                  StepParams P, int step) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ WgSync ws;
+  init_wg_sync(&ws);
+  if (threadIdx.x >= kRowThreads) return;
+  RowSync rs{&ws, 0u};
+  const int unit = blockIdx.x;
+  if (unit < hheads) {
+    AttnArgs a = ph.at;
+    a.q = hq;
+    a.kc = hkc;
+    a.vc = hvc;
+    a.pos = (int*)hpos;
+    a.order = horder;
+    a.cap = hcap;
+    a.window = hwindow;
+    a.B = hB;
+    attn_dispatch<AV>(a, unit, hpos, smem, rs);
+  } else if (step + 1 < P.n_steps && !P.text) {
+    gather_unit(ph.e, P.audio + (size_t)(step + 1) * P.audio_stride, unit - hheads);
+  }
+}
+
+template <int AV>
+void (*attn_phase_kernel_at(int v))(const float*, const void*, const void*, const int*, const int*, int, int, int, int,
+                                    const Phase, StepParams, int) {
+  if constexpr (AV > 8) {
+    return nullptr;
+  } else {
+    return v == AV ? attn_phase_kernel<AV> : attn_phase_kernel_at<AV + 1>(v);
+  }
+}
+
 unsigned program_families(const Phase* phases, int n) {
   unsigned f = 0;
   for (int i = 0; i < n; ++i) {
@@ -307,6 +347,14 @@ hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t s
     const int epn = g.epi | (g.norm << 8) | (g.maxb << 16) | ((g.L.fmt == FMT_BF16C ? 1 : 0) << 24);
     hipLaunchKernelGGL(kq, dim3(ph.units), dim3(kStepThreads), smem, s, g.x, (const void*)g.L.w, (const void*)g.L.scale,
                        g.nw, g.L.in, g.ipw, g.parts, items, epn, g.x_stride, ph, p, step);
+    return hipGetLastError();
+  }
+  if (ph.kind == PH_ATTN) {
+    const AttnArgs& a = ph.at;
+    const int hd = a.hd == 128 ? 128 : 64;
+    auto ka = attn_phase_kernel_at<1>(attn_variant(hd, a.kv_bf16, a.hpu));
+    hipLaunchKernelGGL(ka, dim3(ph.units), dim3(kStepThreads), smem, s, a.q, a.kc, a.vc, (const int*)p.pos, a.order,
+                       a.cap, a.window, a.B, a.B * a.H / a.hpu, ph, p, step);
     return hipGetLastError();
   }
   switch (ph.kind) {

@@ -1645,7 +1645,8 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   const int wstride = ((cap + 7) & ~7) + 8;  // reads of w run up to 7 past the last key
   float* w = (float*)(smem + kAttnStages * kAttnChunkBytes);  // HPU x L weights (16-byte aligned)
   float* slot = w + HPU * wstride;  // [0, HPU): sums; [4, 4 + 32): score maxima of the 32 groups
-  const int h0 = (unit % (H / HPU)) * HPU, b = ldg(a.order + unit / (H / HPU));
+  // a single stream needs no order lookup (one dependent load less before the position)
+  const int h0 = (unit % (H / HPU)) * HPU, b = a.B == 1 ? 0 : ldg(a.order + unit / (H / HPU));
   // the query is requested with the position (the prologue needs only the position)
   const int li = threadIdx.x % 16, grp = threadIdx.x / 16;
   const int hs = grp % HPU;  // this thread's head for the scores
