@@ -19,7 +19,7 @@ Other workloads (one JSON line each, same fields):
 
 Prints ONE JSON line (rank 0).  `value` is decode steps/s; `roofline` prices the dominant
 kernel -- the step's phase kernels (phase_kernel; gemv_phase_kernel for the weight-streaming GEMVs;
-attn_phase_kernel for attention), launched once per phase of every step (83 launches per STT-1B step, 148
+attn_phase_kernel for attention; batch_phase_kernel for the batched MFMA path), launched once per phase of every step (83 launches per STT-1B step, 148
 at B=64) -- against MI355X HBM bandwidth: `achieved` = algorithmic bytes per launch / average
 launch time, i.e. the algorithmic bytes of the timed steps over their HIP-event time (which
 also counts the gaps between launches); `traffic` is the HBM bytes per launch measured by
@@ -193,7 +193,7 @@ def bench_stt(args, wl, steps, warmup):
     line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                         "traffic_counter_steps": traffic_steps,
-                        "kernel": "step phase kernels (phase_kernel, gemv_phase_kernel, attn_phase_kernel; one launch per phase of each step)",
+                        "kernel": "step phase kernels (phase_kernel, gemv_phase_kernel, attn_phase_kernel, batch_phase_kernel; one launch per phase of each step)",
                         "launches": launches,
                         "algorithmic_bytes_per_launch": int(bytes_launch / launches),
                         "avg_launch_us": round(gpu_ms * 1e3 / launches, 3), "timed_ms": round(gpu_ms, 4)}
@@ -266,7 +266,7 @@ def bench_tts(args, steps, warmup):
                      "synthetic (seeded N(0, 0.02) weights, N(0, 1) latents, seeded prefilled K/V)", config)
     line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                        "kernel": "step phase kernels (phase_kernel, gemv_phase_kernel, attn_phase_kernel; one launch per phase; one call = one step)",
+                        "kernel": "step phase kernels (phase_kernel, gemv_phase_kernel, attn_phase_kernel, batch_phase_kernel; one launch per phase; one call = one step)",
                         "algorithmic_bytes_per_step": int(bytes_total / steps)}
     if not args.no_cpu_baseline:
         import oracle

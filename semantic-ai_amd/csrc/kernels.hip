@@ -268,6 +268,46 @@ __global__ __launch_bounds__(kStepThreads) void attn_phase_kernel(const float* h
   }
 }
 
+// The batched Q8_0 phases (activation quantization, MFMA GEMM) launched the same way.  PH_QUANT:
+// `hp0` input rows, `hp1` norm weights, `hp2` / `hp3` quantized rows and their scales; PH_QGEMM:
+// `hp0` / `hp1` quantized rows and scales, `hp2` / `hp3` quants and block scales of the weights.
+// `hepn` = epilogue | norm kind << 8 | phase kind << 24.
+template <int V>
+__global__ __launch_bounds__(kStepThreads) void batch_phase_kernel(const void* hp0, const void* hp1, const void* hp2,
+                                                                   const void* hp3, int hin, int hipw, int hparts,
+                                                                   int hitems, int hepn, int hxs, const Phase ph,
+                                                                   StepParams P, int step) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ WgSync ws;
+  init_wg_sync(&ws);
+  if (threadIdx.x >= kRowThreads) return;
+  RowSync rs{&ws, 0u};
+  GemvArgs a = ph.g;
+  const int epi = hepn & 0xff;
+  a.L.in = hin;
+  a.ipw = hipw;
+  a.parts = hparts;
+  a.epi = epi;
+  if (epi == EPI_SILU_GATE) a.ff_hidden = hitems;
+  else a.L.out = hitems;
+  if ((hepn >> 24) == PH_QUANT) {
+    a.x = (const float*)hp0;
+    a.x_stride = hxs;
+    a.nw = (const float*)hp1;
+    a.norm = (hepn >> 8) & 0xff;
+    a.xq = (int8_t*)hp2;
+    a.xdq = (float*)hp3;
+    quant_unit<V>(a, blockIdx.x, smem, rs);
+  } else {
+    a.xq = (int8_t*)hp0;
+    a.xdq = (float*)hp1;
+    a.L.w = (void*)hp2;
+    a.L.scale = (uint16_t*)hp3;
+    if ((epi == EPI_SILU_GATE ? 2 * hipw : hipw) == kTileRows) qgemm_unit<kTileRows>(a, blockIdx.x, P.pos, smem, rs);
+    else qgemm_unit<kTileRows / 2>(a, blockIdx.x, P.pos, smem, rs);
+  }
+}
+
 template <int AV>
 void (*attn_phase_kernel_at(int v))(const float*, const void*, const void*, const int*, const int*, int, int, int, int,
                                     const Phase, StepParams, int) {
@@ -347,6 +387,25 @@ hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t s
     const int epn = g.epi | (g.norm << 8) | (g.maxb << 16) | ((g.L.fmt == FMT_BF16C ? 1 : 0) << 24);
     hipLaunchKernelGGL(kq, dim3(ph.units), dim3(kStepThreads), smem, s, g.x, (const void*)g.L.w, (const void*)g.L.scale,
                        g.nw, g.L.in, g.ipw, g.parts, items, epn, g.x_stride, ph, p, step);
+    return hipGetLastError();
+  }
+  if (ph.kind == PH_QUANT || ph.kind == PH_QGEMM) {
+    const GemvArgs& g = ph.g;
+    void (*kb)(const void*, const void*, const void*, const void*, int, int, int, int, int, int, const Phase,
+               StepParams, int);
+    switch (row_slots(g.L.in)) {
+      case 2: kb = batch_phase_kernel<2>; break;
+      case 4: kb = batch_phase_kernel<4>; break;
+      case 8: kb = batch_phase_kernel<8>; break;
+      default: kb = batch_phase_kernel<kMaxSlots>; break;
+    }
+    const bool quant = ph.kind == PH_QUANT;
+    const int items = g.epi == EPI_SILU_GATE ? g.ff_hidden : g.L.out;
+    const int epn = g.epi | (g.norm << 8) | (ph.kind << 24);
+    hipLaunchKernelGGL(kb, dim3(ph.units), dim3(kStepThreads), smem, s, quant ? (const void*)g.x : (const void*)g.xq,
+                       quant ? (const void*)g.nw : (const void*)g.xdq, quant ? (const void*)g.xq : (const void*)g.L.w,
+                       quant ? (const void*)g.xdq : (const void*)g.L.scale, g.L.in, g.ipw, g.parts, items, epn,
+                       g.x_stride, ph, p, step);
     return hipGetLastError();
   }
   if (ph.kind == PH_ATTN) {
