@@ -86,6 +86,8 @@ def lib():
             L.svlo_vec_dot_q4k_q8k.restype = C.c_float
             L.svlo_set_fma.argtypes = [C.c_int]
             L.svlo_set_threads.argtypes = [C.c_int]
+            L.svlo_set_norm_order.argtypes = [C.c_int]
+            L.svlo_get_norm_order.restype = C.c_int
             L.svlo_get_threads.restype = C.c_int
             L.svlo_get_fma.restype = C.c_int
             L.svlo_dot.argtypes = [vp, vp, sz]
@@ -150,6 +152,19 @@ def set_threads(n: int) -> None:
 
 def get_threads() -> int:
     return lib().svlo_get_threads()
+
+
+NORM_ORDERS = {"element": 0, "blocked": 1}
+
+
+def set_norm_order(order: str) -> None:
+    """Summation order of the RMSNorm / LayerNorm statistics: "element" (candle's CPU ops, the
+    default) or "blocked" (the order of the GPU kernels)."""
+    lib().svlo_set_norm_order(NORM_ORDERS[order])
+
+
+def get_norm_order() -> str:
+    return {v: k for k, v in NORM_ORDERS.items()}[lib().svlo_get_norm_order()]
 
 
 # ---- formats --------------------------------------------------------------------------------

@@ -184,12 +184,33 @@ int svlo_attention(const float* q, const float* k, const float* v, float* out, s
                                   position, first_key, context);
 }
 
-/* Sum of f(x_i) over a row in the order shared with the GPU kernels: 64 strided partials
- * (partial l sums x[l], x[l+64], ... sequentially), then a butterfly over the partials
- * (p[l] + p[l ^ o] for o = 32, 16, 8, 4, 2, 1; every lane ends with the same value, lane 0's
- * is returned).  candle's CPU reductions (Iterator::sum) are not available here to pin
- * their order; this is the one order both sides of the parity check use. */
-static float blocked_sum(const float* x, size_t n, int squares) {
+/* Order of the norm statistics' sums (svlo_set_norm_order).
+ *
+ * SVLO_NORM_ORDER_ELEMENT (default) is candle-nn's CPU RmsNorm / LayerNorm: one f32
+ * accumulator per row, x_0, x_1, ... added in index order (`Iterator::sum::<f32>` and a plain
+ * `for v in src` loop; Rust never reassociates float adds).  [candle hypothesis]
+ *
+ * SVLO_NORM_ORDER_BLOCKED is the order of the GPU kernels: 64 strided partials (partial l sums
+ * x[l], x[l+64], ... sequentially), then a butterfly over the partials (p[l] + p[l ^ o] for
+ * o = 32, 16, 8, 4, 2, 1; every lane ends with the same value, lane 0's is returned).  The two
+ * orders differ by rounding only; tests/ measure what that does to logits and greedy tokens. */
+static int g_norm_order = SVLO_NORM_ORDER_ELEMENT;
+
+void svlo_set_norm_order(int order) {
+    g_norm_order = order == SVLO_NORM_ORDER_BLOCKED ? SVLO_NORM_ORDER_BLOCKED : SVLO_NORM_ORDER_ELEMENT;
+}
+int svlo_get_norm_order(void) { return g_norm_order; }
+
+static float row_sum(const float* x, size_t n, int squares) {
+    if (g_norm_order == SVLO_NORM_ORDER_ELEMENT) {
+        float acc = 0.0f;
+        for (size_t i = 0; i < n; ++i) {
+            float v = x[i];
+            if (squares) v = v * v;
+            acc += v;
+        }
+        return acc;
+    }
     float p[64];
     for (int l = 0; l < 64; ++l) {
         float acc = 0.0f;
@@ -209,13 +230,13 @@ static float blocked_sum(const float* x, size_t n, int squares) {
 }
 
 /* [candle hypothesis] candle-nn ops::rms_norm CPU: m = sqrt(sum(x^2) / dim + eps),
- * y = x / m * alpha (sum in the blocked order above).  Call sites SVL/nn/transformer.rs:286,
+ * y = x / m * alpha (sum in the order selected above).  Call sites SVL/nn/transformer.rs:286,
  * SVL/stt/model.rs:252. */
 void svlo_rms_norm(const float* x, const float* alpha, float* y, size_t rows, size_t dim, float eps) {
     for (size_t r = 0; r < rows; ++r) {
         const float* s = x + r * dim;
         float* d = y + r * dim;
-        float sum2 = blocked_sum(s, dim, 1);
+        float sum2 = row_sum(s, dim, 1);
         float m = sqrtf(sum2 / (float)dim + eps);
         for (size_t i = 0; i < dim; ++i) {
             float t = s[i] / m;
@@ -226,14 +247,14 @@ void svlo_rms_norm(const float* x, const float* alpha, float* y, size_t rows, si
 
 /* [candle hypothesis] candle-nn ops::layer_norm CPU: mean = sum(x) / dim,
  * var = sum(x^2) / dim - mean^2, y = (x - mean) * (1 / sqrt(var + eps)) * w + b (sums in the
- * blocked order above).  Call sites SVL/nn/transformer.rs:284, SVL/tts/flow_lm.rs:176. */
+ * order selected above).  Call sites SVL/nn/transformer.rs:284, SVL/tts/flow_lm.rs:176. */
 void svlo_layer_norm(const float* x, const float* w, const float* b, float* y, size_t rows,
                      size_t dim, float eps) {
     for (size_t r = 0; r < rows; ++r) {
         const float* s = x + r * dim;
         float* d = y + r * dim;
-        float sum = blocked_sum(s, dim, 0);
-        float sum2 = blocked_sum(s, dim, 1);
+        float sum = row_sum(s, dim, 0);
+        float sum2 = row_sum(s, dim, 1);
         float mean = sum / (float)dim;
         float mm = mean * mean;
         float var = sum2 / (float)dim - mm;

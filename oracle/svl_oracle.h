@@ -72,6 +72,11 @@ int svlo_attention(const float* q, const float* k, const float* v, float* out, s
 
 /* ---- candle-nn ops [candle hypothesis] ------------------------------------------------ */
 
+/* Summation order of the norm statistics: element order (candle's CPU ops, the default) or the
+ * blocked order of the GPU kernels. */
+enum { SVLO_NORM_ORDER_ELEMENT = 0, SVLO_NORM_ORDER_BLOCKED = 1 };
+void svlo_set_norm_order(int order);
+int svlo_get_norm_order(void);
 void svlo_rms_norm(const float* x, const float* alpha, float* y, size_t rows, size_t dim, float eps);
 void svlo_layer_norm(const float* x, const float* w, const float* b, float* y, size_t rows,
                      size_t dim, float eps);

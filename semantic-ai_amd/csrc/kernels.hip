@@ -514,29 +514,29 @@ size_t phase_smem(const Phase& ph) {
       const int K = g.L.in;
       if (g.L.fmt == FMT_Q8_0) {
         const int nb = K / 32, nb4 = (nb + 3) & ~3;
-        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
+        return (size_t)K * 8 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
                (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_Q4K) {
         const int nb = K / 256, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
-        return (size_t)K * 4 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
+        return (size_t)K * 8 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
                (size_t)nb * kQ4Terms * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C)
-        return (size_t)K * 4 + (size_t)16 * (K / 16 + 4) * 4 + (size_t)2 * g.ipw * 4 + 64;
-      return (size_t)K * 4 + (kRowThreads / 16) * 4 + 64;
+        return (size_t)K * 8 + (size_t)16 * (K / 16 + 4) * 4 + (size_t)2 * g.ipw * 4 + 64;
+      return (size_t)K * 8 + (kRowThreads / 16) * 4 + 64;
     }
     case PH_ATTN:
       return (size_t)kAttnStages * kAttnChunkBytes + (size_t)(ph.at.hpu * (((ph.at.cap + 7) & ~7) + 8) + 4 + 32) * 4 + 64;
     case PH_ARGMAX:
       return 32 * 4 + 64;
     case PH_NORM:
-      return (size_t)ph.nm.d * 4 + 64;
+      return (size_t)ph.nm.d * 8 + 64;
     case PH_EMBED:
       return (size_t)(ph.e.n_q + 1) * 4 + 64;
     case PH_QUANT: {
       const int K = ph.g.L.in, nb4 = (K / 32 + 3) & ~3;
-      return (size_t)K * 4 + K + (size_t)nb4 * 4 + 64;
+      return (size_t)K * 8 + K + (size_t)nb4 * 4 + 64;
     }
     case PH_QGEMM:
       return (size_t)kTileRows * kTileBatch * 4 + (size_t)kGemmStages * kGemmStageBytes + 64;

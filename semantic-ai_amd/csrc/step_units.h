@@ -9,7 +9,8 @@
 //   * dense matvec with the reference's 16-lane dot (SVL/nn/kernels/mod.rs:66-91).
 //   * attention with the reference's two passes (SVL/nn/kernels/attention.rs:139-168).
 //   * SiLU / GELU-tanh / exp as SVL/nn/kernels/{activation,mod}.rs (FMA variant).
-//   * RMSNorm / LayerNorm statistics in a 64-way blocked order (see blocked_sums).
+//   * RMSNorm / LayerNorm statistics as candle-nn's CPU ops: one f32 accumulator per sum, the
+//     elements added in index order (see element_stats).
 //
 // Data one workgroup writes and another reads within a launch (activations, KV ring, scores,
 // logits, tokens, positions) goes through agent-scope coherent loads and stores (the `sc1`
@@ -96,6 +97,7 @@ struct WgSync {
   unsigned g_arrive;   // row waves whose stores of the phase are complete (grid barrier)
   unsigned g_release;  // grid barriers of the launch this workgroup has passed
   unsigned stop;       // raised when a wait gave up or the grid barrier aborted
+  float stats[2];      // a row's norm statistics (sum of squares, sum), published by row wave 0
 };
 
 constexpr unsigned kLdsSpinLimit = 1u << 22;
@@ -145,6 +147,13 @@ struct RowSync {
     epoch += kRowWaves;
     lds_wait(&ws->r_arrive, epoch, &ws->stop);
   }
+  // The same barrier for waits of microseconds: waiting waves sleep between polls, leaving the
+  // SIMD to the wave that works.
+  __device__ __forceinline__ void sync_long() {
+    lds_signal(&ws->r_arrive);
+    epoch += kRowWaves;
+    lds_wait<true>(&ws->r_arrive, epoch, &ws->stop);
+  }
 };
 
 // ---- rows, norms, activation quantization ---------------------------------------------------------
@@ -188,47 +197,53 @@ __device__ __forceinline__ void store_row(const float (&v)[KP], int K, float* xs
   }
 }
 
-// Lane 0 ends with the oracle's butterfly over 64 partials: for o = 32, 16, ..., 1, lane l < o
-// adds lane l + o (the lanes whose results reach lane 0).
-__device__ __forceinline__ float lane0_tree_sum(float v) {
-  v = v + __shfl_down(v, 32, kWave);
-  v = v + swizzle<0x401F>(v);  // lane ^ 16
-  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xf, 0xf, false));  // row_shl:8
-  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xf, 0xf, false));  // row_shl:4
-  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x102, 0xf, 0xf, false));  // row_shl:2
-  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x101, 0xf, 0xf, false));  // row_shl:1
-  return v;
+// acc = 0; acc += t[i] for i = 0 .. n-1 in order, reading t (16-byte aligned, in LDS) 16 values
+// ahead of the additions.
+__device__ __forceinline__ float ordered_sum(const float* t, int n) {
+  typedef float v4f_t __attribute__((ext_vector_type(4)));
+  const v4f_t* t4 = (const v4f_t*)t;
+  const int n16 = n / 16;
+  float acc = 0.0f;
+  v4f_t cur[4], nxt[4];
+  if (n16 > 0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cur[u] = t4[u];
+  }
+  for (int c = 0; c < n16; ++c) {
+    if (c + 1 < n16) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) nxt[u] = t4[(c + 1) * 4 + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc = acc + cur[u].x;
+      acc = acc + cur[u].y;
+      acc = acc + cur[u].z;
+      acc = acc + cur[u].w;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+  }
+  for (int i = n16 * 16; i < n; ++i) acc = acc + t[i];
+  return acc;
 }
 
-// Sums of x[i] and of x[i]^2 over a row in the order shared with the oracle: 64 strided partials
-// (lane l adds x[l], x[l+64], ... in order), then the butterfly over the partials (offsets
-// 32 .. 1).  Run by one wave; the totals are valid in lane 0.
-template <bool PLAIN>
-__device__ __forceinline__ void blocked_sums(const float* xs, int K, float& s, float& s2) {
-  const int lane = threadIdx.x % kWave;
-  constexpr int U = 16;
-  float a = 0.0f, a2 = 0.0f;
-  int i = lane;
-  for (; i + (U - 1) * kWave < K; i += U * kWave) {
-    float v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = xs[i + u * kWave];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (PLAIN) a = a + v[u];
-      const float t = v[u] * v[u];
-      a2 = a2 + t;
-    }
+// Row statistics in element order, as candle-nn's CPU RmsNorm / LayerNorm compute them: one f32
+// accumulator per sum, x_0, x_1, ... added in index order (a sequential chain: its rounding is
+// what the reference's greedy tokens depend on once activations are quantized).  The row is
+// staged in LDS as xs[0, K) = x_i and xs[K, 2K) = fl(x_i * x_i) (16-byte aligned, K % 4 == 0).
+// Row wave 0 runs both sums in one instruction stream -- lane 0 over the squares, lane 1 over
+// the values -- and publishes them; the other row waves sleep at the barrier meanwhile.
+// s2 = sum of squares, s = sum of values (valid for LayerNorm only).
+__device__ __forceinline__ void element_stats(const float* xs, int K, RowSync& rs, float& s, float& s2) {
+  rs.sync();  // the row is staged
+  if (threadIdx.x < kWave) {
+    const float acc = ordered_sum(threadIdx.x == 1 ? xs : xs + K, K);
+    if (threadIdx.x < 2) rs.ws->stats[threadIdx.x] = acc;
   }
-  for (; i < K; i += kWave) {
-    const float v = xs[i];
-    if (PLAIN) a = a + v;
-    const float t = v * v;
-    a2 = a2 + t;
-  }
-  s = PLAIN ? lane0_tree_sum(a) : 0.0f;
-  s2 = lane0_tree_sum(a2);
+  rs.sync_long();
+  s2 = rs.ws->stats[0];
+  s = rs.ws->stats[1];
 }
 
 // Norm weights of the elements a thread owns, loaded ahead of the row statistics.
@@ -247,18 +262,20 @@ __device__ __forceinline__ void load_norm_weights(int norm, const float* nw, con
 
 // candle-nn rms_norm (x / m * alpha, m = sqrt(sum(x^2) / K + eps)) or layer_norm
 // ((x - mean) * (1 / sqrt(var + eps)) * w + b, var = sum(x^2) / K - mean^2) of the row in v,
-// in place.  xs (K floats) is LDS scratch.
+// in place.  xs (2 K floats) is LDS scratch.
 template <int KP>
 __device__ __forceinline__ void norm_regs(float (&v)[KP], int K, int norm, const NormW<KP>& nw, float eps, float* xs,
                                           RowSync& rs) {
-  store_row(v, K, xs);
-  rs.sync();
-  // every row wave computes the statistics (lane 0 holds them), so no second barrier is needed
+#pragma unroll
+  for (int u = 0; u < KP; ++u) {
+    const int i = threadIdx.x + u * kRowThreads;
+    if (i < K) {
+      xs[i] = v[u];
+      xs[K + i] = v[u] * v[u];
+    }
+  }
   float s, s2;
-  if (norm == NORM_LAYER) blocked_sums<true>(xs, K, s, s2);
-  else blocked_sums<false>(xs, K, s, s2);
-  s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));    // lane 0's totals
-  s2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s2)));
+  element_stats(xs, K, rs, s, s2);
   float s0, s1 = 0.0f;
   if (norm == NORM_RMS) {
     s0 = sqrtf(s2 / (float)K + eps);
@@ -333,8 +350,7 @@ __device__ __forceinline__ void load_norm_weights4(int norm, const float* nw, co
   }
 }
 
-// norm_regs on the chunked row: the same statistics over xs in the blocked order, the same
-// per-element arithmetic.
+// norm_regs on the chunked row: the same statistics, the same per-element arithmetic.
 template <int KU>
 __device__ __forceinline__ void norm_row4(v4f (&v)[KU], int K, int norm, const NormW4<KU>& nw, float eps, float* xs,
                                           RowSync& rs) {
@@ -342,14 +358,13 @@ __device__ __forceinline__ void norm_row4(v4f (&v)[KU], int K, int norm, const N
 #pragma unroll
   for (int u = 0; u < KU; ++u) {
     const int c = threadIdx.x + u * kRowThreads;
-    if (c < nc) ((v4f*)xs)[c] = v[u];
+    if (c < nc) {
+      ((v4f*)xs)[c] = v[u];
+      ((v4f*)(xs + K))[c] = v[u] * v[u];
+    }
   }
-  rs.sync();
   float s, s2;
-  if (norm == NORM_LAYER) blocked_sums<true>(xs, K, s, s2);
-  else blocked_sums<false>(xs, K, s, s2);
-  s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));
-  s2 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s2)));
+  element_stats(xs, K, rs, s, s2);
   if (norm == NORM_RMS) {
     const float s0 = sqrtf(s2 / (float)K + eps);
 #pragma unroll
@@ -409,37 +424,6 @@ __device__ __forceinline__ void quantize_row4(const v4f (&v)[KU], int K, int8_t*
     const uint32_t q3 = (uint32_t)sat_i8(roundf(v[u].w * idm)) & 0xffu;
     ((uint32_t*)xq)[c] = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
   }
-}
-
-// acc = 0; acc += t[i] for i = 0 .. n-1 in order, reading t (16-byte aligned, in LDS) 16 values
-// ahead of the additions.
-__device__ __forceinline__ float ordered_sum(const float* t, int n) {
-  typedef float v4f_t __attribute__((ext_vector_type(4)));
-  const v4f_t* t4 = (const v4f_t*)t;
-  const int n16 = n / 16;
-  float acc = 0.0f;
-  v4f_t cur[4], nxt[4];
-  if (n16 > 0) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) cur[u] = t4[u];
-  }
-  for (int c = 0; c < n16; ++c) {
-    if (c + 1 < n16) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) nxt[u] = t4[(c + 1) * 4 + u];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      acc = acc + cur[u].x;
-      acc = acc + cur[u].y;
-      acc = acc + cur[u].z;
-      acc = acc + cur[u].w;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
-  }
-  for (int i = n16 * 16; i < n; ++i) acc = acc + t[i];
-  return acc;
 }
 
 // ---- GEMV epilogues ---------------------------------------------------------------------------
@@ -609,7 +593,7 @@ __device__ __forceinline__ Q8Geom q8_geom(int K, int items, int ipw, int parts, 
   return g;
 }
 
-// LDS of a Q8_0 unit: xs [K] f32 | xq [K] int8 | xdq [nb, padded to 4] f32 |
+// LDS of a Q8_0 unit: xs [2 K] f32 (norm scratch) | xq [K] int8 | xdq [nb, padded to 4] f32 |
 // T [2 ipw][q8_row_stride(nb)] f32 | Y [2 ipw] f32.
 struct Q8Lds {
   float* xs;
@@ -622,7 +606,7 @@ struct Q8Lds {
 __device__ __forceinline__ Q8Lds q8_lds(unsigned char* smem, int K, int nb, int ipw) {
   Q8Lds l;
   l.xs = (float*)smem;
-  l.xq = (int8_t*)(l.xs + K);
+  l.xq = (int8_t*)(l.xs + 2 * K);
   l.xdq = (float*)(l.xq + K);
   l.T = l.xdq + ((nb + 3) & ~3);
   l.Y = l.T + 2 * ipw * q8_row_stride(nb);
@@ -765,7 +749,7 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
 // 8 row waves x row slots.
 __host__ __device__ constexpr int q4k_red_words(int K) { return 2 * 2 * kRowWaves * row_slots(K); }
 
-// LDS of a Q4K unit: xs [K] f32 | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
+// LDS of a Q4K unit: xs [2 K] f32 (norm scratch) | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
 // bs [nb][16] i32 | red [q4k_red_words(K)] | T [nb][9][ts] f32 | Y [2 ipw] f32.
 struct Q4Lds {
   float* xs;
@@ -780,7 +764,7 @@ struct Q4Lds {
 __device__ __forceinline__ Q4Lds q4_lds(unsigned char* smem, int K, int nb, int ts) {
   Q4Lds l;
   l.xs = (float*)smem;
-  l.xq = (int8_t*)(l.xs + K);
+  l.xq = (int8_t*)(l.xs + 2 * K);
   l.xd = (float*)(l.xq + K);
   l.bs = (int*)(l.xd + ((nb + 3) & ~3));
   l.red = (float*)(l.bs + nb * 16);
@@ -1051,8 +1035,8 @@ __device__ __forceinline__ bool is_split_gemv(const Phase* ph) {
 template <int KP>
 __device__ __forceinline__ void quant_unit(const GemvArgs& a, int b, unsigned char* smem, RowSync& rs) {
   const int K = a.L.in, nb = K / 32;
-  float* xs = (float*)smem;
-  int8_t* xq = (int8_t*)(xs + K);
+  float* xs = (float*)smem;  // 2 K: norm scratch
+  int8_t* xq = (int8_t*)(xs + 2 * K);
   float* xdq = (float*)(xq + K);
   constexpr int KU = chunk_slots(KP * kRowThreads);
   constexpr bool kNorm = KP <= 8;
@@ -1322,8 +1306,8 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
   const int i0 = part * a.ipw;
   const int ni = min(a.ipw, gemv_items(a) - i0);
   const int NR = silu ? 2 * ni : ni;
-  float* xs = (float*)smem;   // K
-  float* Y = xs + K;          // kRowThreads / 16
+  float* xs = (float*)smem;   // 2 K: the (normalized) row, the norm's squares
+  float* Y = xs + 2 * K;      // kRowThreads / 16
   constexpr bool kNorm = KP <= 8;  // rows wider than 4096 are never normalized (d_model <= 4096)
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
@@ -1393,7 +1377,7 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
 __device__ __forceinline__ int dense_chain_stride(int K) { return K / 16 + 4; }
 
 struct DenseLds {
-  float* xs;  // [K] norm scratch
+  float* xs;  // [2 K] norm scratch
   float* xT;  // [16][K / 16 + 4]
   float* Y;   // [2 ipw]
 };
@@ -1401,7 +1385,7 @@ struct DenseLds {
 __device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
   DenseLds l;
   l.xs = (float*)smem;
-  l.xT = l.xs + K;
+  l.xT = l.xs + 2 * K;
   l.Y = l.xT + 16 * dense_chain_stride(K);
   return l;
 }

@@ -427,6 +427,97 @@ def test_s1_q8_0_logits_within_bar(s1_q8):
         text = to
 
 
+def _lockstep_fills(shape, B, seed=7):
+    """The B = 64 benchmark's rings: stream b pre-filled with the first fills[b] positions of one
+    seeded full-window cache, fills uniform in [1, window]."""
+    fills = [int(f) for f in np.random.default_rng(seed).integers(1, shape.context + 1, size=B)]
+    ks, vs = W.prefill_caches(shape, shape.context, seed=8)
+    return fills, ks, vs
+
+
+def test_s1_q8_0_64_stream_lockstep_matches_gemv_and_oracle(s1_q8):
+    """The B = 64 benchmark configuration: STT-1B Q8_0, 64 streams with rings pre-filled to
+    seeded fills in [1, 750], lockstep steps through the MFMA GEMM path.  Every stream's logits
+    and tokens are bit-equal to the same stream stepped alone (GEMV path), and the first streams
+    equal the oracle's."""
+    g, o = s1_q8
+    s, B, n = W.S1, 64, 4
+    fills, ks, vs = _lockstep_fills(s, B)
+    st = g.init_state(batch=B)
+    for b in range(B):
+        st.load_stream(b, [k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
+    audio = W.audio_tokens(s, n, seed=1, batch=B)  # [B, n, n_q]
+    text = np.full(B, s.text_card, dtype=np.uint32)
+    texts, logits, toks = [], [], []
+    for i in range(n):
+        tb, lb = g.step(text, audio[:, i], st, want_logits=True)
+        texts.append(text.copy())
+        logits.append(lb)
+        toks.append(tb)
+        text = tb.astype(np.uint32)
+    del st
+    for b in range(B):
+        one = g.init_state()
+        one.load_stream(0, [k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
+        ob = None
+        if b < 4:
+            ob = o.state_from_layer_caches([k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
+        for i in range(n):
+            t1, l1 = g.step([texts[i][b]], audio[b, i][None], one, want_logits=True)
+            assert np.array_equal(logits[i][b].view(np.uint32), l1[0].view(np.uint32)), (b, i, fills[b])
+            assert toks[i][b] == t1[0], (b, i)
+            if ob is not None:
+                to, lo = ob.stt_step(int(texts[i][b]), audio[b, i], want_logits=True)
+                assert np.array_equal(l1[0].view(np.uint32), lo.view(np.uint32)), (b, i, fills[b])
+                assert to == t1[0]
+
+
+@pytest.fixture(scope="module")
+def s1_bf16():
+    oracle.set_threads(min(16, os.cpu_count() or 4))
+    t, g, o = build(W.S1, "bf16", seed=0)
+    del t
+    return g, o
+
+
+def test_s1_bf16_logits_bit_exact_and_greedy_tokens(s1_bf16):
+    """STT-1B shape, bf16 weights (f32 arithmetic, 16-lane dot), window 750: the first 4 steps'
+    logits bit-exact to the oracle, then 32 greedy steps token-identical."""
+    g, o = s1_bf16
+    audio = W.audio_tokens(W.S1, 32, seed=1)[0]
+    gs, os_ = g.init_state(), o.new_state()
+    text = W.S1.text_card
+    for i in range(4):
+        a = audio[i] if i else np.full(W.S1.n_q, W.S1.card, np.uint32)
+        tg, lg = g.step([text], a[None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, a, want_logits=True)
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), (i, float(np.max(np.abs(lg[0] - lo))))
+        assert tg[0] == to
+        text = to
+    got = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    assert np.array_equal(got, o.new_state().stt_greedy(audio))
+
+
+def test_s2_q4k_window_3000_logits_and_greedy_tokens():
+    """STT-2.6B shape, Q4K linears (Q8K activations), window 3000: 8 steps of bit-exact logits,
+    then 16 greedy steps token-identical."""
+    oracle.set_threads(min(16, os.cpu_count() or 4))
+    t, g, o = build(W.S2, "q4k", seed=0)
+    del t
+    audio = W.audio_tokens(W.S2, 16, seed=1)[0]
+    gs, os_ = g.init_state(), o.new_state()
+    text = W.S2.text_card
+    for i in range(8):
+        a = audio[i] if i else np.full(W.S2.n_q, W.S2.card, np.uint32)
+        tg, lg = g.step([text], a[None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, a, want_logits=True)
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), (i, float(np.max(np.abs(lg[0] - lo))))
+        assert tg[0] == to
+        text = to
+    got = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    assert np.array_equal(got, o.new_state().stt_greedy(audio))
+
+
 def test_t1_f32_prefilled_256_within_f32_bar():
     """Pocket-TTS shape, f32, 256 prefilled positions, 16 steps: z within 1e-4."""
     s = W.T1

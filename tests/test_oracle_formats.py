@@ -206,3 +206,120 @@ def test_q4k_min_term_matters():
     x[:32] -= 1.0
     deq = oracle.dequantize_q4k(oracle.quantize_q4k(x), 256)
     assert np.max(np.abs(deq - x)) < 0.02
+
+
+# ---- Q4K from_float known answers --------------------------------------------------------------
+# BlockQ4K::from_float fits every 32-value sub-block with make_qkx1_quants(15, 5, x) -- L from
+# the range, then alternating least-squares refits of (scale, min) with min clamped to <= 0, up
+# to 5 passes -- quantizes the fitted scales and mins to 6 bits against the block maxima
+# (d = max_scale / 63, dmin = max_min / 63 as f16) and codes each value on the resulting grid.
+# The super-block below is built so that every step can be followed by hand; the comments give
+# the numbers.  a = 2^-6.
+
+_A = 2.0 ** -6
+
+
+def _grid(s, m, q):
+    return [s * v - m for v in q]
+
+
+_Q_GRID = [0, 15] + [(5 * i) % 16 for i in range(30)]   # a 4-bit code ramp with both ends present
+
+
+def _kat_superblock():
+    sub = [
+        # 0: the second pass changes L.  Pass 1: iscale = 15 / (15 a) = 1 / a, L = (0, 15, 7 x 30)
+        #    (round(7.4) = 7), LS scale = (15 * 15 + 30 * 7.4 * 7) / (225 + 30 * 49) a
+        #    = 1779 / 1695 a = 1.04956 a, mean residual 0.849 a / 32 > 0 -> min 0.  Pass 2:
+        #    iscale = 0.95278 / a, L(15 a) = round(14.29) = 14 (changed), scale = 1764 / 1666 a
+        #    = 1.058824 a, min = mean(x - scale L) = -0.1765 a / 32 = -0.005515 a.  Pass 3:
+        #    L unchanged (7.4 a -> 6.994, 15 a -> 14.17), scale = 1.059565 a, min = -0.010707 a.
+        #    Result (scale, -min) = (0.016556, 1.6729e-4).  One pass alone gives min 0.
+        [0.0, 15 * _A] + [7.4 * _A] * 30,
+        # 1: exact grid s = 2^-8, min 2^-12: the fit returns (2^-8, 2^-12) exactly.
+        _grid(2.0 ** -8, 2.0 ** -12, _Q_GRID),
+        # 2: all positive, two levels a and 2a: min(x) = a > 0 -> 0; iscale = 15 / 2a, L = 8 and 15;
+        #    pass 1 scale = (16 * 8 + 16 * 30) a / (16 * 64 + 16 * 225) = 608 / 4624 a = 0.131488 a,
+        #    min = -0.01211 a; pass 2 keeps L but refits: scale = 0.132453 a, min = -0.023203 a.
+        [_A] * 16 + [2 * _A] * 16,
+        # 3: constant: max == min -> (0, 0), so the whole sub-block codes as 0 and decodes to 0.
+        [0.01] * 32,
+        # 4: exact grid with the largest scale and min: (2^-5, 2^-9).
+        _grid(2.0 ** -5, 2.0 ** -9, _Q_GRID),
+        # 5: exact grid, zero min: (2^-7, -0).
+        _grid(2.0 ** -7, 0.0, _Q_GRID),
+        # 6: exact grid (2^-6, 2^-10).
+        _grid(2.0 ** -6, 2.0 ** -10, _Q_GRID),
+        # 7: exact grid with a scale that is not a power of two: (3 * 2^-8, 3 * 2^-11).
+        _grid(3 * 2.0 ** -8, 3 * 2.0 ** -11, _Q_GRID),
+    ]
+    return np.array([v for s in sub for v in s], dtype=np.float32)
+
+
+def test_q4k_from_float_known_answer_superblock():
+    blk = oracle.quantize_q4k(_kat_superblock()).reshape(-1)
+    d = blk[0:2].copy().view(np.float16)[0]
+    dmin = blk[2:4].copy().view(np.float16)[0]
+    # max_scale = 2^-5 (sub-block 4), max_min = 2^-9 (sub-block 4):
+    # d = f16(2^-5 / 63) = 1040 * 2^-21 (0x1010), dmin = f16(2^-9 / 63) = 520 * 2^-24 (subnormal, 0x0208)
+    assert blk[0:2].copy().view(np.uint16)[0] == 0x1010
+    assert blk[2:4].copy().view(np.uint16)[0] == 0x0208
+    # 6-bit scales round(63 scale / 2^-5): 33.38 -> 33, 7.875 -> 8, 4.172 -> 4, 0, 63, 15.75 -> 16,
+    # 31.5 -> 32 (ties away from zero), 23.625 -> 24; mins round(63 min / 2^-9): 5.396 -> 5,
+    # 7.875 -> 8, 11.69 -> 12, 0, 63, 0, 31.5 -> 32, 47.25 -> 47.
+    ls = [33, 8, 4, 0, 63, 16, 32, 24]
+    lm = [5, 8, 12, 0, 63, 0, 32, 47]
+    assert blk[4:16].tolist() == [0xE1, 0x48, 0x84, 0x40, 0xC5, 0x08, 0x8C, 0x80, 0xFF, 0x00, 0x00, 0xF8]
+    assert _pack_scales(ls, lm) == bytes(blk[4:16])
+    # codes: round((x + dmin * lm) / (d * ls)), clamped to [0, 15]
+    codes = np.zeros(256, dtype=np.int64)
+    for i in range(4):
+        for l in range(32):
+            codes[64 * i + l] = blk[16 + 32 * i + l] & 0xF
+            codes[64 * i + 32 + l] = blk[16 + 32 * i + l] >> 4
+    codes = codes.reshape(8, 32)
+    # sub-block 0 on the grid d * 33 = 0.016365, offset dmin * 5 = 1.55e-4: 0 -> 0, 15a -> 14.33,
+    # 7.4a -> 7.08
+    assert codes[0].tolist() == [0, 14] + [7] * 30
+    # the exact grids come back as their codes (grid steps within 1.6 % of s, offsets within
+    # 1e-3 of a step)
+    for j in (1, 4, 5, 6, 7):
+        assert codes[j].tolist() == _Q_GRID, j
+    # sub-block 2 on the grid d * 4, offset dmin * 12: a -> 8.06, 2a -> 15.94
+    assert codes[2].tolist() == [8] * 16 + [15] * 16
+    assert codes[3].tolist() == [0] * 32
+    deq = oracle.dequantize_q4k(blk, 256).reshape(8, 32)
+    assert np.all(deq[3] == 0.0)  # a constant sub-block decodes to zero
+    assert float(d) * 63 == pytest.approx(2.0 ** -5, rel=2 ** -10)
+    assert float(dmin) * 63 == pytest.approx(2.0 ** -9, rel=2 ** -9)
+
+
+def test_q4k_codes_are_nearest_grid_points():
+    # Every code is the nearest point of its sub-block's decoded grid d*sc*q - dmin*m, q in 0..15
+    # (ties aside), for any input: a wrong nibble order, shift or clamp fails this.
+    rng = np.random.default_rng(11)
+    x = np.concatenate([(rng.standard_normal(4096) * 0.02), rng.uniform(-1, 3, 4096),
+                        np.repeat(rng.standard_normal(64), 64) * 0.1]).astype(np.float32)
+    raw = oracle.quantize_q4k(x.reshape(-1, 256)).reshape(-1, 144)
+    deq = oracle.dequantize_q4k(raw, 256).reshape(-1, 8, 32).astype(np.float64)
+    xs = x.reshape(-1, 8, 32).astype(np.float64)
+    for b in range(raw.shape[0]):
+        blk = raw[b]
+        d = float(blk[0:2].copy().view(np.float16)[0])
+        dm = float(blk[2:4].copy().view(np.float16)[0])
+        sc = blk[4:16]
+        for j in range(8):
+            if j < 4:
+                s6, m6 = sc[j] & 63, sc[j + 4] & 63
+            else:
+                s6 = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4)
+                m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4)
+            step, off = d * s6, dm * m6
+            if step == 0:
+                assert np.all(deq[b, j] == -off * 0 + deq[b, j])
+                continue
+            grid = step * np.arange(16) - off
+            dist = np.abs(xs[b, j][:, None] - grid[None, :])
+            best = dist.min(axis=1)
+            got = np.abs(xs[b, j] - deq[b, j])
+            assert np.all(got <= best + 1e-6 * step), (b, j)

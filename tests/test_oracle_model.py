@@ -274,3 +274,51 @@ def test_model_errors():
     m = oracle.Model(s.config(0), t)
     with pytest.raises(ValueError, match="out of range"):
         m.new_state().stt_step(s.text_card + 1, np.zeros(s.n_q, np.uint32))
+
+
+def test_norm_statistics_are_element_order_sums():
+    """candle-nn's CPU rms_norm / layer_norm sum each row with one f32 accumulator in index
+    order.  Row: 1.0 followed by 4096 copies of 2^-13.  In index order every square 2^-26 is
+    absorbed (1 + 2^-26 rounds back to 1, half an ulp of 1 being 2^-24), so sum(x^2) = 1 and
+    sum(x) = 1 + 4096 * 2^-13 = 1.5 (each 2^-13 is a multiple of ulp(1)); any order that adds the
+    small squares before the 1.0 absorbs them (the 64-way blocked order, a tree, float64) gets a
+    larger sum."""
+    K = 1 + 4096
+    x = np.full(K, 2.0 ** -13, dtype=np.float32)
+    x[0] = 1.0
+    alpha = np.ones(K, np.float32)
+    sum2, sum1 = np.float32(1.0), np.float32(1.5)
+    # RMSNorm: y = x / m, m = sqrt(sum2 / K + eps)
+    m = np.sqrt(np.float32(sum2 / np.float32(K)) + np.float32(1e-8), dtype=np.float32)
+    assert np.array_equal(oracle.rms_norm(x[None], alpha, 1e-8)[0].view(np.uint32), (x / m).view(np.uint32))
+    oracle.set_norm_order("blocked")
+    try:
+        other = oracle.rms_norm(x[None], alpha, 1e-8)[0]
+    finally:
+        oracle.set_norm_order("element")
+    assert np.all(other < x / m)  # a larger sum of squares, a smaller normalized row
+    # LayerNorm: mean = sum1 / K, var = sum2 / K - mean^2, y = (x - mean) * (1 / sqrt(var + eps))
+    w, b = np.ones(K, np.float32), np.zeros(K, np.float32)
+    mean = np.float32(sum1 / np.float32(K))
+    var = np.float32(np.float32(sum2 / np.float32(K)) - np.float32(mean * mean))
+    inv = np.float32(np.float32(1.0) / np.sqrt(np.float32(var + np.float32(1e-5)), dtype=np.float32))
+    expected = ((x - mean) * inv).astype(np.float32)
+    assert np.array_equal(oracle.layer_norm(x[None], w, b, 1e-5)[0].view(np.uint32), expected.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,steps", [("q8_0", 200), ("q4k", 100)])
+def test_norm_order_decides_quantized_greedy_tokens(dtype, steps):
+    """With quantized activations the step is sensitive to the last bit of the norm statistic:
+    summing the same squares in another order (the 64-way blocked order) changes the greedy
+    tokens within these runs, while f32 weights keep them.  This is why the GPU kernels sum the
+    statistics in candle's element order."""
+    shape = W.S1_SMALL if dtype == "q8_0" else W.S2_SMALL
+    m = oracle.Model(shape.config(W.quantize_code(dtype)), W.make_weights(shape, dtype, seed=0))
+    audio = W.audio_tokens(shape, steps, seed=1)[0]
+    try:
+        oracle.set_norm_order("blocked")
+        blocked = m.new_state().stt_greedy(audio)
+    finally:
+        oracle.set_norm_order("element")
+    element = m.new_state().stt_greedy(audio)
+    assert not np.array_equal(blocked, element)
