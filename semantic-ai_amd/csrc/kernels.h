@@ -235,5 +235,6 @@ hipError_t launch_f32_to_kv(const float* src, void* dst, int kv_bf16, size_t n, 
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
 hipError_t launch_fill_i32(int* p, int v, size_t n, hipStream_t s);
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
+hipError_t launch_row_stats(const float* x, int rows, int K, int norm, float* out, hipStream_t s);
 
 }  // namespace svl

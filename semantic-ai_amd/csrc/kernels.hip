@@ -514,29 +514,29 @@ size_t phase_smem(const Phase& ph) {
       const int K = g.L.in;
       if (g.L.fmt == FMT_Q8_0) {
         const int nb = K / 32, nb4 = (nb + 3) & ~3;
-        return (size_t)K * 8 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
+        return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
                (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_Q4K) {
         const int nb = K / 256, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
-        return (size_t)K * 8 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
+        return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
                (size_t)nb * kQ4Terms * ts * 4 + (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C)
-        return (size_t)K * 8 + (size_t)16 * (K / 16 + 4) * 4 + (size_t)2 * g.ipw * 4 + 64;
-      return (size_t)K * 8 + (kRowThreads / 16) * 4 + 64;
+        return (size_t)norm_scratch_floats(K) * 4 + (size_t)16 * (K / 16 + 4) * 4 + (size_t)2 * g.ipw * 4 + 64;
+      return (size_t)norm_scratch_floats(K) * 4 + (kRowThreads / 16) * 4 + 64;
     }
     case PH_ATTN:
       return (size_t)kAttnStages * kAttnChunkBytes + (size_t)(ph.at.hpu * (((ph.at.cap + 7) & ~7) + 8) + 4 + 32) * 4 + 64;
     case PH_ARGMAX:
       return 32 * 4 + 64;
     case PH_NORM:
-      return (size_t)ph.nm.d * 8 + 64;
+      return (size_t)norm_scratch_floats(ph.nm.d) * 4 + 64;
     case PH_EMBED:
       return (size_t)(ph.e.n_q + 1) * 4 + 64;
     case PH_QUANT: {
       const int K = ph.g.L.in, nb4 = (K / 32 + 3) & ~3;
-      return (size_t)K * 8 + K + (size_t)nb4 * 4 + 64;
+      return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 4 + 64;
     }
     case PH_QGEMM:
       return (size_t)kTileRows * kTileBatch * 4 + (size_t)kGemmStages * kGemmStageBytes + 64;
@@ -883,6 +883,37 @@ hipError_t launch_fill_i32(int* p, int v, size_t n, hipStream_t s) {
 __global__ __launch_bounds__(256) void copy_kernel(const v4i* src, v4i* dst, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     __builtin_nontemporal_store(ldg_stream(src + i), gbl(dst + i));
+}
+
+// The norm statistics of rows of x exactly as the step's norm prologues compute them (values
+// staged by the row waves, element-order sums): out[r] = {sum of squares, sum} (the sum for
+// LayerNorm only).  One workgroup of row waves per row.
+template <int KP>
+__global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* x, int K, int norm, float* out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ WgSync ws;
+  init_wg_sync(&ws);
+  RowSync rs{&ws, 0u};
+  float v[KP];
+  load_row(x + (size_t)blockIdx.x * K, K, v);
+  NormW<KP> nw;
+#pragma unroll
+  for (int u = 0; u < KP; ++u) nw.w[u] = 1.0f, nw.b[u] = 0.0f;
+  norm_regs(v, K, norm, nw, 1e-5f, (float*)smem, rs);
+  if (threadIdx.x == 0) {
+    out[2 * blockIdx.x] = ws.stats[0];
+    out[2 * blockIdx.x + 1] = norm == NORM_LAYER ? ws.stats[1] : 0.0f;
+  }
+}
+
+hipError_t launch_row_stats(const float* x, int rows, int K, int norm, float* out, hipStream_t s) {
+  const size_t smem = (size_t)norm_scratch_floats(K) * 4;
+  switch (row_slots(K)) {
+    case 2: hipLaunchKernelGGL(row_stats_kernel<2>, dim3(rows), dim3(kRowThreads), smem, s, x, K, norm, out); break;
+    case 4: hipLaunchKernelGGL(row_stats_kernel<4>, dim3(rows), dim3(kRowThreads), smem, s, x, K, norm, out); break;
+    default: hipLaunchKernelGGL(row_stats_kernel<8>, dim3(rows), dim3(kRowThreads), smem, s, x, K, norm, out); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s) {

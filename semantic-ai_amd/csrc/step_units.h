@@ -31,6 +31,7 @@
 #pragma once
 
 #include "device_math.h"
+#include "exact_sum.h"
 #include "kernels.h"
 
 namespace svl {
@@ -229,17 +230,27 @@ __device__ __forceinline__ float ordered_sum(const float* t, int n) {
 }
 
 // Row statistics in element order, as candle-nn's CPU RmsNorm / LayerNorm compute them: one f32
-// accumulator per sum, x_0, x_1, ... added in index order (a sequential chain: its rounding is
-// what the reference's greedy tokens depend on once activations are quantized).  The row is
-// staged in LDS as xs[0, K) = x_i and xs[K, 2K) = fl(x_i * x_i) (16-byte aligned, K % 4 == 0).
-// Row wave 0 runs both sums in one instruction stream -- lane 0 over the squares, lane 1 over
-// the values -- and publishes them; the other row waves sleep at the barrier meanwhile.
-// s2 = sum of squares, s = sum of values (valid for LayerNorm only).
-__device__ __forceinline__ void element_stats(const float* xs, int K, RowSync& rs, float& s, float& s2) {
+// accumulator per sum, x_0, x_1, ... added in index order.  The row is staged in LDS in the
+// lane-segment layout of exact_sum.h (Q chunks of 8 per lane): xs[0, staged_floats(K)) the values
+// (LayerNorm only; RMSNorm uses that space as the summing wave's scratch) and
+// xs[staged_floats(K), ...) the squares fl(x_i * x_i).  Row wave 0 sums and publishes; the other
+// row waves sleep at the barrier meanwhile.  RMSNorm's sum of squares takes the exact parallel
+// path of exact_sum.h; LayerNorm runs the two sequential chains in one instruction stream (lane 0
+// over the squares, lane 1 over the values).  s2 = sum of squares, s = sum of values (LayerNorm).
+__host__ __device__ constexpr int norm_scratch_floats(int K) { return 2 * staged_floats(K); }
+
+template <int Q>
+__device__ __forceinline__ void element_stats(float* xs, int K, int norm, RowSync& rs, float& s, float& s2) {
   rs.sync();  // the row is staged
   if (threadIdx.x < kWave) {
-    const float acc = ordered_sum(threadIdx.x == 1 ? xs : xs + K, K);
-    if (threadIdx.x < 2) rs.ws->stats[threadIdx.x] = acc;
+    const float* sq = xs + staged_floats(K);
+    if (norm == NORM_RMS) {
+      const float acc = exact_sum_squares<Q>(sq, K, (unsigned char*)xs);
+      if (threadIdx.x == 0) rs.ws->stats[0] = acc;
+    } else {
+      const float acc = staged_sequential_sum<Q>(threadIdx.x == 1 ? xs : sq, K);
+      if (threadIdx.x < 2) rs.ws->stats[threadIdx.x] = acc;
+    }
   }
   rs.sync_long();
   s2 = rs.ws->stats[0];
@@ -266,16 +277,19 @@ __device__ __forceinline__ void load_norm_weights(int norm, const float* nw, con
 template <int KP>
 __device__ __forceinline__ void norm_regs(float (&v)[KP], int K, int norm, const NormW<KP>& nw, float eps, float* xs,
                                           RowSync& rs) {
+  constexpr int Q = KP;  // K <= 512 KP
+  float* sq = xs + staged_floats(K);
 #pragma unroll
   for (int u = 0; u < KP; ++u) {
     const int i = threadIdx.x + u * kRowThreads;
     if (i < K) {
-      xs[i] = v[u];
-      xs[K + i] = v[u] * v[u];
+      const int p = seg_pos<Q>(i);
+      if (norm == NORM_LAYER) xs[p] = v[u];
+      sq[p] = v[u] * v[u];
     }
   }
   float s, s2;
-  element_stats(xs, K, rs, s, s2);
+  element_stats<Q>(xs, K, norm, rs, s, s2);
   float s0, s1 = 0.0f;
   if (norm == NORM_RMS) {
     s0 = sqrtf(s2 / (float)K + eps);
@@ -354,17 +368,20 @@ __device__ __forceinline__ void load_norm_weights4(int norm, const float* nw, co
 template <int KU>
 __device__ __forceinline__ void norm_row4(v4f (&v)[KU], int K, int norm, const NormW4<KU>& nw, float eps, float* xs,
                                           RowSync& rs) {
+  constexpr int Q = 4 * KU;  // K <= 2048 KU
   const int nc = K / 4;
+  float* sq = xs + staged_floats(K);
 #pragma unroll
   for (int u = 0; u < KU; ++u) {
     const int c = threadIdx.x + u * kRowThreads;
     if (c < nc) {
-      ((v4f*)xs)[c] = v[u];
-      ((v4f*)(xs + K))[c] = v[u] * v[u];
+      const int p = seg_pos<Q>(4 * c);  // a multiple of 4: the chunk stays in one segment
+      if (norm == NORM_LAYER) *(v4f*)(xs + p) = v[u];
+      *(v4f*)(sq + p) = v[u] * v[u];
     }
   }
   float s, s2;
-  element_stats(xs, K, rs, s, s2);
+  element_stats<Q>(xs, K, norm, rs, s, s2);
   if (norm == NORM_RMS) {
     const float s0 = sqrtf(s2 / (float)K + eps);
 #pragma unroll
@@ -593,7 +610,7 @@ __device__ __forceinline__ Q8Geom q8_geom(int K, int items, int ipw, int parts, 
   return g;
 }
 
-// LDS of a Q8_0 unit: xs [2 K] f32 (norm scratch) | xq [K] int8 | xdq [nb, padded to 4] f32 |
+// LDS of a Q8_0 unit: xs [norm_scratch_floats(K)] f32 | xq [K] int8 | xdq [nb, padded to 4] f32 |
 // T [2 ipw][q8_row_stride(nb)] f32 | Y [2 ipw] f32.
 struct Q8Lds {
   float* xs;
@@ -606,7 +623,7 @@ struct Q8Lds {
 __device__ __forceinline__ Q8Lds q8_lds(unsigned char* smem, int K, int nb, int ipw) {
   Q8Lds l;
   l.xs = (float*)smem;
-  l.xq = (int8_t*)(l.xs + 2 * K);
+  l.xq = (int8_t*)(l.xs + norm_scratch_floats(K));
   l.xdq = (float*)(l.xq + K);
   l.T = l.xdq + ((nb + 3) & ~3);
   l.Y = l.T + 2 * ipw * q8_row_stride(nb);
@@ -749,7 +766,7 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
 // 8 row waves x row slots.
 __host__ __device__ constexpr int q4k_red_words(int K) { return 2 * 2 * kRowWaves * row_slots(K); }
 
-// LDS of a Q4K unit: xs [2 K] f32 (norm scratch) | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
+// LDS of a Q4K unit: xs [norm_scratch_floats(K)] f32 | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
 // bs [nb][16] i32 | red [q4k_red_words(K)] | T [nb][9][ts] f32 | Y [2 ipw] f32.
 struct Q4Lds {
   float* xs;
@@ -764,7 +781,7 @@ struct Q4Lds {
 __device__ __forceinline__ Q4Lds q4_lds(unsigned char* smem, int K, int nb, int ts) {
   Q4Lds l;
   l.xs = (float*)smem;
-  l.xq = (int8_t*)(l.xs + 2 * K);
+  l.xq = (int8_t*)(l.xs + norm_scratch_floats(K));
   l.xd = (float*)(l.xq + K);
   l.bs = (int*)(l.xd + ((nb + 3) & ~3));
   l.red = (float*)(l.bs + nb * 16);
@@ -1035,8 +1052,8 @@ __device__ __forceinline__ bool is_split_gemv(const Phase* ph) {
 template <int KP>
 __device__ __forceinline__ void quant_unit(const GemvArgs& a, int b, unsigned char* smem, RowSync& rs) {
   const int K = a.L.in, nb = K / 32;
-  float* xs = (float*)smem;  // 2 K: norm scratch
-  int8_t* xq = (int8_t*)(xs + 2 * K);
+  float* xs = (float*)smem;  // norm scratch
+  int8_t* xq = (int8_t*)(xs + norm_scratch_floats(K));
   float* xdq = (float*)(xq + K);
   constexpr int KU = chunk_slots(KP * kRowThreads);
   constexpr bool kNorm = KP <= 8;
@@ -1306,8 +1323,8 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
   const int i0 = part * a.ipw;
   const int ni = min(a.ipw, gemv_items(a) - i0);
   const int NR = silu ? 2 * ni : ni;
-  float* xs = (float*)smem;   // 2 K: the (normalized) row, the norm's squares
-  float* Y = xs + 2 * K;      // kRowThreads / 16
+  float* xs = (float*)smem;   // norm scratch, then the normalized row
+  float* Y = xs + norm_scratch_floats(K);  // kRowThreads / 16
   constexpr bool kNorm = KP <= 8;  // rows wider than 4096 are never normalized (d_model <= 4096)
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
@@ -1377,7 +1394,7 @@ __device__ __forceinline__ void gemv_dense_unit(const GemvArgs& a, int unit, con
 __device__ __forceinline__ int dense_chain_stride(int K) { return K / 16 + 4; }
 
 struct DenseLds {
-  float* xs;  // [2 K] norm scratch
+  float* xs;  // [norm_scratch_floats(K)] norm scratch
   float* xT;  // [16][K / 16 + 4]
   float* Y;   // [2 ipw]
 };
@@ -1385,7 +1402,7 @@ struct DenseLds {
 __device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
   DenseLds l;
   l.xs = (float*)smem;
-  l.xT = l.xs + 2 * K;
+  l.xT = l.xs + norm_scratch_floats(K);
   l.Y = l.xT + 16 * dense_chain_stride(K);
   return l;
 }

@@ -1001,6 +1001,15 @@ int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* s
   return 0;
 }
 
+int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {
+  if (!x || !out || rows <= 0) return set_error(SVL_ERR_INVALID_INPUT, "null argument or no rows");
+  if (k < 4 || k > 4096 || k % 4) return set_error(SVL_ERR_INVALID_INPUT, "row length %d: 4 .. 4096, a multiple of 4", k);
+  if (norm != SVL_NORM_LAYER && norm != SVL_NORM_RMS) return set_error(SVL_ERR_INVALID_INPUT, "unknown norm %d", norm);
+  HIP_TRY(hipSetDevice(device));
+  HIP_TRY(launch_row_stats(x, rows, k, norm == SVL_NORM_LAYER ? NORM_LAYER : NORM_RMS, out, (hipStream_t)stream));
+  return 0;
+}
+
 int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {
   if (!cfg || !out || (!tensors && count)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   *out = nullptr;

@@ -41,7 +41,7 @@ EXPORTS = [
     "svl_state_synchronize", "svl_state_stream", "svl_transformer_forward", "svl_stt_step",
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
-    "svl_bench_copy",
+    "svl_bench_copy", "svl_bench_row_stats",
 ]
 
 
@@ -112,6 +112,7 @@ def load_library(path: str = LIB_PATH):
     L.svl_stt_recognize_async.argtypes = [vp, vp, i64, vp, vp]
     L.svl_tts_backbone_step.argtypes = [vp, vp, vp, vp]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
+    L.svl_bench_row_stats.argtypes = [C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp]
     for name in EXPORTS:
         if name not in ("svl_last_error", "svl_model_destroy", "svl_state_destroy", "svl_state_stream"):
             getattr(L, name).restype = C.c_int
@@ -127,6 +128,21 @@ def _check(rc: int) -> None:
 def _p(a: np.ndarray):
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(C.c_void_p)
+
+
+def row_stats(x: np.ndarray, norm: int, device: int = 0) -> np.ndarray:
+    """[rows, 2] = (sum of x^2, sum of x) of every row of x [rows, k] as the decode step's norm
+    prologues compute them (svl_bench_row_stats)."""
+    from . import hip
+
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    dx = hip.DeviceBuffer.from_array(x)
+    dout = hip.DeviceBuffer(rows * 2 * 4)
+    _check(load_library().svl_bench_row_stats(device, C.c_void_p(dx.address), rows, k, norm,
+                                              C.c_void_p(dout.address), None))
+    hip.synchronize()
+    return dout.to_array(np.float32, rows * 2).reshape(rows, 2)
 
 
 def device_count() -> int:

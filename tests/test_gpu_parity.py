@@ -576,3 +576,66 @@ def test_persistent_and_per_phase_launches_agree(monkeypatch):
     st = g.init_state()
     b = g.recognize(audio, st)
     assert np.array_equal(a, b)
+
+
+# ---- norm statistics on chosen rows -------------------------------------------------------------
+
+def _stat_rows(k, seed):
+    """Rows that stress an element-order sum: normal residuals, magnitudes over 40 binades, few
+    distinct dyadic values (rounding ties at every step), a large first term, sparse spikes,
+    zeros (leading, scattered, whole row), tiny values, and non-finite or huge terms."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for kind in range(12):
+        for _ in range(24 if kind < 8 else 4):
+            if kind == 0:
+                r = rng.standard_normal(k)
+            elif kind == 1:
+                r = rng.standard_normal(k) * 2.0 ** rng.integers(-20, 20, k)
+            elif kind == 2:
+                r = rng.integers(0, 7, k) * 0.25
+            elif kind == 3:
+                r = rng.standard_normal(k) * 0.01
+                r[0] = 1000.0
+            elif kind == 4:
+                r = np.where(np.arange(k) % 97 == 0, rng.standard_normal(k) * 100, rng.standard_normal(k) * 1e-3)
+            elif kind == 5:
+                r = np.where(rng.integers(0, 3, k) == 0, 0.0, rng.standard_normal(k))
+            elif kind == 6:
+                r = np.where(np.arange(k) < k // 2, 0.0, rng.standard_normal(k))
+            elif kind == 7:
+                r = rng.integers(0, 4096, k) * 2.0 ** -12
+            elif kind == 8:
+                r = np.zeros(k)
+            elif kind == 9:
+                r = rng.standard_normal(k) * 1e-30
+            elif kind == 10:
+                r = rng.standard_normal(k) * 1e25
+            else:
+                r = rng.standard_normal(k)
+                r[rng.integers(0, k)] = np.inf
+            rows.append(r)
+    return np.array(rows, dtype=np.float32)
+
+
+@pytest.mark.parametrize("k", [2048, 2560, 1024, 4096, 256, 260, 36])
+def test_norm_statistics_bit_exact_on_stress_rows(k):
+    """The step's RMSNorm / LayerNorm statistics (exact parallel sum of squares, sequential
+    LayerNorm sums) equal the oracle's element-order sums bit for bit, rows chosen to hit every
+    branch: ties, binade edges, zeros, fallbacks."""
+    x = _stat_rows(k, seed=k)
+    alpha = np.ones(k, np.float32)
+    got_rms = svl.row_stats(x, svl.NORM_RMS)
+    got_ln = svl.row_stats(x, svl.NORM_LAYER)
+    with np.errstate(over="ignore", invalid="ignore"):
+        # numpy's accumulate adds in index order with one f32 accumulator (no pairwise blocking)
+        seq2s = np.add.accumulate(x * x, axis=1, dtype=np.float32)[:, -1]
+        seq1s = np.add.accumulate(x, axis=1, dtype=np.float32)[:, -1]
+    for r in range(x.shape[0]):
+        seq2, seq1 = seq2s[r], seq1s[r]
+        for got, want in ((got_rms[r, 0], seq2), (got_ln[r, 0], seq2), (got_ln[r, 1], seq1)):
+            assert (np.isnan(got) and np.isnan(want)) or np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), (k, r, got, want)
+    # the oracle's RMSNorm from the same sums
+    y = oracle.rms_norm(x[:24], alpha, 1e-8)
+    m = np.sqrt(got_rms[:24, 0] / np.float32(k) + np.float32(1e-8), dtype=np.float32)
+    assert np.array_equal((x[:24] / m[:, None]).view(np.uint32), y.view(np.uint32))
