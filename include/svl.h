@@ -7,7 +7,12 @@
  *
  * Conventions (mirroring the crate's Rust API):
  *  - Every function returns 0 on success, a negative svl_status on error (the message is in
- *    svl_last_error(), thread-local), mirroring `Result<T, Error>` (SVL/error.rs:1-32).
+ *    svl_last_error(), thread-local), mirroring `Result<T, Error>` (SVL/error.rs:1-32), or
+ *    SVL_UNSUPPORTED (positive) when the request is valid for the reference but outside what
+ *    these kernels cover: the caller then runs the reference's own path, as the reference's
+ *    kernels return `Ok(None)` to fall back (SVL/nn/kernels/matvec.rs:12-17,
+ *    SVL/nn/kernels/attention.rs:21-23).  Nothing was created or changed in that case.
+ *  - Work enqueued by the *_async functions reports its errors at svl_state_synchronize.
  *  - svl_model is immutable after creation and may be shared by host threads, as
  *    `Stt: Send + Sync` (SVL/stt/mod.rs:159).  svl_state is per stream and used by one host
  *    thread at a time, as `&mut TransformerState` (SVL/nn/transformer.rs:139).
@@ -28,8 +33,10 @@
 extern "C" {
 #endif
 
-/* SVL/error.rs:3-30: Config, InvalidInput, Candle (tensor/device), Io. */
+/* SVL/error.rs:3-30: Config, InvalidInput, Candle (tensor/device), Io; and the kernels'
+ * `None` (fall back to the reference's path, SVL/nn/kernels/matvec.rs:12-17). */
 typedef enum {
+    SVL_UNSUPPORTED = 1,
     SVL_OK = 0,
     SVL_ERR_CONFIG = -1,
     SVL_ERR_INVALID_INPUT = -2,
@@ -119,6 +126,8 @@ int svl_state_layer_cache(const svl_state* state, int32_t stream, int32_t layer,
 int svl_state_positions(const svl_state* state, int64_t* positions /* [batch] */);
 int svl_state_reset(svl_state* state);
 void svl_state_destroy(svl_state* state);
+/* Waits for the state's stream; reports the errors of the *_async work enqueued since the last
+ * call (SVL_ERR_INVALID_INPUT for an out-of-range token id). */
 int svl_state_synchronize(svl_state* state);
 /* The state's HIP stream (hipStream_t), for callers that time or order work around it. */
 void* svl_state_stream(const svl_state* state);
@@ -148,7 +157,10 @@ int svl_stt_step_heads(const svl_model* model, svl_state* state, const uint32_t*
  * token.  audio_tokens [n_steps][batch][n_q], out_tokens [n_steps][batch].  Host pointers. */
 int svl_stt_recognize(const svl_model* model, svl_state* state, int64_t n_steps,
                       const uint32_t* audio_tokens, uint32_t* out_tokens);
-/* The same, enqueued on the state's stream; device pointers; returns without waiting. */
+/* The same, enqueued on the state's stream; device pointers; returns without waiting.  The
+ * audio token ids are checked on the device: an id past `card` raises the state's error flag
+ * (the step then reads the table's last row) and svl_state_synchronize returns
+ * SVL_ERR_INVALID_INPUT, as the synchronous call does for the same input up front. */
 int svl_stt_recognize_async(const svl_model* model, svl_state* state, int64_t n_steps,
                             const uint32_t* d_audio_tokens, uint32_t* d_out_tokens);
 /* svl_stt_recognize with the extra heads' first-class probabilities of every step

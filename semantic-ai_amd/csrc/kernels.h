@@ -51,7 +51,10 @@ struct GemvArgs {
   int ff_hidden;       // SILU: gate rows j, value rows j + ff_hidden
   // QKV_ROPE
   int* pos;            // [B] positions (read by QKV_ROPE, advanced when advance_pos)
-  const float* rope;   // [positions][hd/2][cos, sin] computed on the host
+  const float* rope;   // [rope_cap][hd/2][cos, sin] computed on the host (positions < rope_cap)
+  int rope_cap;
+  const float* rope_ovf;    // positions >= rope_cap: row p + rope_delta[b] of this call's rows
+  const int* rope_delta;    // [B]
   int H, KVH, hd;
   float* q_out;        // [B][H*hd]
   void* kc;            // [B][KVH][cap][hd]
@@ -90,6 +93,7 @@ struct EmbedArgs {
   float* x;                 // [B][d]
   void* stage;              // [B][n_q][d] table rows of the next step's audio tokens, gathered
                             // during the previous step (table element type), or null
+  uint32_t* bad_token;      // set to 1 when a token id is past its table (the id is clamped)
 };
 
 struct ArgmaxArgs {
@@ -180,6 +184,8 @@ constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8
 constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit (or 16)
 constexpr int kTileBatch = 64;   // batch rows of a GEMM unit
 constexpr int kMaxBatch = 1024;
+constexpr int kMaxRingSlots = 12000;
+constexpr size_t kStaticLdsReserve = 8192;  // static LDS of the step kernels (barrier state, positions)  // KV ring slots per stream and layer (attention keeps a head's scores in LDS)
 constexpr int kGemmChunk = 4;    // Q8_0 blocks (128 bytes of K) per LDS stage of a GEMM unit
 constexpr int kGemmStages = 6;   // LDS stages of a GEMM unit (kGemmStages - 1 chunks in flight)
 // weights [kTileRows][128] | activations [kTileBatch][128] | weight scales [kTileRows][4] (f16 in

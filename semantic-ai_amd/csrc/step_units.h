@@ -458,7 +458,8 @@ __device__ __forceinline__ EpiIn gemv_epi_prefetch(const GemvArgs& a, int b, int
     // q rows, then k rows; v rows (no rotation) read an unused but valid entry
     const int qdim = a.H * a.hd;
     const int rr = row < qdim ? row : row - qdim;
-    const v2f cs = ldg((const v2f*)(a.rope + ((size_t)p * (a.hd / 2) + (rr % a.hd) / 2) * 2));
+    const float* tab = p < a.rope_cap ? a.rope + (size_t)p * a.hd : a.rope_ovf + (size_t)(p + ldg(a.rope_delta + b)) * a.hd;
+    const v2f cs = ldg((const v2f*)(tab + (rr % a.hd) / 2 * 2));
     e.a = cs.x;
     e.b = cs.y;
   } else if (a.epi == EPI_RESID) {
@@ -1835,7 +1836,9 @@ __device__ __forceinline__ float embed_sum(const EmbedArgs& a, const uint32_t* s
 }
 
 // SVL/stt/model.rs:246-250: x = text_emb[t] + emb_0[a_0] + ... in that order, f32 adds.  Token
-// ids past the tables are clamped (the host validates its own inputs).  Units: B x d / 512.
+// ids past the tables raise the state's bad-token flag (reported as invalid input when the
+// caller synchronizes) and are clamped, so that every access stays in the tables.  Units:
+// B x d / 512.
 // The stream's tokens are staged in LDS first, then every table row is requested at once.  When
 // `staged`, the audio rows are read from the copies gathered during the previous step (random
 // table rows cost an address-translation miss each; the copies are contiguous).
@@ -1847,12 +1850,17 @@ __device__ __forceinline__ void embed_unit(const EmbedArgs& a, const uint32_t* t
   const bool initial = a.initial_at_zero && spos[b] == 0;
   if ((int)threadIdx.x <= a.n_q) {
     uint32_t t;
+    uint32_t lim;
     if (threadIdx.x == 0) {
       t = text ? ldg(text + b) : ld_co(a.fb_tok + b);
-      t = t > (uint32_t)a.text_card ? (uint32_t)a.text_card : t;
+      lim = (uint32_t)a.text_card;
     } else {
       t = initial ? (uint32_t)a.card : ldg(audio + (size_t)b * a.n_q + threadIdx.x - 1);
-      t = t > (uint32_t)a.card ? (uint32_t)a.card : t;
+      lim = (uint32_t)a.card;
+    }
+    if (t > lim) {
+      if (a.bad_token && unit % chunks == 0) st_co(a.bad_token, 1u);
+      t = lim;
     }
     stok[threadIdx.x] = t;
   }

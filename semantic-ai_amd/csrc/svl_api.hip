@@ -17,7 +17,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -84,12 +87,15 @@ struct svl_model {
   std::vector<Layer> layers;
   // RoPE cos/sin of every position below rope_len: [rope_len][head_dim / 2][2], computed on
   // the host with the C library's cosf/sinf (SVL/nn/transformer.rs:114-118, 161-172) and
-  // grown on demand.  Superseded tables stay allocated until the model is destroyed, since
-  // kernels already enqueued may still read them.
+  // grown by doubling up to rope_cap positions (65536 by default: 32 MiB at head_dim 128).
+  // Superseded tables stay allocated until the model is destroyed, since kernels already
+  // enqueued may still read them; all of them together hold fewer than 2 rope_cap rows.
+  // Positions from rope_cap on get their rows per call, in the state (prepare_rope).
   mutable std::mutex rope_mu;
   mutable float* rope = nullptr;
   mutable int64_t rope_len = 0;
   mutable std::vector<void*> rope_old;
+  int64_t rope_cap = 65536;
   // STT
   void* text_emb = nullptr;
   void* emb = nullptr;  // n_q tables back to back
@@ -146,18 +152,29 @@ struct svl_state {
   void* stage = nullptr;      // STT: next step's audio embedding rows [B][n_q][d]
   int8_t* xqb = nullptr;      // batched Q8_0 path: quantized input rows [B][width]
   float* xdqb = nullptr;      //                    and their block scales [B][width / 32]
-  uint32_t* tok_out = nullptr;
+  uint32_t* tok_out = nullptr;  // [B] tokens, then the bad-token flag (EmbedArgs::bad_token)
+  // RoPE rows of positions at or past the model table's cap, computed for each call
+  float* rope_ovf = nullptr;     // device [ovf_rows][head_dim]
+  int64_t ovf_rows = 0;
+  int* rope_delta = nullptr;     // device [B]: a stream's position p reads row p + delta
+  float* ovf_host = nullptr;     // pinned staging of the rows and deltas
+  size_t ovf_host_bytes = 0;
+  hipEvent_t ovf_copied = nullptr;  // the last staging copy has been read
   // step programs and the grid barrier of the persistent kernel
   Program stt, tts, fwd_prog;
   SyncState* sync = nullptr;
   unsigned gen = 0;
   int grid = 0;
   bool persistent = true;
+  size_t lds_budget = 0;  // dynamic LDS a step launch may request on this device
 
   ~svl_state() {
     hipSetDevice(m->device);
     if (stream) hipStreamSynchronize(stream);
     for (void* p : allocs) hipFree(p);
+    if (rope_ovf) hipFree(rope_ovf);
+    if (ovf_host) hipHostFree(ovf_host);
+    if (ovf_copied) hipEventDestroy(ovf_copied);
     if (stream) hipStreamDestroy(stream);
   }
   int alloc(void** p, size_t bytes) {
@@ -355,23 +372,36 @@ int load_table(svl_model* m, const svl_tensor* ts, size_t n, const std::string& 
   return 0;
 }
 
-// Makes the RoPE table cover positions [0, needed).  The same formula and C library as the
-// reference's f64 inv_freq / f32 angle / cos, sin (SVL/nn/transformer.rs:114-118, 161-172).
+// inv_freq[i] = exp(-ln(max_period) * 2 i / head_dim) in f64, then f32
+// (SVL/nn/transformer.rs:114-118).
+std::vector<float> rope_inv_freq(const svl_config& c) {
+  std::vector<float> inv(c.head_dim / 2);
+  for (int i = 0; i < c.head_dim / 2; ++i)
+    inv[i] = (float)std::exp(-(std::log(c.max_period)) * 2.0 * (double)i / (double)c.head_dim);
+  return inv;
+}
+
+// cos and sin of the f32 angle (f32)p * inv_freq[i] with the C library's cosf / sinf, as the
+// reference computes them (SVL/nn/transformer.rs:161-172): row p is [head_dim / 2][cos, sin].
+void rope_row(const std::vector<float>& inv, int64_t p, float* row) {
+  for (size_t i = 0; i < inv.size(); ++i) {
+    const float f = (float)p * inv[i];
+    row[2 * i] = ::cosf(f);
+    row[2 * i + 1] = ::sinf(f);
+  }
+}
+
+// Makes the model's RoPE table cover positions [0, min(needed, rope_cap)).
 int ensure_rope(const svl_model* m, int64_t needed) {
   std::lock_guard<std::mutex> lock(m->rope_mu);
+  needed = std::min(needed, m->rope_cap);
   if (needed <= m->rope_len) return 0;
-  int64_t len = m->rope_len ? m->rope_len : 4096;
-  while (len < needed) len *= 2;
-  const int half = m->cfg.head_dim / 2;
-  std::vector<float> inv(half), tab((size_t)len * half * 2);
-  for (int i = 0; i < half; ++i)
-    inv[i] = (float)std::exp(-(std::log(m->cfg.max_period)) * 2.0 * (double)i / (double)m->cfg.head_dim);
-  for (int64_t p = 0; p < len; ++p)
-    for (int i = 0; i < half; ++i) {
-      const float f = (float)p * inv[i];
-      tab[((size_t)p * half + i) * 2] = ::cosf(f);
-      tab[((size_t)p * half + i) * 2 + 1] = ::sinf(f);
-    }
+  int64_t len = m->rope_len ? m->rope_len : std::min<int64_t>(4096, m->rope_cap);
+  while (len < needed) len = std::min(2 * len, m->rope_cap);
+  const std::vector<float> inv = rope_inv_freq(m->cfg);
+  const int hd = m->cfg.head_dim;
+  std::vector<float> tab((size_t)len * hd);
+  for (int64_t p = 0; p < len; ++p) rope_row(inv, p, tab.data() + (size_t)p * hd);
   void* d;
   HIP_TRY(hipMalloc(&d, tab.size() * 4));
   hipError_t e = hipMemcpy(d, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
@@ -423,29 +453,34 @@ int load_extra_heads(svl_model* m, const svl_tensor* ts, size_t n) {
   return load_linear(m, &all, 1, "extra_heads", nh * hd, d, 0, &m->extra_heads);
 }
 
+// Configuration errors (what the reference itself rejects or cannot build) are SVL_ERR_CONFIG;
+// valid configurations outside what these kernels cover are SVL_UNSUPPORTED, for the caller to
+// run the reference's own path (the reference's kernels return None: SVL/nn/kernels/matvec.rs:12-17).
 int check_config(const svl_config* c) {
   if (c->d_model <= 0 || c->num_layers <= 0 || c->num_heads <= 0 || c->num_kv_heads <= 0 || c->head_dim <= 0)
     return set_error(SVL_ERR_CONFIG, "invalid transformer dimensions");
   if (c->num_heads % c->num_kv_heads) return set_error(SVL_ERR_CONFIG, "num_heads must be a multiple of num_kv_heads");
-  if (c->head_dim != 64 && c->head_dim != 128) return set_error(SVL_ERR_CONFIG, "head_dim must be 64 or 128");
-  if (c->d_model % 32) return set_error(SVL_ERR_CONFIG, "d_model must be a multiple of 32");
-  if (c->ff_hidden <= 0 || c->ff_hidden % 32) return set_error(SVL_ERR_CONFIG, "ff_hidden must be a positive multiple of 32");
-  if ((c->num_heads * c->head_dim) % 32) return set_error(SVL_ERR_CONFIG, "attention width must be a multiple of 32");
-  // a GEMV input row is held by 512 row-wave threads, 16 elements each (8 for normalized rows)
-  if (c->d_model > 4096) return set_error(SVL_ERR_CONFIG, "d_model must be <= 4096");
-  if (c->ff_hidden > 8192 || c->num_heads * c->head_dim > 8192)
-    return set_error(SVL_ERR_CONFIG, "ff_hidden and num_heads * head_dim must be <= 8192");
-  // attention stages one head's weights over the window in LDS
-  if (c->context > 16000) return set_error(SVL_ERR_CONFIG, "context must be <= 16000");
+  if (c->ff_hidden <= 0) return set_error(SVL_ERR_CONFIG, "ff_hidden must be positive");
   if (c->norm_kind != SVL_NORM_LAYER && c->norm_kind != SVL_NORM_RMS) return set_error(SVL_ERR_CONFIG, "unknown norm");
   if (c->ff_kind != SVL_FF_PLAIN_GELU && c->ff_kind != SVL_FF_GATED_SILU) return set_error(SVL_ERR_CONFIG, "unknown feed-forward");
   if (c->context < 0) return set_error(SVL_ERR_CONFIG, "context must be >= 0");
   if (c->kv_dtype != SVL_F32 && c->kv_dtype != SVL_BF16) return set_error(SVL_ERR_CONFIG, "kv_dtype must be F32 or BF16");
   if (c->kind == SVL_MODEL_STT && (c->n_q <= 0 || c->card <= 0 || c->text_card <= 0))
     return set_error(SVL_ERR_CONFIG, "invalid STT heads");
-  if (c->kind == SVL_MODEL_STT && c->n_q > 64) return set_error(SVL_ERR_CONFIG, "n_q must be <= 64");
   if (c->kind == SVL_MODEL_TTS && c->latent_dim <= 0) return set_error(SVL_ERR_CONFIG, "invalid TTS latent_dim");
-  if (c->kind == SVL_MODEL_TTS && c->latent_dim % 4) return set_error(SVL_ERR_CONFIG, "latent_dim must be a multiple of 4");
+  // shapes the kernels do not cover
+  if (c->head_dim != 64 && c->head_dim != 128) return set_error(SVL_UNSUPPORTED, "head_dim must be 64 or 128");
+  if (c->d_model % 32) return set_error(SVL_UNSUPPORTED, "d_model must be a multiple of 32");
+  if (c->ff_hidden % 32) return set_error(SVL_UNSUPPORTED, "ff_hidden must be a multiple of 32");
+  if ((c->num_heads * c->head_dim) % 32) return set_error(SVL_UNSUPPORTED, "attention width must be a multiple of 32");
+  // a GEMV input row is held by 512 row-wave threads, 16 elements each (8 for normalized rows)
+  if (c->d_model > 4096) return set_error(SVL_UNSUPPORTED, "d_model must be <= 4096");
+  if (c->ff_hidden > 8192 || c->num_heads * c->head_dim > 8192)
+    return set_error(SVL_UNSUPPORTED, "ff_hidden and num_heads * head_dim must be <= 8192");
+  // the ring buffer of a stream and layer (attention stages a head's scores over it in LDS)
+  if (c->context > kMaxRingSlots) return set_error(SVL_UNSUPPORTED, "context must be <= %d", kMaxRingSlots);
+  if (c->kind == SVL_MODEL_STT && c->n_q > 64) return set_error(SVL_UNSUPPORTED, "n_q must be <= 64");
+  if (c->kind == SVL_MODEL_TTS && c->latent_dim % 4) return set_error(SVL_UNSUPPORTED, "latent_dim must be a multiple of 4");
   return 0;
 }
 
@@ -584,6 +619,9 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     g.g.epi = EPI_QKV_ROPE;
     g.g.pos = s->pos;
     g.g.rope = nullptr;  // set per launch (the table grows)
+    g.g.rope_cap = (int)m->rope_cap;
+    g.g.rope_ovf = nullptr;
+    g.g.rope_delta = s->rope_delta;
     g.g.H = H;
     g.g.KVH = KVH;
     g.g.hd = hd;
@@ -614,6 +652,7 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     const char* pairs = getenv("SVL_ATTN_PAIRS");
     a.at.hpu = H % 2 == 0 && (s->B * H >= 2 * s->grid || (pairs && !strcmp(pairs, "1"))) ? 2 : 1;
     a.kind = PH_ATTN;
+    if (a.at.hpu == 2 && phase_smem(a) > s->lds_budget) a.at.hpu = 1;  // two heads' scores do not fit
     a.units = s->B * H / a.at.hpu;
     out.push_back(a);
     // out_proj + residual (layer scale if any)
@@ -668,13 +707,15 @@ int upload_program(svl_state* s, Program& p) {
   return 0;
 }
 
-// Writes the current RoPE table pointer into the program's in_proj phases (host and device
-// copies) when it changed.
+// Writes the current RoPE table pointers into the program's in_proj phases (host and device
+// copies) when they changed.
 int refresh_rope(svl_state* s, Program& p, const float* rope) {
   bool changed = false;
   for (Phase& ph : p.phases)
-    if ((ph.kind == PH_GEMV || ph.kind == PH_QGEMM) && ph.g.epi == EPI_QKV_ROPE && ph.g.rope != rope) {
+    if ((ph.kind == PH_GEMV || ph.kind == PH_QGEMM) && ph.g.epi == EPI_QKV_ROPE &&
+        (ph.g.rope != rope || ph.g.rope_ovf != s->rope_ovf)) {
       ph.g.rope = rope;
+      ph.g.rope_ovf = s->rope_ovf;
       changed = true;
     }
   if (changed)
@@ -704,6 +745,7 @@ int build_programs(const svl_model* m, svl_state* s) {
     e.e.pos = s->pos;
     e.e.x = s->x;
     e.e.stage = s->stage;
+    e.e.bad_token = s->tok_out + s->B;
     e.units = s->B * ((d + kRowThreads - 1) / kRowThreads);
     P.push_back(e);
     build_layers(m, s, P);
@@ -817,9 +859,60 @@ int build_programs(const svl_model* m, svl_state* s) {
   return 0;
 }
 
-// Validates that every stream has room for `steps` more positions and that the RoPE table
-// covers them.
-int check_room(const svl_state* s, int64_t steps) {
+// RoPE rows for the next `steps` positions of every stream: the model's table below its cap;
+// past it, this call's rows are computed into the state's overflow buffer (stream b's position
+// p at row p + delta[b]), so a long stream holds only the rows of one call.
+int prepare_rope(svl_state* s, int64_t steps, int64_t top) {
+  const svl_model* m = s->m;
+  TRY(ensure_rope(m, top));
+  if (top <= m->rope_cap) return 0;
+  const int hd = m->cfg.head_dim;
+  std::vector<int> delta(s->B, 0);
+  int64_t rows = 0;
+  for (int b = 0; b < s->B; ++b) {
+    const int64_t r0 = std::max(s->pos_host[b], m->rope_cap), r1 = s->pos_host[b] + steps;
+    delta[b] = (int)(rows - r0);
+    rows += std::max<int64_t>(0, r1 - r0);
+  }
+  if (rows > s->ovf_rows) {
+    // kernels already enqueued may read the old rows
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    if (s->rope_ovf) HIP_TRY(hipFree(s->rope_ovf));
+    s->rope_ovf = nullptr;
+    s->ovf_rows = 0;
+    int64_t cap = 64;
+    while (cap < rows) cap *= 2;
+    void* d;
+    HIP_TRY(hipMalloc(&d, (size_t)cap * hd * 4));
+    s->rope_ovf = (float*)d;
+    s->ovf_rows = cap;
+  }
+  const size_t bytes = (size_t)rows * hd * 4 + (size_t)s->B * 4;
+  if (s->ovf_copied) HIP_TRY(hipEventSynchronize(s->ovf_copied));  // the staging is free again
+  if (bytes > s->ovf_host_bytes) {
+    if (s->ovf_host) HIP_TRY(hipHostFree(s->ovf_host));
+    s->ovf_host = nullptr;
+    s->ovf_host_bytes = 0;
+    void* h;
+    HIP_TRY(hipHostMalloc(&h, 2 * bytes));
+    s->ovf_host = (float*)h;
+    s->ovf_host_bytes = 2 * bytes;
+  }
+  if (!s->ovf_copied) HIP_TRY(hipEventCreateWithFlags(&s->ovf_copied, hipEventDisableTiming));
+  const std::vector<float> inv = rope_inv_freq(m->cfg);
+  for (int b = 0; b < s->B; ++b)
+    for (int64_t p = std::max(s->pos_host[b], m->rope_cap); p < s->pos_host[b] + steps; ++p)
+      rope_row(inv, p, s->ovf_host + (size_t)(p + delta[b]) * hd);
+  memcpy(s->ovf_host + (size_t)rows * hd, delta.data(), (size_t)s->B * 4);
+  HIP_TRY(hipMemcpyAsync(s->rope_ovf, s->ovf_host, (size_t)rows * hd * 4, hipMemcpyHostToDevice, s->stream));
+  HIP_TRY(hipMemcpyAsync(s->rope_delta, s->ovf_host + (size_t)rows * hd, (size_t)s->B * 4, hipMemcpyHostToDevice,
+                         s->stream));
+  HIP_TRY(hipEventRecord(s->ovf_copied, s->stream));
+  return 0;
+}
+
+// Validates that every stream has room for `steps` more positions and prepares their RoPE rows.
+int check_room(svl_state* s, int64_t steps) {
   int64_t top = 0;
   for (int64_t p : s->pos_host) {
     if (s->m->cfg.context == 0 && p + steps > s->slots)
@@ -828,7 +921,7 @@ int check_room(const svl_state* s, int64_t steps) {
     top = std::max(top, p + steps);
   }
   if (top >= ((int64_t)1 << 31)) return set_error(SVL_ERR_INVALID_INPUT, "position beyond 2^31");
-  return ensure_rope(s->m, top);
+  return prepare_rope(s, steps, top);
 }
 
 // Attention units take the streams longest first, so that the workgroups that get a second
@@ -897,12 +990,14 @@ int check_abort(svl_state* s) {
 
 int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** out) {
   const svl_config& c = m->cfg;
-  if (batch <= 0 || batch > kMaxBatch) return set_error(SVL_ERR_INVALID_INPUT, "batch must be in [1, %d]", kMaxBatch);
+  if (batch <= 0) return set_error(SVL_ERR_INVALID_INPUT, "batch must be positive");
+  if (batch > kMaxBatch) return set_error(SVL_UNSUPPORTED, "batch must be <= %d", kMaxBatch);
   int slots = c.context > 0 ? c.context : capacity;
   if (slots <= 0) return set_error(SVL_ERR_INVALID_INPUT, "an unlimited-context model needs a positive capacity");
-  if (slots > 12000) return set_error(SVL_ERR_INVALID_INPUT, "capacity must be <= 12000");
+  if (slots > kMaxRingSlots) return set_error(SVL_UNSUPPORTED, "capacity must be <= %d", kMaxRingSlots);
   HIP_TRY(hipSetDevice(m->device));
-  svl_state* s = new svl_state();
+  std::unique_ptr<svl_state> holder(new svl_state());
+  svl_state* s = holder.get();
   s->m = m;
   s->B = batch;
   s->slots = slots;
@@ -911,11 +1006,12 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   // one launch per phase by default (kernel boundaries order the phases); SVL_STEP_LAUNCH=persistent
   // runs the steps of a call in one cooperative launch with grid barriers instead
   s->persistent = mode && !strcmp(mode, "persistent");
-  auto fail = [&](int rc) {
-    delete s;
-    return rc;
-  };
+  auto fail = [](int rc) { return rc; };  // the holder frees the state
   if (s->grid <= 0) return fail(set_error(SVL_ERR_DEVICE, "cannot query the compute unit count"));
+  int max_lds = 0;
+  if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device) != hipSuccess || max_lds <= 0)
+    return fail(set_error(SVL_ERR_DEVICE, "cannot query the LDS size"));
+  s->lds_budget = (size_t)max_lds - kStaticLdsReserve;
   if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
     return fail(set_error(SVL_ERR_DEVICE, "hipStreamCreate failed"));
   const size_t kvb = (size_t)batch * c.num_kv_heads * slots * c.head_dim * (c.kv_dtype == SVL_BF16 ? 2 : 4);
@@ -953,17 +1049,24 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
     rc = s->alloc(&p, (size_t)batch * wmax), s->xqb = (int8_t*)p;
     if (!rc) rc = s->alloc(&p, (size_t)batch * (wmax / 32) * 4), s->xdqb = (float*)p;
   }
-  if (!rc) rc = s->alloc(&p, (size_t)batch * 4), s->tok_out = (uint32_t*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)(batch + 1) * 4), s->tok_out = (uint32_t*)p;
+  if (!rc) rc = s->alloc(&p, (size_t)batch * sizeof(int)), s->rope_delta = (int*)p;
   if (!rc) rc = s->alloc(&p, sizeof(SyncState)), s->sync = (SyncState*)p;
   if (!rc && hipMemsetAsync(s->sync, 0, sizeof(SyncState), s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
   if (!rc) rc = build_programs(m, s);
   if (rc) return fail(rc);
+  for (const Program* p : {&s->stt, &s->tts, &s->fwd_prog})
+    if (p->smem > s->lds_budget)
+      return fail(set_error(SVL_UNSUPPORTED, "a step phase needs %zu bytes of LDS, more than the %zu available (window %d)",
+                            p->smem, s->lds_budget, s->slots));
   s->pos_host.assign(batch, 0);
   if (launch_fill_i32(s->pos, 0, batch, s->stream) != hipSuccess ||
+      launch_fill_i32(s->rope_delta, 0, batch, s->stream) != hipSuccess ||
+      launch_fill_u32(s->tok_out, 0u, batch + 1, s->stream) != hipSuccess ||
       launch_fill_u32(s->fb_tok, (uint32_t)std::max(c.text_card, 0), batch, s->stream) != hipSuccess ||
       hipStreamSynchronize(s->stream) != hipSuccess)
     return fail(set_error(SVL_ERR_DEVICE, "state initialisation failed"));
-  *out = s;
+  *out = holder.release();
   return 0;
 }
 
@@ -981,18 +1084,33 @@ StepParams stt_params(const svl_state* s, const uint32_t* d_audio, const uint32_
   return P;
 }
 
+// Runs an entry point's body; a C++ exception (a failed host allocation, most likely) becomes an
+// error code instead of crossing the C boundary.
+template <class F>
+int guarded(F&& f) {
+  try {
+    return f();
+  } catch (const std::bad_alloc&) {
+    return set_error(SVL_ERR_DEVICE, "host memory allocation failed");
+  } catch (const std::exception& e) {
+    return set_error(SVL_ERR_DEVICE, "internal error: %s", e.what());
+  } catch (...) {
+    return set_error(SVL_ERR_DEVICE, "internal error");
+  }
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* svl_last_error(void) { return g_error.c_str(); }
 
-int svl_device_count(int* count) {
+static int device_count_impl(int* count) {
   HIP_TRY(hipGetDeviceCount(count));
   return 0;
 }
 
-int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* stream) {
+static int bench_copy_impl(int device, const void* src, void* dst, size_t bytes, void* stream) {
   if ((bytes % 16) || ((uintptr_t)src % 16) || ((uintptr_t)dst % 16))
     return set_error(SVL_ERR_INVALID_INPUT, "copy needs 16-byte multiples and alignment");
   if (bytes && (!src || !dst)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
@@ -1001,7 +1119,7 @@ int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* s
   return 0;
 }
 
-int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {
+static int bench_row_stats_impl(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {
   if (!x || !out || rows <= 0) return set_error(SVL_ERR_INVALID_INPUT, "null argument or no rows");
   if (k < 4 || k > 4096 || k % 4) return set_error(SVL_ERR_INVALID_INPUT, "row length %d: 4 .. 4096, a multiple of 4", k);
   if (norm != SVL_NORM_LAYER && norm != SVL_NORM_RMS) return set_error(SVL_ERR_INVALID_INPUT, "unknown norm %d", norm);
@@ -1010,7 +1128,7 @@ int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, f
   return 0;
 }
 
-int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {
+static int model_create_impl(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {
   if (!cfg || !out || (!tensors && count)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   *out = nullptr;
   TRY(check_config(cfg));
@@ -1018,21 +1136,19 @@ int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t co
   HIP_TRY(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) return set_error(SVL_ERR_DEVICE, "device %d not available (%d devices)", device, ndev);
   HIP_TRY(hipSetDevice(device));
-  svl_model* m = new svl_model();
+  std::unique_ptr<svl_model> m(new svl_model());
   m->cfg = *cfg;
   m->device = device;
-  int rc = create_model(cfg, tensors, count, m);
-  if (rc) {
-    delete m;
-    return rc;
-  }
-  *out = m;
+  if (const char* cap = getenv("SVL_ROPE_TABLE_POSITIONS"))  // smaller tables exercise the per-call rows in tests
+    m->rope_cap = std::min<int64_t>(std::max<int64_t>(atoll(cap), 16), (int64_t)1 << 30);
+  TRY(create_model(cfg, tensors, count, m.get()));
+  *out = m.release();
   return 0;
 }
 
 void svl_model_destroy(svl_model* model) { delete model; }
 
-int svl_model_linear_weight(const svl_model* m, const char* name, float* f32, size_t f32_count, void* blocks,
+static int model_linear_weight_impl(const svl_model* m, const char* name, float* f32, size_t f32_count, void* blocks,
                             size_t block_bytes) {
   if (!m || !name) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   const LinearDev* L = find_linear(m, name);
@@ -1072,13 +1188,13 @@ int svl_model_linear_weight(const svl_model* m, const char* name, float* f32, si
   return 0;
 }
 
-int svl_state_create(const svl_model* model, int32_t batch, int32_t capacity, svl_state** out) {
+static int state_create_impl(const svl_model* model, int32_t batch, int32_t capacity, svl_state** out) {
   if (!model || !out) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   *out = nullptr;
   return make_state(model, batch, capacity, out);
 }
 
-int svl_state_duplicate(const svl_state* s, svl_state** out) {
+static int state_duplicate_impl(const svl_state* s, svl_state** out) {
   if (!s || !out) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   svl_state* c = nullptr;
   TRY(make_state(s->m, s->B, s->slots, &c));
@@ -1101,7 +1217,7 @@ int svl_state_duplicate(const svl_state* s, svl_state** out) {
   return 0;
 }
 
-int svl_state_load_stream(svl_state* s, int32_t stream, int64_t len, const float* const* keys,
+static int state_load_stream_impl(svl_state* s, int32_t stream, int64_t len, const float* const* keys,
                           const float* const* values) {
   if (!s || (len > 0 && (!keys || !values))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (stream < 0 || stream >= s->B) return set_error(SVL_ERR_INVALID_INPUT, "stream %d out of range", stream);
@@ -1142,7 +1258,7 @@ int svl_state_load_stream(svl_state* s, int32_t stream, int64_t len, const float
   return 0;
 }
 
-int svl_state_layer_cache(const svl_state* s, int32_t stream, int32_t layer, float* keys, float* values, int64_t* len,
+static int state_layer_cache_impl(const svl_state* s, int32_t stream, int32_t layer, float* keys, float* values, int64_t* len,
                           int64_t* first) {
   if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   const svl_config& c = s->m->cfg;
@@ -1179,17 +1295,18 @@ int svl_state_layer_cache(const svl_state* s, int32_t stream, int32_t layer, flo
   return 0;
 }
 
-int svl_state_positions(const svl_state* s, int64_t* positions) {
+static int state_positions_impl(const svl_state* s, int64_t* positions) {
   if (!s || !positions) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   for (int b = 0; b < s->B; ++b) positions[b] = s->pos_host[b];
   return 0;
 }
 
-int svl_state_reset(svl_state* s) {
+static int state_reset_impl(svl_state* s) {
   if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   HIP_TRY(hipSetDevice(s->m->device));
   HIP_TRY(launch_fill_i32(s->pos, 0, s->B, s->stream));
   HIP_TRY(launch_fill_u32(s->fb_tok, (uint32_t)std::max(s->m->cfg.text_card, 0), s->B, s->stream));
+  HIP_TRY(launch_fill_u32(s->tok_out + s->B, 0u, 1, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
   s->pos_host.assign(s->B, 0);
   return 0;
@@ -1197,16 +1314,27 @@ int svl_state_reset(svl_state* s) {
 
 void svl_state_destroy(svl_state* s) { delete s; }
 
-int svl_state_synchronize(svl_state* s) {
+static int state_synchronize_impl(svl_state* s) {
   if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   HIP_TRY(hipSetDevice(s->m->device));
   HIP_TRY(hipStreamSynchronize(s->stream));
-  return check_abort(s);
+  TRY(check_abort(s));
+  // token ids of the *_async calls are validated on the device (the host never sees them)
+  uint32_t bad = 0;
+  HIP_TRY(hipMemcpy(&bad, s->tok_out + s->B, 4, hipMemcpyDeviceToHost));
+  if (bad) {
+    HIP_TRY(launch_fill_u32(s->tok_out + s->B, 0u, 1, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return set_error(SVL_ERR_INVALID_INPUT,
+                     "an asynchronous call read a token id past its embedding table (the step used the last "
+                     "row); its outputs are not the model's");
+  }
+  return 0;
 }
 
 void* svl_state_stream(const svl_state* s) { return s ? (void*)s->stream : nullptr; }
 
-int svl_transformer_forward(const svl_model* m, svl_state* s, const float* xs, int64_t t, float* ys) {
+static int transformer_forward_impl(const svl_model* m, svl_state* s, const float* xs, int64_t t, float* ys) {
   if (!m || !s || (t > 0 && (!xs || !ys))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
   if (t < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative length");
@@ -1242,12 +1370,12 @@ int svl_transformer_forward(const svl_model* m, svl_state* s, const float* xs, i
   return check_abort(s);
 }
 
-int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
+static int stt_step_impl(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
                  uint32_t* out_tokens, float* out_logits) {
   return svl_stt_step_heads(m, s, text_tokens, audio_tokens, out_tokens, out_logits, nullptr);
 }
 
-int svl_stt_step_heads(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
+static int stt_step_heads_impl(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
                        uint32_t* out_tokens, float* out_logits, float* out_probs) {
   if (!m || !s || !text_tokens || !audio_tokens || !out_tokens) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
@@ -1283,12 +1411,12 @@ int svl_stt_step_heads(const svl_model* m, svl_state* s, const uint32_t* text_to
   return check_abort(s);
 }
 
-int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+static int stt_recognize_async_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
                             uint32_t* d_out_tokens) {
   return svl_stt_recognize_heads_async(m, s, n_steps, d_audio_tokens, d_out_tokens, nullptr);
 }
 
-int svl_stt_recognize_heads_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+static int stt_recognize_heads_async_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
                                   uint32_t* d_out_tokens, float* d_out_probs) {
   if (!m || !s || (n_steps > 0 && (!d_audio_tokens || !d_out_tokens)))
     return set_error(SVL_ERR_INVALID_INPUT, "null argument");
@@ -1303,12 +1431,12 @@ int svl_stt_recognize_heads_async(const svl_model* m, svl_state* s, int64_t n_st
                      n_steps);
 }
 
-int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+static int stt_recognize_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                       uint32_t* out_tokens) {
   return svl_stt_recognize_heads(m, s, n_steps, audio_tokens, out_tokens, nullptr);
 }
 
-int svl_stt_recognize_heads(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+static int stt_recognize_heads_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                             uint32_t* out_tokens, float* out_probs) {
   if (!m || !s || (n_steps > 0 && (!audio_tokens || !out_tokens))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
@@ -1350,7 +1478,7 @@ int svl_stt_recognize_heads(const svl_model* m, svl_state* s, int64_t n_steps, c
   return check_abort(s);
 }
 
-int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
+static int tts_backbone_step_impl(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
   if (!m || !s || !out_z) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
   const svl_config& c = m->cfg;
@@ -1369,6 +1497,97 @@ int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent,
   HIP_TRY(hipMemcpyAsync(out_z, s->z, (size_t)s->B * zd * 4, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
   return check_abort(s);
+}
+
+
+// The C entry points: no C++ exception crosses the boundary.
+int svl_device_count(int* count) {
+  return guarded([&] { return device_count_impl(count); });
+}
+
+int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* stream) {
+  return guarded([&] { return bench_copy_impl(device, src, dst, bytes, stream); });
+}
+
+int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {
+  return guarded([&] { return bench_row_stats_impl(device, x, rows, k, norm, out, stream); });
+}
+
+int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {
+  return guarded([&] { return model_create_impl(cfg, tensors, count, device, out); });
+}
+
+int svl_model_linear_weight(const svl_model* m, const char* name, float* f32, size_t f32_count, void* blocks,
+                            size_t block_bytes) {
+  return guarded([&] { return model_linear_weight_impl(m, name, f32, f32_count, blocks, block_bytes); });
+}
+
+int svl_state_create(const svl_model* model, int32_t batch, int32_t capacity, svl_state** out) {
+  return guarded([&] { return state_create_impl(model, batch, capacity, out); });
+}
+
+int svl_state_duplicate(const svl_state* s, svl_state** out) {
+  return guarded([&] { return state_duplicate_impl(s, out); });
+}
+
+int svl_state_load_stream(svl_state* s, int32_t stream, int64_t len, const float* const* keys,
+                          const float* const* values) {
+  return guarded([&] { return state_load_stream_impl(s, stream, len, keys, values); });
+}
+
+int svl_state_layer_cache(const svl_state* s, int32_t stream, int32_t layer, float* keys, float* values, int64_t* len,
+                          int64_t* first) {
+  return guarded([&] { return state_layer_cache_impl(s, stream, layer, keys, values, len, first); });
+}
+
+int svl_state_positions(const svl_state* s, int64_t* positions) {
+  return guarded([&] { return state_positions_impl(s, positions); });
+}
+
+int svl_state_reset(svl_state* s) {
+  return guarded([&] { return state_reset_impl(s); });
+}
+
+int svl_state_synchronize(svl_state* s) {
+  return guarded([&] { return state_synchronize_impl(s); });
+}
+
+int svl_transformer_forward(const svl_model* m, svl_state* s, const float* xs, int64_t t, float* ys) {
+  return guarded([&] { return transformer_forward_impl(m, s, xs, t, ys); });
+}
+
+int svl_stt_step(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
+                 uint32_t* out_tokens, float* out_logits) {
+  return guarded([&] { return stt_step_impl(m, s, text_tokens, audio_tokens, out_tokens, out_logits); });
+}
+
+int svl_stt_step_heads(const svl_model* m, svl_state* s, const uint32_t* text_tokens, const uint32_t* audio_tokens,
+                       uint32_t* out_tokens, float* out_logits, float* out_probs) {
+  return guarded([&] { return stt_step_heads_impl(m, s, text_tokens, audio_tokens, out_tokens, out_logits, out_probs); });
+}
+
+int svl_stt_recognize_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+                            uint32_t* d_out_tokens) {
+  return guarded([&] { return stt_recognize_async_impl(m, s, n_steps, d_audio_tokens, d_out_tokens); });
+}
+
+int svl_stt_recognize_heads_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+                                  uint32_t* d_out_tokens, float* d_out_probs) {
+  return guarded([&] { return stt_recognize_heads_async_impl(m, s, n_steps, d_audio_tokens, d_out_tokens, d_out_probs); });
+}
+
+int svl_stt_recognize(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                      uint32_t* out_tokens) {
+  return guarded([&] { return stt_recognize_impl(m, s, n_steps, audio_tokens, out_tokens); });
+}
+
+int svl_stt_recognize_heads(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                            uint32_t* out_tokens, float* out_probs) {
+  return guarded([&] { return stt_recognize_heads_impl(m, s, n_steps, audio_tokens, out_tokens, out_probs); });
+}
+
+int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
+  return guarded([&] { return tts_backbone_step_impl(m, s, latent, out_z); });
 }
 
 }  // extern "C"

@@ -33,6 +33,7 @@ FF_PLAIN_GELU, FF_GATED_SILU = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
 
 ERR_CONFIG, ERR_INVALID_INPUT, ERR_DEVICE, ERR_IO = -1, -2, -3, -4
+UNSUPPORTED = 1  # valid for the reference, outside these kernels: run the reference's path
 
 EXPORTS = [
     "svl_last_error", "svl_device_count", "svl_model_create", "svl_model_destroy",
@@ -49,6 +50,12 @@ class SvlError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"[{code}] {message}")
         self.code = code
+
+
+class SvlUnsupported(SvlError):
+    """The request is valid but outside what the GPU kernels cover (svl.h SVL_UNSUPPORTED): the
+    reference's kernels return None in that case and the caller runs the reference's own path
+    (SVL/nn/kernels/matvec.rs:12-17)."""
 
 
 class Config(C.Structure):
@@ -121,6 +128,8 @@ def load_library(path: str = LIB_PATH):
 
 
 def _check(rc: int) -> None:
+    if rc == UNSUPPORTED:
+        raise SvlUnsupported(rc, load_library().svl_last_error().decode())
     if rc != 0:
         raise SvlError(rc, load_library().svl_last_error().decode())
 

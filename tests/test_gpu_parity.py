@@ -639,3 +639,92 @@ def test_norm_statistics_bit_exact_on_stress_rows(k):
     y = oracle.rms_norm(x[:24], alpha, 1e-8)
     m = np.sqrt(got_rms[:24, 0] / np.float32(k) + np.float32(1e-8), dtype=np.float32)
     assert np.array_equal((x[:24] / m[:, None]).view(np.uint32), y.view(np.uint32))
+
+
+# ---- boundary: bounded RoPE storage, device-side input checks, LDS fit --------------------------
+
+def test_rope_rows_past_the_table_cap_match_oracle(monkeypatch):
+    """With the model's RoPE table capped at 64 positions every later position takes its rows from
+    the per-call computation: 150 steps through a window of 24 stay bit-exact, and a lockstep batch
+    whose streams straddle the cap equals its streams run alone."""
+    monkeypatch.setenv("SVL_ROPE_TABLE_POSITIONS", "64")
+    s = W.S1_SMALL
+    t, g, o = build(s, "q8_0", seed=51)
+    audio = W.audio_tokens(s, 150, seed=52)[0]
+    gs, os_ = g.init_state(), o.new_state()
+    text = s.text_card
+    for i in range(150):
+        a = audio[i] if i else np.full(s.n_q, s.card, np.uint32)
+        tg, lg = g.step([text], a[None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, a, want_logits=True)
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), i
+        text = to
+    got = g.recognize(audio[:, None, :], g.init_state())[:, 0]
+    assert np.array_equal(got, o.new_state().stt_greedy(audio))
+    B, n = 4, 12
+    fills = [10, 58, 63, 90]
+    batch = W.audio_tokens(s, n, seed=53, batch=B)
+    st = g.init_state(batch=B)
+    caches = []
+    for b in range(B):
+        ks, vs = W.prefill_caches(s, fills[b], seed=60 + b)
+        caches.append((ks, vs))
+        st.load_stream(b, ks, vs)
+    together = g.recognize(np.ascontiguousarray(batch.transpose(1, 0, 2)), st)
+    for b in range(B):
+        one = g.init_state()
+        one.load_stream(0, *caches[b])
+        assert np.array_equal(g.recognize(batch[b][:, None, :], one)[:, 0], together[:, b]), b
+        ob = o.state_from_layer_caches(*caches[b])
+        assert np.array_equal(ob.stt_greedy(batch[b]), together[:, b]), b
+
+
+def test_async_recognize_reports_bad_token_ids_at_synchronize():
+    """The async entry point cannot see its device token ids on the host: an id past `card`
+    raises the state's flag and svl_state_synchronize returns InvalidInput once, as the
+    synchronous call rejects the same input up front."""
+    from svl import hip
+
+    s = W.S1_SMALL
+    _, g, _ = build(s, "q8_0", seed=54)
+    audio = W.audio_tokens(s, 6, seed=55)[0][:, None, :].copy()
+    st = g.init_state()
+    d_ok = hip.DeviceBuffer.from_array(audio)
+    d_out = hip.DeviceBuffer(6 * 4)
+    g.recognize_async(6, d_ok.address, d_out.address, st)
+    st.synchronize()
+    bad = audio.copy()
+    bad[3, 0, 1] = s.card + 5
+    with pytest.raises(svl.SvlError) as e:
+        g.recognize(bad, g.init_state())
+    assert e.value.code == svl.ERR_INVALID_INPUT
+    d_bad = hip.DeviceBuffer.from_array(bad)
+    st2 = g.init_state()
+    g.recognize_async(6, d_bad.address, d_out.address, st2)
+    with pytest.raises(svl.SvlError) as e:
+        st2.synchronize()
+    assert e.value.code == svl.ERR_INVALID_INPUT
+    st2.synchronize()  # reported once
+    st2.reset()
+    g.recognize_async(6, d_ok.address, d_out.address, st2)
+    st2.synchronize()
+
+
+def test_large_capacity_batch_fits_lds_or_is_unsupported():
+    """A TTS state with 10000 slots and 32 streams: two heads' scores per attention unit would
+    exceed the LDS, so the state falls back to one head per unit and steps correctly; past the
+    ring limit the library answers "unsupported" instead of failing at launch."""
+    s = W.T1_SMALL
+    t = W.make_weights(s, "f32", seed=56)
+    g = svl.Model(s.config(0), t)
+    o = oracle.Model(s.config(0), t)
+    st = g.init_state(batch=32, capacity=10000)
+    lat = W.latents(s, 3, seed=57)
+    os_ = o.new_state()
+    for i in range(3):
+        z = g.backbone_step(np.repeat(lat[i][None], 32, axis=0), st)
+        zo = os_.tts_step(lat[i])
+        for b in (0, 31):
+            assert np.array_equal(z[b].view(np.uint32), zo.view(np.uint32)), (i, b)
+    with pytest.raises(svl.SvlUnsupported):
+        g.init_state(batch=1, capacity=20000)

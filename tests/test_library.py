@@ -41,19 +41,27 @@ def test_oracle_library_loads():
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("head_dim", 96, svl.ERR_CONFIG),
-    ("num_kv_heads", 3, svl.ERR_CONFIG),
-    ("ff_hidden", 100, svl.ERR_CONFIG),
+    ("num_kv_heads", 3, svl.ERR_CONFIG),       # heads not a multiple of the KV heads
     ("context", -1, svl.ERR_CONFIG),
     ("kv_dtype", svl.Q8_0, svl.ERR_CONFIG),
     ("n_q", 0, svl.ERR_CONFIG),
+    ("ff_hidden", 0, svl.ERR_CONFIG),
+    # valid for the reference, outside the kernels: the caller falls back to the reference
+    ("head_dim", 96, svl.UNSUPPORTED),
+    ("ff_hidden", 100, svl.UNSUPPORTED),
+    ("d_model", 8192, svl.UNSUPPORTED),
+    ("context", 20000, svl.UNSUPPORTED),
+    ("n_q", 65, svl.UNSUPPORTED),
 ])
 def test_config_errors_before_device_access(field, value, code):
+    """Errors and the positive "unsupported" status (SVL/nn/kernels/matvec.rs:12-17 returns None to
+    fall back) are decided on the host before any device call."""
     cfg = W.S1_SMALL.config(0)
     cfg[field] = value
     with pytest.raises(svl.SvlError) as e:
         svl.Model(cfg, {}, kv_dtype=cfg.get("kv_dtype", 0))
     assert e.value.code == code
+    assert isinstance(e.value, svl.SvlUnsupported) == (code == svl.UNSUPPORTED)
 
 
 def test_missing_library_fails_loudly(tmp_path):
