@@ -174,6 +174,16 @@ int svl_stt_recognize_heads_async(const svl_model* model, svl_state* state, int6
                                   const uint32_t* d_audio_tokens, uint32_t* d_out_tokens,
                                   float* d_out_probs);
 
+/* svl_stt_recognize without any allocation: no counterpart in the reference; for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The device copies of the audio and output tokens go through a
+ * library-owned scratch of 2 MiB per GPU instead of buffers allocated per call, so
+ * n_steps * batch * (n_q + 1) * 4 bytes must fit in it (SVL_ERR_INVALID_INPUT otherwise), and
+ * every position must be covered by the model's precomputed RoPE table (65536 positions).
+ * Calls on one GPU share its scratch; the library runs them one at a time.  Host pointers. */
+int svl_stt_recognize_noalloc(const svl_model* model, svl_state* state, int64_t n_steps,
+                              const uint32_t* audio_tokens, uint32_t* out_tokens);
+
 /* FlowLm::step's backbone (SVL/tts/flow_lm.rs:169-180) for every stream: latent
  * [batch][latent_dim] f32, or NULL for the learnt `bos_emb` -> z [batch][z_dim or d_model]. */
 int svl_tts_backbone_step(const svl_model* model, svl_state* state, const float* latent,

@@ -22,6 +22,7 @@
 #include <new>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/svl.h"
@@ -140,7 +141,7 @@ struct svl_state {
   int* pos = nullptr;
   std::vector<int64_t> pos_host;
   int* attn_order = nullptr;     // [B] streams by visible keys, longest first (attention units)
-  std::vector<int> order_host;
+  std::vector<int> order_host, order_tmp;
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
   float* in = nullptr;        // TTS latent staging [B][latent_dim]
@@ -401,7 +402,13 @@ int ensure_rope(const svl_model* m, int64_t needed) {
   const std::vector<float> inv = rope_inv_freq(m->cfg);
   const int hd = m->cfg.head_dim;
   std::vector<float> tab((size_t)len * hd);
-  for (int64_t p = 0; p < len; ++p) rope_row(inv, p, tab.data() + (size_t)p * hd);
+  const int nt = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<std::thread> workers;
+  for (int w = 0; w < nt; ++w)
+    workers.emplace_back([&, w] {
+      for (int64_t p = w; p < len; p += nt) rope_row(inv, p, tab.data() + (size_t)p * hd);
+    });
+  for (auto& t : workers) t.join();
   void* d;
   HIP_TRY(hipMalloc(&d, tab.size() * 4));
   hipError_t e = hipMemcpy(d, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
@@ -520,7 +527,7 @@ int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_mode
       TRY(load_linear(m, ts, n, p + "linear2.weight", d, c.ff_hidden, c.quantize, &L.ff2));
     }
   }
-  TRY(ensure_rope(m, 4096));
+  TRY(ensure_rope(m, m->rope_cap));  // the whole table up front: steps never allocate for it
   if (c.kind == SVL_MODEL_STT) {
     bool all_bf16 = true;
     const svl_tensor* te = find_tensor(ts, n, "text_emb.weight");
@@ -929,12 +936,16 @@ int check_room(svl_state* s, int64_t steps) {
 // order of the streams does not change while they step together).
 int refresh_attn_order(svl_state* s) {
   const int64_t window = s->m->cfg.context;
-  std::vector<int> order(s->B);
+  std::vector<int>& order = s->order_tmp;  // sized at creation: no allocation per call
   for (int b = 0; b < s->B; ++b) order[b] = b;
   auto visible = [&](int b) { return window > 0 ? std::min(s->pos_host[b] + 1, window) : s->pos_host[b] + 1; };
-  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return visible(x) > visible(y); });
+  // longest first, ties in stream order (an in-place sort)
+  std::sort(order.begin(), order.end(), [&](int x, int y) {
+    const int64_t vx = visible(x), vy = visible(y);
+    return vx != vy ? vx > vy : x < y;
+  });
   if (order == s->order_host) return 0;
-  s->order_host = order;
+  std::copy(order.begin(), order.end(), s->order_host.begin());
   HIP_TRY(hipMemcpyAsync(s->attn_order, s->order_host.data(), (size_t)s->B * sizeof(int), hipMemcpyHostToDevice,
                          s->stream));
   return 0;
@@ -1060,6 +1071,8 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
       return fail(set_error(SVL_UNSUPPORTED, "a step phase needs %zu bytes of LDS, more than the %zu available (window %d)",
                             p->smem, s->lds_budget, s->slots));
   s->pos_host.assign(batch, 0);
+  s->order_tmp.assign(batch, 0);
+  s->order_host.assign(batch, -1);  // differs from any order: the first run uploads it
   if (launch_fill_i32(s->pos, 0, batch, s->stream) != hipSuccess ||
       launch_fill_i32(s->rope_delta, 0, batch, s->stream) != hipSuccess ||
       launch_fill_u32(s->tok_out, 0u, batch + 1, s->stream) != hipSuccess ||
@@ -1082,6 +1095,35 @@ StepParams stt_params(const svl_state* s, const uint32_t* d_audio, const uint32_
   P.out_tok = d_out;
   P.out_stride = (size_t)s->B;
   return P;
+}
+
+}  // namespace
+
+// ---- scratch of the allocation-free entry point ----------------------------------------------
+// svl_stt_recognize_noalloc stages its audio tokens and output tokens in this array instead of
+// buffers allocated per call.  Each GPU holds its own copy until the process ends; host code
+// uses the address hipGetSymbolAddress returns for the current device, never the array's name
+// (a host-side stand-in).
+constexpr size_t kNoAllocScratchBytes = (size_t)2 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;  // calls share their device's scratch: they run one at a time
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on `device` (current), looked up on the first call there.
+int scratch_on(int device, unsigned char** out) {
+  if (device < 0 || device >= kMaxScratchDevices) return set_error(SVL_ERR_DEVICE, "device %d out of range", device);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_error(SVL_ERR_DEVICE, "no device address for the scratch array");
+    g_scratch_ptr[device] = p;
+  }
+  *out = (unsigned char*)g_scratch_ptr[device];
+  return 0;
 }
 
 // Runs an entry point's body; a C++ exception (a failed host allocation, most likely) becomes an
@@ -1478,6 +1520,42 @@ static int stt_recognize_heads_impl(const svl_model* m, svl_state* s, int64_t n_
   return check_abort(s);
 }
 
+static int stt_recognize_noalloc_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                                      uint32_t* out_tokens) {
+  if (!m || !s || (n_steps > 0 && (!audio_tokens || !out_tokens))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  const svl_config& c = m->cfg;
+  if (c.kind != SVL_MODEL_STT) return set_error(SVL_ERR_CONFIG, "not an STT model");
+  if (n_steps < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative step count");
+  if (n_steps == 0) return 0;
+  const size_t na = (size_t)n_steps * s->B * c.n_q, nt = (size_t)n_steps * s->B;
+  if ((na + nt) * 4 > kNoAllocScratchBytes)
+    return set_error(SVL_ERR_INVALID_INPUT, "%lld steps x %d streams x (%d + 1) token ids exceed the %zu-byte scratch",
+                     (long long)n_steps, s->B, c.n_q, kNoAllocScratchBytes);
+  for (size_t i = 0; i < na; ++i)
+    if (audio_tokens[i] > (uint32_t)c.card) return set_error(SVL_ERR_INVALID_INPUT, "audio token %u out of range", audio_tokens[i]);
+  int64_t top = 0;
+  for (int64_t p : s->pos_host) top = std::max(top, p + n_steps);
+  {
+    std::lock_guard<std::mutex> lock(m->rope_mu);
+    if (top > m->rope_len)
+      return set_error(SVL_ERR_INVALID_INPUT, "positions up to %lld: the RoPE table covers %lld (later rows are prepared "
+                       "per call by svl_stt_recognize)", (long long)top, (long long)m->rope_len);
+  }
+  TRY(check_room(s, n_steps));  // capacity only: the table covers every position
+  HIP_TRY(hipSetDevice(m->device));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  unsigned char* base;
+  TRY(scratch_on(m->device, &base));
+  uint32_t* da = (uint32_t*)base;
+  uint32_t* dout = da + na;
+  HIP_TRY(hipMemcpyAsync(da, audio_tokens, na * 4, hipMemcpyHostToDevice, s->stream));
+  TRY(run_program(s, s->stt, stt_params(s, da, nullptr, dout, nullptr), n_steps));
+  HIP_TRY(hipMemcpyAsync(out_tokens, dout, nt * 4, hipMemcpyDeviceToHost, s->stream));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return check_abort(s);
+}
+
 static int tts_backbone_step_impl(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
   if (!m || !s || !out_z) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
@@ -1588,6 +1666,10 @@ int svl_stt_recognize_heads(const svl_model* m, svl_state* s, int64_t n_steps, c
 
 int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
   return guarded([&] { return tts_backbone_step_impl(m, s, latent, out_z); });
+}
+int svl_stt_recognize_noalloc(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                              uint32_t* out_tokens) {
+  return guarded([&] { return stt_recognize_noalloc_impl(m, s, n_steps, audio_tokens, out_tokens); });
 }
 
 }  // extern "C"
