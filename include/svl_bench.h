@@ -25,6 +25,18 @@ int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* s
  * for numerics tests on chosen rows. */
 int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream);
 
+/* Launches phase `phase` (program order) of the state's decode-step program -- program 0 the
+ * STT step, 1 the TTS backbone step -- `reps` times back to back on the state's stream, after one
+ * untimed launch, and returns the mean time per launch from HIP events around the batch (which
+ * includes the gap between back-to-back launches).  info[6] receives the phase's kind, weight
+ * format, linear rows and input width (GEMV phases), work units and attention heads per unit.
+ * The phases recompute their outputs from the state's current contents; use a state whose
+ * contents do not matter afterwards (a duplicate). */
+typedef struct svl_model svl_model;
+typedef struct svl_state svl_state;
+int svl_bench_phase(const svl_model* model, svl_state* state, int program, int phase, int reps,
+                    float* us_per_launch, int* info);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1520,6 +1520,60 @@ static int stt_recognize_heads_impl(const svl_model* m, svl_state* s, int64_t n_
   return check_abort(s);
 }
 
+static int bench_phase_impl(const svl_model* m, svl_state* s, int program, int phase, int reps, float* us_per_launch,
+                            int* info) {
+  if (!m || !s || !us_per_launch || !info) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  Program* p = program == 0 ? &s->stt : (program == 1 ? &s->tts : nullptr);
+  if (!p || p->phases.empty()) return set_error(SVL_ERR_INVALID_INPUT, "no such program for this model");
+  if (phase < 0 || phase >= (int)p->phases.size() || reps <= 0)
+    return set_error(SVL_ERR_INVALID_INPUT, "phase %d of %zu, reps %d", phase, p->phases.size(), reps);
+  const Phase& ph = p->phases[phase];
+  info[0] = ph.kind;
+  info[1] = (ph.kind == PH_GEMV || ph.kind == PH_QUANT || ph.kind == PH_QGEMM) ? ph.g.L.fmt : -1;
+  info[2] = (ph.kind == PH_GEMV || ph.kind == PH_QUANT || ph.kind == PH_QGEMM) ? ph.g.L.out : 0;
+  info[3] = (ph.kind == PH_GEMV || ph.kind == PH_QUANT || ph.kind == PH_QGEMM) ? ph.g.L.in : 0;
+  info[4] = ph.units;
+  info[5] = ph.kind == PH_ATTN ? ph.at.hpu : 0;
+  if (ph.kind == PH_GEMV && ph.g.epi == EPI_QKV_ROPE) TRY(check_room(s, 1));
+  HIP_TRY(hipSetDevice(m->device));
+  TRY(refresh_attn_order(s));
+  const float* rope;
+  {
+    std::lock_guard<std::mutex> lock(m->rope_mu);
+    rope = m->rope;
+  }
+  TRY(refresh_rope(s, *p, rope));
+  // the embedding phase reads token ids: the state's own token staging (zeros are valid ids)
+  HIP_TRY(launch_fill_u32(s->tok_in, 0u, (size_t)s->B * (1 + std::max(m->cfg.n_q, 0)), s->stream));
+  StepParams P = stt_params(s, s->tok_in + s->B, s->tok_in, nullptr);
+  P.prog = p->dev;
+  P.nphase = (int)p->phases.size();
+  P.sync = s->sync;
+  P.pos = s->pos;
+  P.B = s->B;
+  P.n_steps = 1;
+  HIP_TRY(launch_phase(ph, P, 0, p->smem, s->stream));  // warm-up
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0));
+  hipError_t e = hipEventCreate(&e1);
+  if (e != hipSuccess) {
+    hipEventDestroy(e0);
+    HIP_TRY(e);
+  }
+  e = hipEventRecord(e0, s->stream);
+  for (int r = 0; r < reps && e == hipSuccess; ++r) e = launch_phase(ph, P, 0, p->smem, s->stream);
+  if (e == hipSuccess) e = hipEventRecord(e1, s->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  HIP_TRY(e);
+  *us_per_launch = ms * 1000.0f / (float)reps;
+  return 0;
+}
+
 static int stt_recognize_noalloc_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                                       uint32_t* out_tokens) {
   if (!m || !s || (n_steps > 0 && (!audio_tokens || !out_tokens))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
@@ -1667,6 +1721,11 @@ int svl_stt_recognize_heads(const svl_model* m, svl_state* s, int64_t n_steps, c
 int svl_tts_backbone_step(const svl_model* m, svl_state* s, const float* latent, float* out_z) {
   return guarded([&] { return tts_backbone_step_impl(m, s, latent, out_z); });
 }
+int svl_bench_phase(const svl_model* m, svl_state* s, int program, int phase, int reps, float* us_per_launch,
+                    int* info) {
+  return guarded([&] { return bench_phase_impl(m, s, program, phase, reps, us_per_launch, info); });
+}
+
 int svl_stt_recognize_noalloc(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                               uint32_t* out_tokens) {
   return guarded([&] { return stt_recognize_noalloc_impl(m, s, n_steps, audio_tokens, out_tokens); });

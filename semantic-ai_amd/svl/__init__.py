@@ -42,7 +42,7 @@ EXPORTS = [
     "svl_state_synchronize", "svl_state_stream", "svl_transformer_forward", "svl_stt_step",
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
-    "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats",
+    "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase",
 ]
 
 
@@ -119,6 +119,7 @@ def load_library(path: str = LIB_PATH):
     L.svl_stt_recognize_async.argtypes = [vp, vp, i64, vp, vp]
     L.svl_tts_backbone_step.argtypes = [vp, vp, vp, vp]
     L.svl_stt_recognize_noalloc.argtypes = [vp, vp, i64, vp, vp]
+    L.svl_bench_phase.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int)]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
     L.svl_bench_row_stats.argtypes = [C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp]
     for name in EXPORTS:
