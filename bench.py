@@ -1,34 +1,32 @@
 """Decode-step benchmark of the streaming-transformer step on one MI355X.
 
-Default workload (--workload stt1b-q8-b1): STT-1B shape (16 layers, d_model 2048, 16 heads x 128,
-gated SiLU 5632, RMSNorm, window 750, text vocabulary 8000, 32 audio codebooks) with every
-linear in candle Q8_0, bf16 embeddings, f32 KV cache, batch 1, greedy decoding from an empty
-state.  A step is one decode step: embedding gather-sum, 16 layers, output norm, text_linear,
-argmax, with the argmax fed back as the next text token on the device.  Inputs (weights, audio
-tokens) are resident in HBM before timing.
+The metric is decode steps/s at B = 1 and B = 64 on the STT-1B shape with Q8_0 linears (16 layers,
+d_model 2048, 16 heads x 128, gated SiLU 5632, RMSNorm, window 750, text vocabulary 8000, 32 audio
+codebooks; bf16 embeddings, f32 KV cache), as a fraction of the HBM roofline.  A step is one
+decode step: embedding gather-sum, 16 layers, output norm, text_linear, argmax, the argmax fed
+back as the next text token on the device.  Weights and token ids are synthetic and seeded;
+inputs are resident in HBM before timing.
 
-Other workloads (one JSON line each, same fields):
-  stt1b-q8-b64   64 lockstep streams, each ring pre-filled to a seeded fill in [1, 750], 128
-                 steps; linears run as int8 MFMA GEMMs; a step advances all 64 streams.
-  stt1b-bf16-b1  the default workload with bf16 linears (dense 16-lane-dot GEMV), 256 steps.
-  stt2.6b-q4k-b1 STT-2.6B shape (24 layers, d_model 2560, 20 heads x 128, gated SiLU 6912, window
-                 3000) with every linear in candle Q4K (activations quantized to Q8K), 256 steps.
-  tts-f32-b1     Pocket-TTS backbone (6 layers, d 1024, 16 x 64, GELU 4096, LayerNorm), f32,
-                 256 prefilled positions, 128 steps of seeded N(0, 1) latents; one call per step
-                 (the reference returns to the host every frame).
+Default run (--workload stt1b-q8): ONE JSON line whose `value` is the B = 1 rate, with
+  * the timed window placed so that its mean position is that of a 256-step greedy run from
+    position 0 (the window starts at max(0, 128 - steps / 2); with --steps 256 it starts at 0):
+    the visible keys per step, hence the bytes per step, are those of the 256-step config;
+  * `steady_state`: the same step with the ring full (750 visible keys), a long-running stream;
+  * `b64`: 64 lockstep streams, each ring pre-filled to a seeded fill in [1, 750] (MFMA GEMMs),
+    with its own roofline and CPU baseline;
+  * `roofline`: the dominant kernel of the B = 1 step -- the Q8_0 GEMV kernel instance
+    gemv_phase_kernel<1u,4> (the step's GEMVs over rows of 2048) -- priced by the algorithmic
+    bytes of its launches over their durations, each phase of the step replayed back to back
+    on the state's stream and timed with HIP events (svl_bench_phase; the time includes the gap
+    between consecutive launches); `step_roofline` prices the whole step (every launch, gaps
+    included) the same way;
+  * `cpu_baseline`: the oracle (this repository's C restatement of the reference's CPU path) on
+    4 host threads (the reference's default) over a bounded sample, with its tokens compared
+    to the GPU's, the CPU model and an all-cores figure.
+Other workloads (--workload): stt1b-bf16-b1, stt2.6b-q4k-b1, tts-f32-b1 (one line each).
 
-Prints ONE JSON line (rank 0).  `value` is decode steps/s; `roofline` prices the dominant
-kernel -- the step's phase kernels (phase_kernel; gemv_phase_kernel for the weight-streaming GEMVs;
-attn_phase_kernel for attention; batch_phase_kernel for the batched MFMA path), launched once per phase of every step (83 launches per STT-1B step, 148
-at B=64) -- against MI355X HBM bandwidth: `achieved` = algorithmic bytes per launch / average
-launch time, i.e. the algorithmic bytes of the timed steps over their HIP-event time (which
-also counts the gaps between launches); `traffic` is the HBM bytes per launch measured by
-rocprofv3 counters on a run of the same workload (profiles/; `traffic_counter_steps` says how
-many steps that run had); `cpu_baseline` is the oracle (this repository's C restatement of the
-reference's CPU path) on the host cores.
-
-`--calibrate-copy BYTES` instead runs the plain copy kernel of libsvl three times over BYTES
-(the known-size reference that scales the traffic counters) and prints one JSON line.
+`--calibrate-copy BYTES` runs libsvl's plain copy kernel over BYTES three times (the known-size
+reference that scales the traffic counters) and prints one JSON line.
 """
 import argparse
 import json
@@ -45,18 +43,24 @@ for p in (ROOT, PKG):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-WORKLOADS = ["stt1b-q8-b1", "stt1b-q8-b64", "stt1b-bf16-b1", "stt2.6b-q4k-b1", "tts-f32-b1"]
+WORKLOADS = ["stt1b-q8", "stt1b-bf16-b1", "stt2.6b-q4k-b1", "tts-f32-b1"]
+METRIC = "decode steps/s at B=1 and B=64 (STT-1B-shape, Q8_0); % of HBM roofline"
+PH_EMBED, PH_GEMV, PH_ATTN, PH_ARGMAX, PH_QUANT, PH_QGEMM = 0, 1, 2, 4, 8, 9
 
 
-def traffic_file(workload):
-    return os.path.join(ROOT, "profiles", f"phase_kernel.{workload.replace('-', '_')}.traffic.txt")
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
 
 
-def read_traffic(workload):
-    """(HBM bytes per phase_kernel launch, steps of the counter run) from the committed counter
-    summary of this workload (FETCH_SIZE + WRITE_SIZE summed over the run's dispatches, scaled
-    by the copy-kernel calibration, divided by the dispatches), or (None, None)."""
-    path = traffic_file(workload)
+def traffic_file(name):
+    return os.path.join(ROOT, "profiles", f"{name}.traffic.txt")
+
+
+def read_traffic(name):
+    """(HBM bytes per step, steps of the counter run) from a committed counter summary
+    (FETCH_SIZE + WRITE_SIZE over the run's dispatches, scaled by the copy-kernel
+    calibration), or (None, None)."""
+    path = traffic_file(name)
     if not os.path.exists(path):
         return None, None
     kv = {}
@@ -65,7 +69,7 @@ def read_traffic(workload):
             k, v = line.split(":", 1)
             kv[k.strip()] = v.strip()
     try:
-        return int(float(kv["hbm_bytes_per_launch"])), int(kv["steps"])
+        return int(float(kv["hbm_bytes_per_step"])), int(kv["steps"])
     except (KeyError, ValueError):
         return None, None
 
@@ -85,13 +89,36 @@ def step_bytes(shape, dtype, kv_bytes, visible):
     return w + float(sum(per_stream))
 
 
-def stt_phases_per_step(shape, B, dtype):
-    """Launches per STT step: embedding; per layer QKV, attention, out, FF-in, FF-out (each
-    Q8_0 linear of a batch of 16 or more streams is an activation-quantization launch and a GEMM
-    launch); text_linear (+ quantization) and argmax."""
-    batched = dtype == "q8_0" and B >= 16
-    per_layer = 5 + (4 if batched else 0)
-    return 1 + shape.num_layers * per_layer + (2 if batched else 1) + 1
+def phase_bytes(info, shape, B, visible, kv_bytes=4):
+    """Algorithmic HBM bytes of one launch of a step phase (svl_bench_phase's info): a GEMV's
+    weights (in the format held on the device) and input rows; an attention launch's visible K/V;
+    the embedding rows; the logits the argmax reads."""
+    kind, fmt, rows, k = info[0], info[1], info[2], info[3]
+    if kind in (PH_GEMV, PH_QGEMM):
+        wb = {3: k // 32 * 34, 4: k // 256 * 144, 0: 4 * k, 5: 4 * k, 1: 2 * k, 6: 2 * k}[fmt]
+        return rows * wb + B * k * 4
+    if kind == PH_QUANT:
+        return B * k * 5
+    if kind == PH_ATTN:
+        kvw = shape.num_kv_heads * shape.head_dim
+        return sum(2 * v * kvw * kv_bytes for v in visible)
+    if kind == PH_EMBED:
+        return B * (1 + shape.n_q) * shape.d_model * 2
+    if kind == PH_ARGMAX:
+        return B * shape.text_card * 4
+    return 0
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count()
 
 
 def calibrate_copy(nbytes):
@@ -134,104 +161,270 @@ def timed_launch(model, st, n, d_audio, d_out, warmup):
     return e0.elapsed_ms(e1), time.perf_counter() - t0
 
 
-def base_line(value, steps, warmup, ms_per_step, dtype, data, config):
-    return {"metric": "decode steps/s at B=1 and B=64 (STT-1B-shape, Q8_0); % of HBM roofline",
-            "value": round(value, 2), "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
-            "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": dtype, "data": data, "config": config}
+def roofline_obj(achieved_gbs, traffic=None, **extra):
+    r = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+    r.update(extra)
+    return r
 
 
-def bench_stt(args, wl, steps, warmup):
+def phase_table(model, st, shape, B, visible, program=0, reps=40):
+    """Every phase of the state's step program replayed `reps` times back to back (on a copy of
+    the state): [(index, info, us_per_launch, algorithmic bytes)]."""
+    import ctypes as C
+
+    import svl
+
+    L = svl.load_library()
+    dup = st.duplicate()
+    out = []
+    i = 0
+    while True:
+        us = C.c_float()
+        info = (C.c_int * 6)()
+        rc = L.svl_bench_phase(model.h, dup.h, program, i, reps, C.byref(us), info)
+        if rc == svl.ERR_INVALID_INPUT and i > 0:
+            break
+        svl._check(rc)
+        inf = list(info)
+        out.append((i, inf, us.value, phase_bytes(inf, shape, B, visible)))
+        i += 1
+    dup.close()
+    return out
+
+
+def kernel_roofline(table, pick, name):
+    """The roofline of one kernel instance: the algorithmic bytes of its launches in a step over
+    their replayed durations."""
+    sel = [(us, b) for _, inf, us, b in table if pick(inf)]
+    if not sel:
+        return None
+    t = sum(us for us, _ in sel)
+    b = sum(b for _, b in sel)
+    return {"kernel": name, "launches_per_step": len(sel), "algorithmic_bytes_per_launch": int(b / len(sel)),
+            "avg_launch_us": round(t / len(sel), 3), "achieved_gbs": b / (t * 1e-6) / 1e9,
+            "share_of_replayed_step": None}
+
+
+def dominant_roofline(table, B):
+    """Roofline of the kernel instance with the largest share of the step: the Q8_0 GEMV over
+    rows of 2048 (gemv_phase_kernel<1u,4>) at B = 1, the MFMA GEMM (batch_phase_kernel) at B = 64.
+    Also the shares of every kind."""
+    total = sum(us for _, _, us, _ in table)
+    groups = {
+        "gemv_phase_kernel<1u,4> (Q8_0 GEMV, input rows <= 2048)": lambda i: i[0] == PH_GEMV and i[1] == 3 and i[3] <= 2048,
+        "gemv_phase_kernel<1u,16> (Q8_0 GEMV, input rows > 4096)": lambda i: i[0] == PH_GEMV and i[1] == 3 and i[3] > 4096,
+        "gemv_phase_kernel<2u,*> (Q4K GEMV)": lambda i: i[0] == PH_GEMV and i[1] == 4,
+        "gemv_phase_kernel<4u,*> (dense GEMV)": lambda i: i[0] == PH_GEMV and i[1] in (0, 1, 5, 6),
+        "attn_phase_kernel (attention)": lambda i: i[0] == PH_ATTN,
+        "batch_phase_kernel (MFMA int8 GEMM)": lambda i: i[0] == PH_QGEMM,
+        "batch_phase_kernel (activation quantization)": lambda i: i[0] == PH_QUANT,
+        "phase_kernel (embedding, argmax, other)": lambda i: i[0] not in (PH_GEMV, PH_ATTN, PH_QGEMM, PH_QUANT),
+    }
+    shares = {}
+    best = None
+    for name, pick in groups.items():
+        r = kernel_roofline(table, pick, name)
+        if r is None:
+            continue
+        t = r["avg_launch_us"] * r["launches_per_step"]
+        r["share_of_replayed_step"] = round(t / total, 3)
+        shares[name] = r
+        if best is None or t > best[0]:
+            best = (t, r)
+    return best[1], shares
+
+
+def stt_model(shape, dtype):
+    import svl
+    from svl import workloads as W
+
+    t0 = time.perf_counter()
+    tensors = W.make_weights(shape, dtype, seed=0)
+    log(f"weights generated in {time.perf_counter() - t0:.1f} s")
+    model = svl.Model(shape.config(W.quantize_code(dtype)), tensors, kv_dtype=svl.F32)
+    return tensors, model
+
+
+def bench_b1(args, shape, dtype, tensors, model, steps, warmup, with_steady=True):
+    """B = 1 greedy decode: the timed window of `steps` steps starts at position p0, reached by
+    untimed greedy steps of the same stream."""
     import svl
     from svl import hip
     from svl import workloads as W
 
-    shape = W.S2 if wl == "stt2.6b-q4k-b1" else W.S1
-    dtype = {"stt1b-bf16-b1": "bf16", "stt2.6b-q4k-b1": "q4k"}.get(wl, "q8_0")
-    B = 64 if wl == "stt1b-q8-b64" else 1
-    t0 = time.perf_counter()
-    tensors = W.make_weights(shape, dtype, seed=0)
-    print(f"weights generated in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
-    model = svl.Model(shape.config(W.quantize_code(dtype)), tensors, kv_dtype=svl.F32)
-    audio = W.audio_tokens(shape, max(steps, args.cpu_steps), seed=1, batch=B)  # [B, n, n_q]
-    d_audio = hip.DeviceBuffer.from_array(np.ascontiguousarray(audio[:, :steps].transpose(1, 0, 2)))
-    d_out = hip.DeviceBuffer(steps * B * 4)
-    st = model.init_state(batch=B)
-    fills = [0] * B
-    if B > 1:
-        # each stream's ring pre-filled to a seeded fill in [1, window]; one seeded cache of the
-        # full window is shared, each stream taking its first `fill` positions
-        fills = [int(f) for f in np.random.default_rng(7).integers(1, shape.context + 1, size=B)]
-        ks, vs = W.prefill_caches(shape, shape.context, seed=8)
-        for b in range(B):
-            st.load_stream(b, [k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
-        del ks, vs
-        st.synchronize()
+    p0 = max(0, int(round(127.5 - (steps - 1) / 2)))
+    audio = W.audio_tokens(shape, max(p0 + steps, args.cpu_steps), seed=1)[0]  # [>= p0 + steps, n_q]
+    st = model.init_state()
+    pre = model.recognize(audio[:p0, None, :], st) if p0 else np.zeros((0, 1), np.uint32)
+    d_audio = hip.DeviceBuffer.from_array(np.ascontiguousarray(audio[p0:p0 + steps, None, :]))
+    d_out = hip.DeviceBuffer(steps * 4)
     gpu_ms, wall = timed_launch(model, st, steps, d_audio, d_out, warmup)
-    print(f"timed {steps} steps: {gpu_ms:.2f} ms", file=sys.stderr, flush=True)
-    bytes_launch = sum(step_bytes(shape, dtype, 4, [min(f + s + 1, shape.context) for f in fills])
-                       for s in range(steps))
-    achieved = bytes_launch / (gpu_ms / 1e3) / 1e9
-    name = {"stt1b-q8-b1": "stt-1b q8_0 greedy decode, batch 1, from position 0",
-            "stt1b-bf16-b1": "stt-1b bf16 greedy decode, batch 1, from position 0",
-            "stt2.6b-q4k-b1": "stt-2.6b q4k greedy decode, batch 1, from position 0",
-            "stt1b-q8-b64": "stt-1b q8_0 greedy decode, 64 lockstep streams, rings pre-filled to U[1, 750]"}[wl]
-    config = {"workload": name, "layers": shape.num_layers, "d_model": shape.d_model, "heads": shape.num_heads,
-              "head_dim": shape.head_dim, "ff_hidden": shape.ff_hidden, "window": shape.context,
-              "text_vocab": shape.text_card, "codebooks": shape.n_q, "batch": B, "kv_dtype": "f32",
-              "wall_s": round(wall, 4)}
-    if B > 1:
-        config["tokens_per_s"] = round(steps * B / (gpu_ms / 1e3), 1)
-        config["mean_fill"] = round(float(np.mean(fills)), 1)
-    dt = {"q8_0": "q8_0 (int8 x int8 -> int32 block dots, f32 scales and sums)",
-          "q4k": "q4k x q8k (4-bit x int8 -> int32 sub-block dots, f32 scales and lane sums)",
-          "bf16": "bf16 weights, f32 arithmetic (16-lane FMA dot)"}[dtype]
-    line = base_line(steps / (gpu_ms / 1e3), steps, warmup, gpu_ms / steps, dt,
-                     "synthetic (seeded N(0, 0.02) weights, uniform audio ids, greedy text feedback)", config)
-    launches = steps * stt_phases_per_step(shape, B, dtype)
-    traffic, traffic_steps = read_traffic(wl)
-    line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                        "traffic_counter_steps": traffic_steps,
-                        "kernel": "step phase kernels (phase_kernel, gemv_phase_kernel, attn_phase_kernel, batch_phase_kernel; one launch per phase of each step)",
-                        "launches": launches,
-                        "algorithmic_bytes_per_launch": int(bytes_launch / launches),
-                        "avg_launch_us": round(gpu_ms * 1e3 / launches, 3), "timed_ms": round(gpu_ms, 4)}
+    toks = np.concatenate([pre[:, 0], d_out.to_array(np.uint32, steps)])
+    log(f"B=1: {steps} steps from position {p0}: {gpu_ms:.2f} ms")
+    visible = [[min(p + 1, shape.context)] for p in range(p0, p0 + steps)]
+    sb = sum(step_bytes(shape, dtype, 4, v) for v in visible)
+    res = {"steps_per_s": steps / (gpu_ms / 1e3), "ms_per_step": gpu_ms / steps, "gpu_ms": gpu_ms, "wall": wall,
+           "p0": p0, "tokens": toks, "audio": audio, "bytes": sb}
+    # per-phase replay at the window's middle position
+    mid = model.init_state()
+    if p0 + steps // 2:
+        model.recognize(audio[: p0 + steps // 2, None, :], mid)
+    vis_mid = [min(p0 + steps // 2 + 1, shape.context)]
+    res["table"] = phase_table(model, mid, shape, 1, vis_mid)
+    mid.close()
+    if with_steady:
+        # the ring full: 750 seeded keys, then `steps` timed steps
+        ks, vs = W.prefill_caches(shape, shape.context, seed=3)
+        full = model.init_state()
+        full.load_stream(0, ks, vs)
+        del ks, vs
+        gms, _ = timed_launch(model, full, steps, d_audio, d_out, warmup)
+        vb = step_bytes(shape, dtype, 4, [shape.context])
+        res["steady"] = {"steps_per_s": round(steps / (gms / 1e3), 2), "ms_per_step": round(gms / steps, 4),
+                         "visible_keys": shape.context,
+                         "roofline_frac": round(vb * steps / (gms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+        full.close()
+    st.close()
+    return res
+
+
+def cpu_b1(args, shape, dtype, tensors, res):
+    """The oracle from position 0 through the GPU's timed window (at least 64 steps): steps/s on
+    4 threads and on all cores, tokens compared with the GPU's."""
+    import oracle
+    from svl import workloads as W
+
+    audio = res["audio"]
+    n = min(len(res["tokens"]), args.cpu_steps)  # through the GPU's timed window, bounded
+    m = oracle.Model(shape.config(W.quantize_code(dtype)), tensors)
+    model_name, nproc = cpu_info()
+    out = {}
+    for threads in (args.cpu_threads, min(16, nproc or 1)):
+        oracle.set_threads(threads)
+        m.new_state().stt_greedy(audio[:2])  # warm-up
+        t0 = time.perf_counter()
+        toks = m.new_state().stt_greedy(audio[:n])
+        out[threads] = (n / (time.perf_counter() - t0), toks)
+    value, toks = out[args.cpu_threads]
+    k = min(len(toks), len(res["tokens"]))
+    return {"value": round(value, 3), "unit": "steps/s", "cores": args.cpu_threads, "kind": "port",
+            "sample": f"{n} greedy steps of the same stream from position 0 (the GPU's timed window is steps "
+                      f"{res['p0']} .. {len(res['tokens']) - 1}; oracle, {args.cpu_threads} threads, the reference's "
+                      f"default)",
+            "tokens_match": bool(np.array_equal(toks[:k], res["tokens"][:k])), "tokens_compared": int(k),
+            "cpu_model": model_name, "nproc": nproc,
+            "all_cores": {"threads": min(16, nproc or 1), "value": round(out[min(16, nproc or 1)][0], 3)}}
+
+
+def bench_b64(args, shape, dtype, tensors, model, steps, warmup):
+    """64 lockstep streams, rings pre-filled to seeded fills in [1, window]."""
+    from svl import hip
+    from svl import workloads as W
+
+    B = 64
+    fills = [int(f) for f in np.random.default_rng(7).integers(1, shape.context + 1, size=B)]
+    ks, vs = W.prefill_caches(shape, shape.context, seed=8)
+    st = model.init_state(batch=B)
+    for b in range(B):
+        st.load_stream(b, [k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
+    st.synchronize()
+    audio = W.audio_tokens(shape, steps, seed=1, batch=B)  # [B, n, n_q]
+    d_audio = hip.DeviceBuffer.from_array(np.ascontiguousarray(audio.transpose(1, 0, 2)))
+    d_out = hip.DeviceBuffer(steps * B * 4)
+    gpu_ms, wall = timed_launch(model, st, steps, d_audio, d_out, warmup)
+    log(f"B=64: {steps} steps: {gpu_ms:.2f} ms")
+    toks = d_out.to_array(np.uint32, steps * B).reshape(steps, B)
+    sb = sum(step_bytes(shape, dtype, 4, [min(f + s + 1, shape.context) for f in fills]) for s in range(steps))
+    mid = [min(f + steps // 2 + 1, shape.context) for f in fills]
+    table = phase_table(model, st, shape, B, mid, reps=10)
+    st.close()
+    dom, shares = dominant_roofline(table, B)
+    achieved = sb / (gpu_ms / 1e3) / 1e9
+    out = {"value": round(steps / (gpu_ms / 1e3), 2), "unit": "lockstep steps/s",
+           "tokens_per_s": round(steps * B / (gpu_ms / 1e3), 1), "ms_per_step": round(gpu_ms / steps, 4),
+           "steps": steps, "warmup": warmup, "batch": B, "mean_fill": round(float(np.mean(fills)), 1),
+           "roofline": roofline_obj(dom["achieved_gbs"], kernel=dom["kernel"],
+                                    launches_per_step=dom["launches_per_step"],
+                                    algorithmic_bytes_per_launch=dom["algorithmic_bytes_per_launch"],
+                                    avg_launch_us=dom["avg_launch_us"]),
+           "step_roofline": roofline_obj(achieved, algorithmic_bytes_per_step=int(sb / steps)),
+           "kernel_shares": {k: {"share": v["share_of_replayed_step"], "avg_launch_us": v["avg_launch_us"],
+                                 "GBps": round(v["achieved_gbs"], 1)} for k, v in shares.items()}}
+    traffic, tsteps = read_traffic("stt1b_q8_b64")
+    out["step_roofline"]["traffic"] = traffic
+    out["step_roofline"]["traffic_counter_steps"] = tsteps
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_stt(args, shape, dtype, tensors, audio, fills, d_out, steps, B)
-    return line
+        out["cpu_baseline"] = cpu_b64(args, shape, dtype, tensors, fills, ks, vs, audio, toks)
+    return out
 
 
-def cpu_stt(args, shape, dtype, tensors, audio, fills, d_out, steps, B):
+def cpu_b64(args, shape, dtype, tensors, fills, ks, vs, audio, gpu_toks):
     import oracle
     from svl import workloads as W
 
     oracle.set_threads(args.cpu_threads)
     m = oracle.Model(shape.config(W.quantize_code(dtype)), tensors)
-    if B == 1:
-        n = args.cpu_steps
-        m.new_state().stt_greedy(audio[0, :2])  # warm-up
-        st = m.new_state()
-        t0 = time.perf_counter()
-        toks = st.stt_greedy(audio[0, :n])
-        dt = time.perf_counter() - t0
-        gpu_toks = d_out.to_array(np.uint32, steps)[: min(n, steps)]
-        return {"value": round(n / dt, 3), "unit": "steps/s", "cores": args.cpu_threads, "kind": "port",
-                "sample": f"{n} greedy steps of the same workload from position 0 "
-                          f"(oracle, {args.cpu_threads} threads)",
-                "tokens_match": bool(np.array_equal(gpu_toks, toks[: gpu_toks.size]))}
-    # batched: a sample of streams, two steps each at their fills, scaled to lockstep steps of B
-    ns, n = 4, 2
-    ks, vs = W.prefill_caches(shape, shape.context, seed=8)
-    t_total = 0.0
+    ns, n = 8, min(4, gpu_toks.shape[0])
+    t_total, match = 0.0, True
     for b in range(ns):
         st = m.state_from_layer_caches([k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
         t0 = time.perf_counter()
-        st.stt_greedy(audio[b, :n])
+        toks = st.stt_greedy(audio[b, :n])
         t_total += time.perf_counter() - t0
-    return {"value": round(ns * n / t_total / B, 4), "unit": "steps/s", "cores": args.cpu_threads, "kind": "port",
-            "sample": f"{ns} of the {B} streams x {n} steps each at their fills (oracle, {args.cpu_threads} "
-                      f"threads), stream-steps/s divided by {B}"}
+        match &= bool(np.array_equal(toks, gpu_toks[:n, b]))
+    return {"value": round(ns * n / t_total / 64, 4), "unit": "lockstep steps/s", "cores": args.cpu_threads,
+            "kind": "port", "tokens_match": match, "streams_compared": ns,
+            "sample": f"{ns} of the 64 streams x {n} steps each from their fills (oracle, {args.cpu_threads} "
+                      f"threads); stream-steps/s divided by 64"}
+
+
+def base_line(value, steps, warmup, ms_per_step, dtype, data, config):
+    return {"metric": METRIC, "value": round(value, 2), "unit": "steps/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": data, "config": config}
+
+
+DTYPES = {"q8_0": "q8_0 (int8 x int8 -> int32 block dots, f32 scales and sums)",
+          "q4k": "q4k x q8k (4-bit x int8 -> int32 sub-block dots, f32 scales and lane sums)",
+          "bf16": "bf16 weights, f32 arithmetic (16-lane FMA dot)"}
+DATA = "synthetic (seeded N(0, 0.02) weights, uniform audio ids, greedy text feedback)"
+
+
+def stt_config(shape, name, B, p0, steps):
+    return {"workload": name, "layers": shape.num_layers, "d_model": shape.d_model, "heads": shape.num_heads,
+            "head_dim": shape.head_dim, "ff_hidden": shape.ff_hidden, "window": shape.context,
+            "text_vocab": shape.text_card, "codebooks": shape.n_q, "batch": B, "kv_dtype": "f32",
+            "start_position": p0, "mean_visible_keys": round(
+                float(np.mean([min(p + 1, shape.context) for p in range(p0, p0 + steps)])), 1)}
+
+
+def b1_line(args, shape, dtype, tensors, model, steps, warmup, name, traffic_name):
+    res = bench_b1(args, shape, dtype, tensors, model, steps, warmup, with_steady=dtype == "q8_0")
+    cfg = stt_config(shape, name, 1, res["p0"], steps)
+    cfg["wall_s"] = round(res["wall"], 4)
+    line = base_line(res["steps_per_s"], steps, warmup, res["ms_per_step"], DTYPES[dtype], DATA, cfg)
+    dom, shares = dominant_roofline(res["table"], 1)
+    traffic, tsteps = read_traffic(traffic_name)
+    line["roofline"] = roofline_obj(dom["achieved_gbs"], kernel=dom["kernel"],
+                                    launches_per_step=dom["launches_per_step"],
+                                    algorithmic_bytes_per_launch=dom["algorithmic_bytes_per_launch"],
+                                    avg_launch_us=dom["avg_launch_us"],
+                                    timing="each phase replayed back to back on the state's stream, HIP events "
+                                           "(includes the gap between launches)")
+    achieved = res["bytes"] / (res["gpu_ms"] / 1e3) / 1e9
+    line["step_roofline"] = roofline_obj(achieved, traffic=traffic, traffic_counter_steps=tsteps,
+                                         algorithmic_bytes_per_step=int(res["bytes"] / steps),
+                                         launches_per_step=len(res["table"]),
+                                         timing="the timed launch's HIP events: every phase launch of the steps, "
+                                                "gaps included")
+    line["kernel_shares"] = {k: {"share": v["share_of_replayed_step"], "avg_launch_us": v["avg_launch_us"],
+                                 "GBps": round(v["achieved_gbs"], 1)} for k, v in shares.items()}
+    if "steady" in res:
+        line["steady_state"] = res["steady"]
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_b1(args, shape, dtype, tensors, res)
+    return line
 
 
 def bench_tts(args, steps, warmup):
@@ -255,7 +448,7 @@ def bench_tts(args, steps, warmup):
     for i in range(steps):
         model.backbone_step(lat[i][None], st)
     wall = time.perf_counter() - t0
-    print(f"timed {steps} steps: {wall * 1e3:.2f} ms (host loop)", file=sys.stderr, flush=True)
+    log(f"timed {steps} steps: {wall * 1e3:.2f} ms (host loop)")
     bytes_total = sum(step_bytes(shape, "f32", 4, [257 + s]) for s in range(steps))
     achieved = bytes_total / wall / 1e9
     config = {"workload": "pocket-tts backbone f32, batch 1, 256 prefilled positions, one call per step",
@@ -264,10 +457,8 @@ def bench_tts(args, steps, warmup):
               "timing": f"host wall clock over the {steps} synchronous calls"}
     line = base_line(steps / wall, steps, warmup, wall * 1e3 / steps, "f32",
                      "synthetic (seeded N(0, 0.02) weights, N(0, 1) latents, seeded prefilled K/V)", config)
-    line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                        "kernel": "step phase kernels (phase_kernel, gemv_phase_kernel, attn_phase_kernel, batch_phase_kernel; one launch per phase; one call = one step)",
-                        "algorithmic_bytes_per_step": int(bytes_total / steps)}
+    line["roofline"] = roofline_obj(achieved, kernel="the step's phase kernels, one call per step (host loop)",
+                                    algorithmic_bytes_per_step=int(bytes_total / steps))
     if not args.no_cpu_baseline:
         import oracle
 
@@ -290,11 +481,13 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", choices=WORKLOADS, default=WORKLOADS[0])
-    ap.add_argument("--steps", type=int, default=0, help="timed steps (default 256; 128 for b64 and tts)")
+    ap.add_argument("--steps", type=int, default=0, help="timed steps (default 256; 128 for B=64 and tts)")
     ap.add_argument("--warmup", type=int, default=-1, help="warm-up steps (default: as many as timed)")
-    ap.add_argument("--cpu-steps", type=int, default=0, help="oracle steps (default 64; 16 for q4k)")
+    ap.add_argument("--cpu-steps", type=int, default=0,
+                    help="oracle steps at B=1 (default 256 for q8_0, 128 for bf16, 32 for q4k)")
     ap.add_argument("--cpu-threads", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-b64", action="store_true", help="skip the B=64 part of the default workload")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -304,11 +497,31 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return
+    from svl import workloads as W
+
     wl = args.workload
-    args.cpu_steps = args.cpu_steps or (16 if wl == "stt2.6b-q4k-b1" else 64)
-    steps = args.steps or (128 if wl in ("stt1b-q8-b64", "tts-f32-b1") else 256)
-    warmup = steps if args.warmup < 0 else args.warmup
-    line = bench_tts(args, steps, warmup) if wl == "tts-f32-b1" else bench_stt(args, wl, steps, warmup)
+    if wl == "tts-f32-b1":
+        steps = args.steps or 128
+        line = bench_tts(args, steps, steps if args.warmup < 0 else args.warmup)
+    elif wl == "stt1b-q8":
+        args.cpu_steps = args.cpu_steps or 256
+        steps = args.steps or 256
+        warmup = steps if args.warmup < 0 else args.warmup
+        tensors, model = stt_model(W.S1, "q8_0")
+        line = b1_line(args, W.S1, "q8_0", tensors, model, steps, warmup,
+                       "stt-1b q8_0 greedy decode, batch 1", "stt1b_q8_b1")
+        if not args.no_b64:
+            s64 = args.steps or 128
+            line["b64"] = bench_b64(args, W.S1, "q8_0", tensors, model, s64, s64 if args.warmup < 0 else args.warmup)
+    else:
+        shape = W.S2 if wl == "stt2.6b-q4k-b1" else W.S1
+        dtype = "q4k" if wl == "stt2.6b-q4k-b1" else "bf16"
+        steps = args.steps or 256
+        warmup = steps if args.warmup < 0 else args.warmup
+        args.cpu_steps = args.cpu_steps or (32 if dtype == "q4k" else 128)
+        tensors, model = stt_model(shape, dtype)
+        name = f"{shape.name} {dtype} greedy decode, batch 1"
+        line = b1_line(args, shape, dtype, tensors, model, steps, warmup, name, wl.replace("-", "_"))
     print(json.dumps(line), flush=True)
 
 
