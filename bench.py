@@ -379,6 +379,43 @@ def cpu_b64(args, shape, dtype, tensors, fills, ks, vs, audio, gpu_toks):
                       f"threads); stream-steps/s divided by 64"}
 
 
+def counter_run(args, steps):
+    """One launch of `steps` steps at B = 1 from position 0 and (unless --no-b64) one at B = 64 from
+    the seeded fills, nothing else: every step-kernel dispatch of a counter run belongs to them."""
+    from svl import hip
+    from svl import workloads as W
+
+    shape = W.S1
+    _, model = stt_model(shape, "q8_0")
+    out = {"counter_run": True, "steps": steps}
+    if not args.no_b1:
+        audio = W.audio_tokens(shape, steps, seed=1)[0]
+        d_audio = hip.DeviceBuffer.from_array(np.ascontiguousarray(audio[:, None, :]))
+        d_out = hip.DeviceBuffer(steps * 4)
+        st = model.init_state()
+        model.recognize_async(steps, d_audio.address, d_out.address, st)
+        st.synchronize()
+        out["b1_algorithmic_bytes_per_step"] = sum(step_bytes(shape, "q8_0", 4, [min(p + 1, shape.context)])
+                                                   for p in range(steps)) / steps
+        st.close()
+    if not args.no_b64:
+        B = 64
+        fills = [int(f) for f in np.random.default_rng(7).integers(1, shape.context + 1, size=B)]
+        ks, vs = W.prefill_caches(shape, shape.context, seed=8)
+        st = model.init_state(batch=B)
+        for b in range(B):
+            st.load_stream(b, [k[:, :, :fills[b]] for k in ks], [v[:, :, :fills[b]] for v in vs])
+        st.synchronize()
+        audio = W.audio_tokens(shape, steps, seed=1, batch=B)
+        d_audio = hip.DeviceBuffer.from_array(np.ascontiguousarray(audio.transpose(1, 0, 2)))
+        d_out = hip.DeviceBuffer(steps * B * 4)
+        model.recognize_async(steps, d_audio.address, d_out.address, st)
+        st.synchronize()
+        out["b64_algorithmic_bytes_per_step"] = sum(
+            step_bytes(shape, "q8_0", 4, [min(f + s + 1, shape.context) for f in fills]) for s in range(steps)) / steps
+    print(json.dumps(out), flush=True)
+
+
 def base_line(value, steps, warmup, ms_per_step, dtype, data, config):
     return {"metric": METRIC, "value": round(value, 2), "unit": "steps/s", "n_gpus": 1, "steps": steps,
             "warmup": warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -488,6 +525,9 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b64", action="store_true", help="skip the B=64 part of the default workload")
+    ap.add_argument("--no-b1", action="store_true", help="counter runs: skip the B=1 launch")
+    ap.add_argument("--counter-run", action="store_true",
+                    help="one launch per batch size and nothing else (for rocprofv3 counter runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -496,6 +536,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.counter_run:
+        counter_run(args, args.steps or 16)
         return
     from svl import workloads as W
 
