@@ -57,21 +57,23 @@ def traffic_file(name):
 
 
 def read_traffic(name):
-    """(HBM bytes per step, steps of the counter run) from a committed counter summary
-    (FETCH_SIZE + WRITE_SIZE over the run's dispatches, scaled by the copy-kernel
-    calibration), or (None, None)."""
+    """The committed counter summary of a workload (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy-kernel calibration): {"hbm_bytes_per_step", "dominant_hbm_bytes_per_launch", "steps"}, or {}."""
     path = traffic_file(name)
     if not os.path.exists(path):
-        return None, None
+        return {}
     kv = {}
     for line in open(path):
         if ":" in line and not line.lstrip().startswith("#"):
             k, v = line.split(":", 1)
             kv[k.strip()] = v.strip()
-    try:
-        return int(float(kv["hbm_bytes_per_step"])), int(kv["steps"])
-    except (KeyError, ValueError):
-        return None, None
+    out = {}
+    for k in ("hbm_bytes_per_step", "dominant_hbm_bytes_per_launch", "steps"):
+        try:
+            out[k] = int(float(kv[k]))
+        except (KeyError, ValueError):
+            pass
+    return out
 
 
 def step_bytes(shape, dtype, kv_bytes, visible):
@@ -351,9 +353,10 @@ def bench_b64(args, shape, dtype, tensors, model, steps, warmup):
            "step_roofline": roofline_obj(achieved, algorithmic_bytes_per_step=int(sb / steps)),
            "kernel_shares": {k: {"share": v["share_of_replayed_step"], "avg_launch_us": v["avg_launch_us"],
                                  "GBps": round(v["achieved_gbs"], 1)} for k, v in shares.items()}}
-    traffic, tsteps = read_traffic("stt1b_q8_b64")
-    out["step_roofline"]["traffic"] = traffic
-    out["step_roofline"]["traffic_counter_steps"] = tsteps
+    tr = read_traffic("stt1b_q8_b64")
+    out["roofline"]["traffic"] = tr.get("dominant_hbm_bytes_per_launch")
+    out["step_roofline"]["traffic"] = tr.get("hbm_bytes_per_step")
+    out["step_roofline"]["traffic_counter_steps"] = tr.get("steps")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_b64(args, shape, dtype, tensors, fills, ks, vs, audio, toks)
     return out
@@ -442,8 +445,10 @@ def b1_line(args, shape, dtype, tensors, model, steps, warmup, name, traffic_nam
     cfg["wall_s"] = round(res["wall"], 4)
     line = base_line(res["steps_per_s"], steps, warmup, res["ms_per_step"], DTYPES[dtype], DATA, cfg)
     dom, shares = dominant_roofline(res["table"], 1)
-    traffic, tsteps = read_traffic(traffic_name)
-    line["roofline"] = roofline_obj(dom["achieved_gbs"], kernel=dom["kernel"],
+    tr = read_traffic(traffic_name)
+    traffic, tsteps = tr.get("hbm_bytes_per_step"), tr.get("steps")
+    line["roofline"] = roofline_obj(dom["achieved_gbs"], traffic=tr.get("dominant_hbm_bytes_per_launch"),
+                                    traffic_counter_steps=tsteps, kernel=dom["kernel"],
                                     launches_per_step=dom["launches_per_step"],
                                     algorithmic_bytes_per_launch=dom["algorithmic_bytes_per_launch"],
                                     avg_launch_us=dom["avg_launch_us"],
