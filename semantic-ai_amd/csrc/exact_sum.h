@@ -1,44 +1,35 @@
 // Element-order row sums, as candle-nn's CPU RmsNorm / LayerNorm compute their statistics: one
 // f32 accumulator, x_0, x_1, ... added in index order.  With quantized activations the greedy
 // tokens depend on the last bit of these sums, so the kernels reproduce the sequential rounding
-// exactly -- but a plain dependent chain costs ~6 cycles per element (2048 elements: 5 us).
+// exactly -- but a plain dependent chain costs ~6 cycles per element (2048 elements: 5 us, 11 us
+// when fed from LDS).
 //
-// Sum of squares (non-negative terms), exactly and mostly in parallel.  While the running sum
-// S stays in one binade [2^E, 2^(E+1)), every partial sum is a multiple of u = 2^(E-23) and
-// fl(S + t) = S + rint(t / u) u (ties aside: they round to the even multiple, which depends on
-// S).  So a chunk of terms whose partial sums stay in one binade adds the integer
-// A = sum rint(t_i / u) -- computable from the chunk alone once E is known -- and chunks combine
-// by an exact (f64) prefix sum.  The row is cut into chunks of 8; each chunk's binade is taken
-// from an approximate prefix sum, and a chunk is "special" when that guess is unsafe: the first
-// chunk, a start below 2^-100, a start or end within 2^-9 (relative) of a binade edge, or a
-// tie.  Special chunks (about 14 of 256 for a row of 2048 normal values) are added sequentially
-// in f32 from their exact start, in chunk order; every other chunk is then verified against its
-// exact start (start in binade E, start + A u below 2^(E+1), which bounds every partial sum
-// since the terms are >= 0).  Any failed check -- a guess that did not hold, an f64 sum that
-// could round, a non-finite or huge term -- falls back to the plain sequential chain, so the
-// result is the sequential sum in every case.
+// Sum of squares (non-negative terms), exactly and mostly in parallel, by the 8 row waves of a
+// workgroup.  While the running sum S stays in one binade [2^E, 2^(E+1)), every partial sum is a
+// multiple of u = 2^(E-23) and fl(S + t) = S + rint(t / u) u (ties aside: they round to the even
+// multiple, which depends on S).  So a chunk of terms whose partial sums stay in one binade adds
+// the integer A = sum rint(t_i / u) -- computable from the chunk alone once E is known -- and
+// chunks combine by an exact (f64) prefix sum.  The row is cut into chunks of 4 (one per thread
+// and slab of 2048 elements); each chunk's binade is taken from an approximate prefix sum, and a
+// chunk is "special" when that guess is unsafe: the first chunk, a start below 2^-120, a start or
+// end within 2^-9 (relative) of a binade edge, or a tie.  A chunk of zeros adds exactly 0 and is
+// never special.  Special chunks (about 17 of 512 for a row of 2048 normal values) are added
+// sequentially in f32 by one wave from their exact start, in chunk order; every other chunk is
+// then verified against its exact start (start in binade E, start + A u below 2^(E+1), which
+// bounds every partial sum since the terms are >= 0).  Any failed check -- a guess that did not
+// hold, an f64 sum that could round, a non-finite or huge term, too many specials -- falls back
+// to the plain sequential chain, so the result is the sequential sum in every case.
 #pragma once
 
 #include "device_math.h"
 
 namespace svl {
 
-constexpr int kSumChunk = 8;
-
-// Lane-segment layout of a staged row: element i of a row of K at i + 4 (i / (8 Q)), so that lane
-// j of the summing wave owns elements [8 Q j, 8 Q (j + 1)) (Q chunks of 8) contiguously, and the
-// 16-byte reads of consecutive lanes fall on distinct LDS banks.  Q is chosen per call site
-// with 512 Q >= K (K <= 64 lanes x 8 Q).
-template <int Q>
-__device__ __forceinline__ int seg_pos(int i) {
-  return i + 4 * (i / (kSumChunk * Q));
-}
-
-// LDS floats of one staged array: the padded row (it also covers the reads of the last, partial
-// segment), or the summing wave's list of special chunks (at most 64 entries of 48 bytes).
-__host__ __device__ constexpr int staged_floats(int K) { return K + 768; }
-
 typedef float sum_v4 __attribute__((ext_vector_type(4)));
+
+// LDS floats of one staged array of a row of K: the row itself (contiguous, 16-byte aligned), or
+// the summing workgroup's scratch (block-scan partials and the list of special chunks).
+__host__ __device__ constexpr int staged_floats(int K) { return K + 768; }
 
 // acc += t[i] for i = 0 .. n - 1 in order (t 16-byte aligned, LDS), reading 16 values ahead.
 __device__ __forceinline__ float ordered_sum_from(const float* t, int n, float acc) {
@@ -65,15 +56,6 @@ __device__ __forceinline__ float ordered_sum_from(const float* t, int n, float a
     for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
   }
   for (int i = n16 * 16; i < n; ++i) acc = acc + t[i];
-  return acc;
-}
-
-// The plain sequential sum of a staged row (every lane runs it on its own `arr`).
-template <int Q>
-__device__ __forceinline__ float staged_sequential_sum(const float* arr, int K) {
-  constexpr int SEG = kSumChunk * Q;
-  float acc = 0.0f;
-  for (int s = 0; s * SEG < K; ++s) acc = ordered_sum_from(arr + s * (SEG + 4), min(SEG, K - s * SEG), acc);
   return acc;
 }
 
@@ -118,11 +100,7 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
   return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
 }
 
-__device__ __forceinline__ float readlane_f32(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
-// Wave minimum / maximum of an int (lane 63 of a DPP scan holds it; broadcast from there).
+// Wave minimum of an int (lane 63 of a DPP scan holds it; broadcast from there).
 __device__ __forceinline__ int wave_min(int v) {
   v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));
   v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));
@@ -133,220 +111,257 @@ __device__ __forceinline__ int wave_min(int v) {
   return __builtin_amdgcn_readlane(v, kWave - 1);
 }
 
-__device__ __forceinline__ int wave_max(int v) { return -wave_min(-v); }
+// The LDS the block sum works in (`scratch`, staged_floats(K) floats): per-wave partials, then the
+// list of special chunks.
+struct SumPartials {
+  float approx[4][8];   // approximate chunk-sum totals per slab and wave
+  double exact[4][8];   // exact increment totals per slab and wave
+  int count[4][8];      // special chunks per slab and wave
+  int emin[8], emax[8];
+  int bad[8];
+  int fail;
+  float result;
+};
 
-// Sequential f32 sum of the staged squares `sq` (K >= 1 terms, Q chunks of 8 per lane) by one
-// full wave; every lane returns the same value.  `scratch` is LDS for the list of special chunks
-// (48 bytes each, at most 64 of them; 16-byte aligned).
-template <int Q>
-__device__ __forceinline__ float exact_sum_squares(const float* sq, int K, unsigned char* scratch) {
-  constexpr int SEG = kSumChunk * Q;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int G = (K + kSumChunk - 1) / kSumChunk;
-  // this lane's chunks g = Q lane + q, elements 8 g .. 8 g + 7 (0 past K)
-  float t[Q][kSumChunk];
-  const float* seg = sq + lane * (SEG + 4);
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int i0 = lane * SEG + q * kSumChunk;
-    sum_v4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
-    if (i0 < K) {
-      a = *(const sum_v4*)(seg + q * kSumChunk);
-      b = *(const sum_v4*)(seg + q * kSumChunk + 4);
-    }
-    t[q][0] = a.x; t[q][1] = a.y; t[q][2] = a.z; t[q][3] = a.w;
-    t[q][4] = b.x; t[q][5] = b.y; t[q][6] = b.z; t[q][7] = b.w;
-#pragma unroll
-    for (int e = 0; e < kSumChunk; ++e)
-      if (i0 + e >= K) t[q][e] = 0.0f;
-  }
-  // approximate chunk sums and starts (any order: they only pick the binade)
+struct SumEntry {       // one special chunk: its terms, Sp (the ordinary increments before it),
+  sum_v4 t;             // and, after the serial pass, the exact sum at its end
+  double sp;
+  float end;
+  float pad;
+};
+
+constexpr int kSumWaves = 8;
+constexpr int kSumThreads = kSumWaves * kWave;  // the 512 row threads
+constexpr int kSlab = 4 * kSumThreads;          // elements per slab: one chunk of 4 per thread
+
+constexpr int kSumPartialsBytes = (int)((sizeof(SumPartials) + 15) & ~(size_t)15);
+
+// Special chunks the list holds for a row of K (the serial pass has to stay short anyway).
+__host__ __device__ constexpr int sum_list_capacity(int K) {
+  return (staged_floats(K) * 4 - kSumPartialsBytes) / (int)sizeof(SumEntry) < 256
+             ? (staged_floats(K) * 4 - kSumPartialsBytes) / (int)sizeof(SumEntry)
+             : 256;
+}
+
+// Sequential f32 sum of the staged squares sq[0, K) (contiguous, 16-byte aligned, K % 4 == 0,
+// K <= 2048 U) by the kSumThreads row threads, which all call it and all get the result.
+// `sync` is the row threads' barrier.  `scratch` is LDS of staged_floats(K) floats.
+template <int U, class Sync>
+__device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K, unsigned char* scratch, Sync& sync) {
+  static_assert(U >= 1 && U <= 4, "rows of at most 8192 elements");
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int NC = K / 4;  // chunks
+  SumPartials* part = (SumPartials*)scratch;
+  SumEntry* list = (SumEntry*)(scratch + kSumPartialsBytes);
+  const int cap = sum_list_capacity(K);
+  // this thread's chunks c = tid + 512 u (slab u), elements 4 c .. 4 c + 3
+  sum_v4 t[U];
+  float c4[U];
   bool bad = false;
-  float c[Q];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    float s4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s4[e] = t[q][e] + t[q][e + 4];
-    c[q] = (s4[0] + s4[2]) + (s4[1] + s4[3]);
-#pragma unroll
-    for (int e = 0; e < kSumChunk; ++e) bad |= !(t[q][e] <= 0x1p100f);  // non-finite or huge
+  for (int u = 0; u < U; ++u) {
+    const int c = tid + kSumThreads * u;
+    t[u] = c < NC ? ((const sum_v4*)sq)[c] : sum_v4{0.0f, 0.0f, 0.0f, 0.0f};
+    c4[u] = (t[u].x + t[u].y) + (t[u].z + t[u].w);
+    bad |= !(t[u].x <= 0x1p120f) | !(t[u].y <= 0x1p120f) | !(t[u].z <= 0x1p120f) | !(t[u].w <= 0x1p120f);
   }
-  float lt = 0.0f;
+  // approximate exclusive prefix of the chunk sums (any order: it only picks the binade)
+  float wincl[U];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) lt = lt + c[q];
-  float run = wave_incl_scan(lt) - lt;  // approximate exclusive prefix
-  // classification, and for ordinary chunks the exact increment D = A u
-  unsigned spmask = 0;  // bit q: chunk q of this lane is special
-  double D[Q];
-  int E[Q];
+  for (int u = 0; u < U; ++u) {
+    wincl[u] = wave_incl_scan(c4[u]);
+    if (lane == kWave - 1) part->approx[u][wave] = wincl[u];
+  }
+  sync.sync();
+  float P[U];
+  {
+    float before_slab = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float wave_off = 0.0f, slab_total = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kSumWaves; ++w) {
+        const float v = part->approx[u][w];
+        if (w < wave) wave_off = wave_off + v;
+        slab_total = slab_total + v;
+      }
+      P[u] = before_slab + wave_off + (wincl[u] - c4[u]);
+      before_slab = before_slab + slab_total;
+    }
+  }
+  // classification; an ordinary chunk's exact increment D = A u
+  bool sp[U], zero[U];
+  double D[U];
+  int E[U];
   int emin = 1 << 20, emax = -(1 << 20);
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int g = lane * Q + q;
-    const float P = run;
-    run = run + c[q];
-    D[q] = 0.0;
-    E[q] = 0;
-    if (g >= G) continue;  // empty chunk past the row
-    bool sp = g == 0 || !(P >= 0x1p-100f);
-    const int e = exp_of(P);
+  for (int u = 0; u < U; ++u) {
+    const int c = tid + kSumThreads * u;
+    sp[u] = false;
+    zero[u] = true;  // adds exactly 0 wherever it starts
+    D[u] = 0.0;
+    E[u] = 0;
+    if (c >= NC || (c > 0 && c4[u] == 0.0f)) continue;  // past the row, or all terms 0
+    zero[u] = false;
+    bool s = c == 0 || !(P[u] >= 0x1p-120f);
+    const int e = exp_of(P[u]);
     const float lo = __builtin_ldexpf(1.0f, e), hi = __builtin_ldexpf(1.0f, e + 1);
-    sp |= P < lo * (1.0f + 0x1p-9f) || P + c[q] > hi * (1.0f - 0x1p-9f);
-    float A0 = 0.0f, A1 = 0.0f;
-    bool tie = false;
-#pragma unroll
-    for (int k = 0; k < kSumChunk; ++k) {
-      const float y = __builtin_ldexpf(t[q][k], 23 - e);
-      const float r = __builtin_rintf(y);
-      if (k & 1) A1 = A1 + r;
-      else A0 = A0 + r;
-      tie |= fabsf(y - r) == 0.5f;
-    }
-    sp |= tie;
-    if (sp) {
-      spmask |= 1u << q;
-    } else {
-      E[q] = e;
-      D[q] = __builtin_ldexp((double)(A0 + A1), e - 23);  // integers below 2^24: the f32 sum is exact
+    s |= P[u] < lo * (1.0f + 0x1p-9f) || P[u] + c4[u] > hi * (1.0f - 0x1p-9f);
+    const float y0 = __builtin_ldexpf(t[u].x, 23 - e), y1 = __builtin_ldexpf(t[u].y, 23 - e);
+    const float y2 = __builtin_ldexpf(t[u].z, 23 - e), y3 = __builtin_ldexpf(t[u].w, 23 - e);
+    const float r0 = __builtin_rintf(y0), r1 = __builtin_rintf(y1), r2 = __builtin_rintf(y2), r3 = __builtin_rintf(y3);
+    s |= fabsf(y0 - r0) == 0.5f || fabsf(y1 - r1) == 0.5f || fabsf(y2 - r2) == 0.5f || fabsf(y3 - r3) == 0.5f;
+    sp[u] = s;
+    if (!s) {
+      E[u] = e;
+      D[u] = __builtin_ldexp((double)((r0 + r1) + (r2 + r3)), e - 23);  // integers below 2^24: exact
       emin = min(emin, e);
       emax = max(emax, e);
     }
   }
-  // wave-uniform guards: huge terms, or binades too far apart for exact f64 sums
+  // exact exclusive prefix of D over chunks, special counts, guards
+  double dincl[U];
+  int cincl[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    dincl[u] = wave_incl_scan(D[u]);
+    cincl[u] = wave_incl_scan(sp[u] ? 1 : 0);
+    if (lane == kWave - 1) {
+      part->exact[u][wave] = dincl[u];
+      part->count[u][wave] = cincl[u];
+    }
+  }
   emin = wave_min(emin);
-  emax = wave_max(emax);
-  if (__any(bad) || (emax >= emin && emax - emin > 28)) return staged_sequential_sum<Q>(sq, K);
-  // exact exclusive prefix of D over chunks (specials contribute 0 here)
-  double ld = 0.0;
-#pragma unroll
-  for (int q = 0; q < Q; ++q) ld = ld + D[q];
-  const double lincl = wave_incl_scan(ld);
-  const double total_d = readlane_f64(lincl, kWave - 1);
-  double sp_run = lincl - ld;  // exact: the same multiples of 2^(emin-23)
-  double Sp[Q];
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    Sp[q] = sp_run;
-    sp_run = sp_run + D[q];
+  emax = -wave_min(-emax);
+  const bool wbad = __any(bad);
+  if (lane == 0) {
+    part->emin[wave] = emin;
+    part->emax[wave] = emax;
+    part->bad[wave] = wbad;
+    if (wave == 0) part->fail = 0;
   }
-  // the specials in chunk order (lane-major, g = Q lane + q): each owning lane writes its terms
-  // and Sp at the special's rank in an LDS list
-  const int cnt = __builtin_popcount(spmask);
-  const int cincl = wave_incl_scan(cnt);
-  const int nspecial = __builtin_amdgcn_readlane(cincl, kWave - 1);
-  const int before0 = cincl - cnt;  // specials before this lane's first chunk
-  if (nspecial > kWave) return staged_sequential_sum<Q>(sq, K);  // rows built to defeat the guesses
-  struct Entry {
-    sum_v4 a, b;
-    double sp;
-    float gap, pad;
-  };
-  Entry* list = (Entry*)scratch;  // [nspecial rounded up to 8], 48 bytes each
-  const int nlist = (nspecial + 7) & ~7;
-  {
-    int r = before0;
+  sync.sync();
+  bool anybad = false;
+  emin = 1 << 20;
+  emax = -(1 << 20);
 #pragma unroll
-    for (int q = 0; q < Q; ++q)
-      if (spmask & (1u << q)) {
-        list[r].a = sum_v4{t[q][0], t[q][1], t[q][2], t[q][3]};
-        list[r].b = sum_v4{t[q][4], t[q][5], t[q][6], t[q][7]};
-        list[r].sp = Sp[q];
-        ++r;
+  for (int w = 0; w < kSumWaves; ++w) {
+    anybad |= part->bad[w] != 0;
+    emin = min(emin, part->emin[w]);
+    emax = max(emax, part->emax[w]);
+  }
+  double Sp[U];
+  int rank[U];
+  double total_d = 0.0;
+  int nspecial = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    double doff = 0.0, dslab = 0.0;
+    int coff = 0, cslab = 0;
+#pragma unroll
+    for (int w = 0; w < kSumWaves; ++w) {
+      const double dv = part->exact[u][w];
+      const int cv = part->count[u][w];
+      if (w < wave) {
+        doff = doff + dv;
+        coff += cv;
       }
-    // zero entries up to a multiple of 8: they add +0 to a non-negative sum, which changes nothing
-    if (lane >= nspecial && lane < nlist) {
-      list[lane].a = sum_v4{0.0f, 0.0f, 0.0f, 0.0f};
-      list[lane].b = list[lane].a;
-      list[lane].sp = 0.0;
+      dslab = dslab + dv;
+      cslab += cv;
     }
+    Sp[u] = total_d + doff + (dincl[u] - D[u]);  // exact: the same multiples of 2^(emin-23)
+    rank[u] = nspecial + coff + cincl[u] - (sp[u] ? 1 : 0);
+    total_d = total_d + dslab;
+    nspecial += cslab;
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  // A special's start is the previous special's end plus the ordinary chunks between them,
-  // end_{k-1} + gap_k, gap_k = Sp_k - Sp_{k-1}.  Those chunks all lie in one binade E (an edge
-  // would have made one of them special), so gap_k is a multiple of 2^(E-23) below 2^(E+1) --
-  // an f32 -- and end_{k-1} + gap_k is an exact f32 add.  Lane k prepares gap_k; the serial pass
-  // is then nine dependent f32 adds per special, and lane k checks afterwards, in parallel, that
-  // its gap and its start were exact.
-  double my_sp = 0.0;
-  float my_gap = 0.0f;
-  bool inexact = false;
-  if (lane < nspecial) my_sp = list[lane].sp;
-  {
-    const double sp_prev = __shfl_up(my_sp, 1, kWave);
-    const double gap = lane == 0 ? my_sp : my_sp - sp_prev;  // exact: multiples of 2^(emin-23)
-    my_gap = (float)gap;
-    if (lane < nspecial) inexact = (double)my_gap != gap;
-    if (lane < nlist) list[lane].gap = lane < nspecial ? my_gap : 0.0f;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  // serial pass (uniform across the wave); terms past K and padding entries are 0 and add nothing
-  float end = 0.0f, my_end_f = 0.0f;
-  constexpr int kBatch = 8;  // entries loaded together, before the batch's additions
-  for (int k0 = 0; k0 < nlist; k0 += kBatch) {
-    sum_v4 a[kBatch], b[kBatch];
-    float gp[kBatch];
+  // Uniform across the workgroup: every thread read the same partials.  The increments are
+  // multiples of 2^(emin-23); with their total below 2^(emin+29) every partial sum of them, in
+  // any order, is exact in f64 (a checked bound: the computed total cannot undershoot a true
+  // total of 2^(emin+30) by that much).  Spread and total hold for any row that can verify.
+  const bool ok = !anybad && (K & 3) == 0 && K <= kSlab * U && nspecial >= 1 && nspecial <= cap &&
+                  !(emax >= emin && (emax - emin > 28 || !(total_d < __builtin_ldexp(1.0, emin + 29))));
+  if (ok) {
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      a[i] = list[k0 + i].a;
-      b[i] = list[k0 + i].b;
-      gp[i] = list[k0 + i].gap;
-    }
+    for (int u = 0; u < U; ++u)
+      if (sp[u]) {
+        list[rank[u]].t = t[u];
+        list[rank[u]].sp = Sp[u];
+      }
+  }
+  sync.sync();
+  if (ok && wave == 0) {
+    // serial pass: a special's start is the previous special's end plus the ordinary chunks
+    // between them, end_{k-1} + gap_k, gap_k = Sp_k - Sp_{k-1}.  Those chunks all lie in one binade
+    // E (an edge would have made one of them special), so gap_k is a multiple of 2^(E-23) below
+    // 2^(E+1) -- an f32 -- and end_{k-1} + gap_k is an exact f32 add: the chain is five dependent
+    // f32 adds per special.  The exactness of each start is checked afterwards, in parallel.
+    float end = 0.0f;
+    double prev = 0.0;
+    constexpr int kBatch = 8;
+    for (int k0 = 0; k0 < nspecial; k0 += kBatch) {
+      sum_v4 tv[kBatch];
+      float gp[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      float s = end + gp[i];
-      s = s + a[i].x;
-      s = s + a[i].y;
-      s = s + a[i].z;
-      s = s + a[i].w;
-      s = s + b[i].x;
-      s = s + b[i].y;
-      s = s + b[i].z;
-      s = s + b[i].w;
-      my_end_f = lane == k0 + i ? s : my_end_f;
-      end = s;
-    }
-  }
-  // lane k: was end_{k-1} + gap_k exact?  The f64 sum is exact when end_{k-1}'s lowest bit is
-  // >= 2^(emax-51) (the gap is nonzero only right after an ordinary chunk, below 2^(emax+1)).
-  const double my_end = (double)my_end_f;
-  {
-    const float e_prev = __shfl_up(my_end_f, 1, kWave);
-    const float pe = lane == 0 ? 0.0f : e_prev;
-    const float start = pe + my_gap;
-    if (lane < nspecial) {
-      if (my_gap != 0.0f && pe != 0.0f && !(pe >= 0x1p-126f && exp_of(pe) >= emax - 28)) inexact = true;
-      inexact |= (double)start != (double)pe + (double)my_gap;
-    }
-  }
-  inexact = __any(inexact);
-  // verify every ordinary chunk against its exact start: the last special's end plus the
-  // ordinary chunks since (chunk 0 is always special, so an ordinary chunk has before >= 1).
-  // The shuffles run on every lane (a lane-exchange from an inactive lane reads 0).
-  bool fail = inexact;
-  int before = before0;
+      for (int i = 0; i < kBatch; ++i) {
+        const int k = min(k0 + i, nspecial - 1);
+        tv[i] = list[k].t;
+        const double spk = list[k].sp;
+        gp[i] = (float)(spk - prev);
+        prev = k0 + i < nspecial ? spk : prev;
+      }
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int src = max(before - 1, 0);
-    const double e_k = __shfl(my_end, src, kWave), sp_k = __shfl(my_sp, src, kWave);
-    const bool spq = (spmask >> q) & 1u;
-    if (!spq && lane * Q + q < G) {
-      // exact whenever the start can pass (e_k below 2^(E+1))
-      const double st = e_k + (Sp[q] - sp_k);
-      const double lo = __builtin_ldexp(1.0, E[q]), hi = __builtin_ldexp(1.0, E[q] + 1);
-      fail |= !(st >= lo && st < hi && st + D[q] < hi);
+      for (int i = 0; i < kBatch; ++i) {
+        if (k0 + i < nspecial) {  // uniform
+          float s = end + gp[i];
+          s = s + tv[i].x;
+          s = s + tv[i].y;
+          s = s + tv[i].z;
+          s = s + tv[i].w;
+          if (lane == 0) list[k0 + i].end = s;
+          end = s;
+        }
+      }
     }
-    before += spq ? 1 : 0;
   }
-  if (__any(fail)) return staged_sequential_sum<Q>(sq, K);
-  const double S = readlane_f64(my_end, nspecial - 1) + (total_d - readlane_f64(my_sp, nspecial - 1));
-  const float out = (float)S;
-  if ((double)out != S) return staged_sequential_sum<Q>(sq, K);
-  return out;
+  sync.sync_long();
+  bool fail = !ok;
+  if (ok) {
+    // each special's start was an exact f32 add (the f64 sum is exact when the previous end's lowest
+    // bit is >= 2^(emax-51); the gap is nonzero only right after an ordinary chunk, below 2^(emax+1))
+    for (int k = tid; k < nspecial; k += kSumThreads) {
+      const double spk = list[k].sp, spp = k ? list[k - 1].sp : 0.0;
+      const float pe = k ? list[k - 1].end : 0.0f;
+      const double gap = spk - spp;
+      const float gapf = (float)gap;
+      if (gap != 0.0 && pe != 0.0f && !(pe >= 0x1p-126f && exp_of(pe) >= emax - 28)) fail = true;
+      fail |= (double)gapf != gap || (double)(pe + gapf) != (double)pe + gap;
+    }
+    // every ordinary chunk against its exact start: the last special's end plus the ordinary
+    // chunks since (chunk 0 is always special, so rank >= 1); exact whenever it can pass
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (sp[u] || zero[u]) continue;
+      const SumEntry& last = list[rank[u] - 1];
+      const double st = (double)last.end + (Sp[u] - last.sp);
+      const double lo = __builtin_ldexp(1.0, E[u]), hi = __builtin_ldexp(1.0, E[u] + 1);
+      fail |= !(st >= lo && st < hi && st + D[u] < hi);
+    }
+    if (__any(fail) && lane == 0) part->fail = 1;
+  }
+  sync.sync();
+  if (ok && !part->fail) {
+    const SumEntry& last = list[nspecial - 1];
+    const double S = (double)last.end + (total_d - last.sp);
+    const float out = (float)S;
+    if ((double)out == S) return out;  // uniform: every thread computed the same S
+  }
+  // fallback: the plain sequential chain by wave 0, published through the scratch
+  if (wave == 0) {
+    const float acc = ordered_sum_from(sq, K, 0.0f);
+    if (lane == 0) part->result = acc;
+  }
+  sync.sync_long();
+  return part->result;
 }
 
 }  // namespace svl

@@ -198,60 +198,29 @@ __device__ __forceinline__ void store_row(const float (&v)[KP], int K, float* xs
   }
 }
 
-// acc = 0; acc += t[i] for i = 0 .. n-1 in order, reading t (16-byte aligned, in LDS) 16 values
-// ahead of the additions.
-__device__ __forceinline__ float ordered_sum(const float* t, int n) {
-  typedef float v4f_t __attribute__((ext_vector_type(4)));
-  const v4f_t* t4 = (const v4f_t*)t;
-  const int n16 = n / 16;
-  float acc = 0.0f;
-  v4f_t cur[4], nxt[4];
-  if (n16 > 0) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) cur[u] = t4[u];
-  }
-  for (int c = 0; c < n16; ++c) {
-    if (c + 1 < n16) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) nxt[u] = t4[(c + 1) * 4 + u];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      acc = acc + cur[u].x;
-      acc = acc + cur[u].y;
-      acc = acc + cur[u].z;
-      acc = acc + cur[u].w;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
-  }
-  for (int i = n16 * 16; i < n; ++i) acc = acc + t[i];
-  return acc;
-}
+static_assert(kSumThreads == kRowThreads, "the row waves sum the norm statistics");
 
 // Row statistics in element order, as candle-nn's CPU RmsNorm / LayerNorm compute them: one f32
-// accumulator per sum, x_0, x_1, ... added in index order.  The row is staged in LDS in the
-// lane-segment layout of exact_sum.h (Q chunks of 8 per lane): xs[0, staged_floats(K)) the values
-// (LayerNorm only; RMSNorm uses that space as the summing wave's scratch) and
-// xs[staged_floats(K), ...) the squares fl(x_i * x_i).  Row wave 0 sums and publishes; the other
-// row waves sleep at the barrier meanwhile.  RMSNorm's sum of squares takes the exact parallel
-// path of exact_sum.h; LayerNorm runs the two sequential chains in one instruction stream (lane 0
-// over the squares, lane 1 over the values).  s2 = sum of squares, s = sum of values (LayerNorm).
+// accumulator per sum, x_0, x_1, ... added in index order.  The row is staged in LDS contiguously:
+// xs[0, staged_floats(K)) the values (LayerNorm only; RMSNorm uses that space as the summing
+// scratch) and xs[staged_floats(K), ...) the squares fl(x_i * x_i).  RMSNorm's sum of squares
+// takes the exact parallel path of exact_sum.h over all row waves; LayerNorm runs the two
+// sequential chains in one instruction stream (lane 0 over the squares, lane 1 over the values)
+// while the other row waves sleep at the barrier.  s2 = sum of squares, s = sum of values
+// (LayerNorm).  U = slabs of 2048 elements (K <= 2048 U).
 __host__ __device__ constexpr int norm_scratch_floats(int K) { return 2 * staged_floats(K); }
 
-template <int Q>
+template <int U>
 __device__ __forceinline__ void element_stats(float* xs, int K, int norm, RowSync& rs, float& s, float& s2) {
   rs.sync();  // the row is staged
-  if (threadIdx.x < kWave) {
-    const float* sq = xs + staged_floats(K);
-    if (norm == NORM_RMS) {
-      const float acc = exact_sum_squares<Q>(sq, K, (unsigned char*)xs);
-      if (threadIdx.x == 0) rs.ws->stats[0] = acc;
-    } else {
-      const float acc = staged_sequential_sum<Q>(threadIdx.x == 1 ? xs : sq, K);
-      if (threadIdx.x < 2) rs.ws->stats[threadIdx.x] = acc;
-    }
+  const float* sq = xs + staged_floats(K);
+  if (norm == NORM_RMS) {
+    s2 = block_exact_sum_squares<U>(sq, K, (unsigned char*)xs, rs);
+    s = 0.0f;
+    if (threadIdx.x == 0) rs.ws->stats[0] = s2;
+    return;
   }
+  if (threadIdx.x < 2) rs.ws->stats[threadIdx.x] = ordered_sum_from(threadIdx.x == 1 ? xs : sq, K, 0.0f);
   rs.sync_long();
   s2 = rs.ws->stats[0];
   s = rs.ws->stats[1];
@@ -277,19 +246,18 @@ __device__ __forceinline__ void load_norm_weights(int norm, const float* nw, con
 template <int KP>
 __device__ __forceinline__ void norm_regs(float (&v)[KP], int K, int norm, const NormW<KP>& nw, float eps, float* xs,
                                           RowSync& rs) {
-  constexpr int Q = KP;  // K <= 512 KP
+  constexpr int U = (KP + 3) / 4;  // K <= 512 KP
   float* sq = xs + staged_floats(K);
 #pragma unroll
   for (int u = 0; u < KP; ++u) {
     const int i = threadIdx.x + u * kRowThreads;
     if (i < K) {
-      const int p = seg_pos<Q>(i);
-      if (norm == NORM_LAYER) xs[p] = v[u];
-      sq[p] = v[u] * v[u];
+      if (norm == NORM_LAYER) xs[i] = v[u];
+      sq[i] = v[u] * v[u];
     }
   }
   float s, s2;
-  element_stats<Q>(xs, K, norm, rs, s, s2);
+  element_stats<U>(xs, K, norm, rs, s, s2);
   float s0, s1 = 0.0f;
   if (norm == NORM_RMS) {
     s0 = sqrtf(s2 / (float)K + eps);
@@ -368,20 +336,18 @@ __device__ __forceinline__ void load_norm_weights4(int norm, const float* nw, co
 template <int KU>
 __device__ __forceinline__ void norm_row4(v4f (&v)[KU], int K, int norm, const NormW4<KU>& nw, float eps, float* xs,
                                           RowSync& rs) {
-  constexpr int Q = 4 * KU;  // K <= 2048 KU
-  const int nc = K / 4;
+  const int nc = K / 4;  // K <= 2048 KU
   float* sq = xs + staged_floats(K);
 #pragma unroll
   for (int u = 0; u < KU; ++u) {
     const int c = threadIdx.x + u * kRowThreads;
     if (c < nc) {
-      const int p = seg_pos<Q>(4 * c);  // a multiple of 4: the chunk stays in one segment
-      if (norm == NORM_LAYER) *(v4f*)(xs + p) = v[u];
-      *(v4f*)(sq + p) = v[u] * v[u];
+      if (norm == NORM_LAYER) *(v4f*)(xs + 4 * c) = v[u];
+      *(v4f*)(sq + 4 * c) = v[u] * v[u];
     }
   }
   float s, s2;
-  element_stats<Q>(xs, K, norm, rs, s, s2);
+  element_stats<KU>(xs, K, norm, rs, s, s2);
   if (norm == NORM_RMS) {
     const float s0 = sqrtf(s2 / (float)K + eps);
 #pragma unroll
@@ -1729,7 +1695,7 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   for (int hh = 0; hh < HPU; ++hh)
     for (int j = threadIdx.x; j < L; j += kRowThreads) w[hh * wstride + j] = ref_exp(w[hh * wstride + j] - mxh[hh]);
   rs.sync();
-  if (lane == 0 && wave < HPU) slot[wave] = ordered_sum(w + wave * wstride, L);
+  if (lane == 0 && wave < HPU) slot[wave] = ordered_sum_from(w + wave * wstride, L, 0.0f);
   rs.sync();
 #pragma unroll
   for (int hh = 0; hh < HPU; ++hh) {
