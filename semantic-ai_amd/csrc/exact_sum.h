@@ -114,17 +114,16 @@ __device__ __forceinline__ int wave_min(int v) {
 // The LDS the block sum works in (`scratch`, staged_floats(K) floats): per-wave partials, then the
 // list of special chunks.
 struct SumPartials {
-  float approx[4][8];   // approximate chunk-sum totals per slab and wave
-  double exact[4][8];   // exact increment totals per slab and wave
-  int count[4][8];      // special chunks per slab and wave
-  int emin[8], emax[8];
-  int bad[8];
+  float approx[4][8];  // approximate chunk-sum totals per slab and wave
+  double exact[4][8];  // exact increment totals per slab and wave
+  int count[4][8];     // special chunks per slab and wave
+  int bad[4][8];       // non-finite or huge terms per slab and wave
   int fail;
   float result;
 };
 
-struct SumEntry {       // one special chunk: its terms, Sp (the ordinary increments before it),
-  sum_v4 t;             // and, after the serial pass, the exact sum at its end
+struct SumEntry {  // one special chunk: its terms, Sp (the ordinary increments before it),
+  sum_v4 t;        // and, after the serial pass, the exact sum at its end
   double sp;
   float end;
   float pad;
@@ -133,7 +132,6 @@ struct SumEntry {       // one special chunk: its terms, Sp (the ordinary increm
 constexpr int kSumWaves = 8;
 constexpr int kSumThreads = kSumWaves * kWave;  // the 512 row threads
 constexpr int kSlab = 4 * kSumThreads;          // elements per slab: one chunk of 4 per thread
-
 constexpr int kSumPartialsBytes = (int)((sizeof(SumPartials) + 15) & ~(size_t)15);
 
 // Special chunks the list holds for a row of K (the serial pass has to stay short anyway).
@@ -143,9 +141,30 @@ __host__ __device__ constexpr int sum_list_capacity(int K) {
              : 256;
 }
 
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ double shfl_up1_f64(double v) {  // lane l gets lane l - 1's value (lane 0: its own)
+  const long long b = __builtin_bit_cast(long long, v);
+  const int src = (int)((threadIdx.x & (kWave - 1)) == 0 ? threadIdx.x & (kWave - 1) : (threadIdx.x & (kWave - 1)) - 1) * 4;
+  const int lo = __builtin_amdgcn_ds_bpermute(src, (int)b), hi = __builtin_amdgcn_ds_bpermute(src, (int)(b >> 32));
+  return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+__device__ __forceinline__ float shfl_up1_f32(float v) {
+  const int l = threadIdx.x & (kWave - 1);
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((l == 0 ? 0 : l - 1) * 4, __float_as_int(v)));
+}
+
 // Sequential f32 sum of the staged squares sq[0, K) (contiguous, 16-byte aligned, K % 4 == 0,
 // K <= 2048 U) by the kSumThreads row threads, which all call it and all get the result.
 // `sync` is the row threads' barrier.  `scratch` is LDS of staged_floats(K) floats.
+//
+// Binade guards without reductions: every ordinary chunk's binade E lies in [Ea - 26, Ea + 1],
+// Ea = the binade of the approximate row total (known to every thread after the first barrier),
+// so the increments are multiples of 2^(Ea-49); with their total below 2^(Ea+3) (checked), every
+// partial sum of them, in any order, is exact in f64.
 template <int U, class Sync>
 __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K, unsigned char* scratch, Sync& sync) {
   static_assert(U >= 1 && U <= 4, "rows of at most 8192 elements");
@@ -154,7 +173,7 @@ __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K,
   SumPartials* part = (SumPartials*)scratch;
   SumEntry* list = (SumEntry*)(scratch + kSumPartialsBytes);
   const int cap = sum_list_capacity(K);
-  // this thread's chunks c = tid + 512 u (slab u), elements 4 c .. 4 c + 3
+  // ---- this thread's chunks c = tid + 512 u (slab u), elements 4 c .. 4 c + 3
   sum_v4 t[U];
   float c4[U];
   bool bad = false;
@@ -165,46 +184,45 @@ __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K,
     c4[u] = (t[u].x + t[u].y) + (t[u].z + t[u].w);
     bad |= !(t[u].x <= 0x1p120f) | !(t[u].y <= 0x1p120f) | !(t[u].z <= 0x1p120f) | !(t[u].w <= 0x1p120f);
   }
-  // approximate exclusive prefix of the chunk sums (any order: it only picks the binade)
+  // ---- approximate exclusive prefix of the chunk sums (any order: it only picks the binade)
   float wincl[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     wincl[u] = wave_incl_scan(c4[u]);
     if (lane == kWave - 1) part->approx[u][wave] = wincl[u];
   }
+  if (tid == 0) part->fail = 0;
   sync.sync();
   float P[U];
-  {
-    float before_slab = 0.0f;
+  float ptotal = 0.0f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float wave_off = 0.0f, slab_total = 0.0f;
+  for (int u = 0; u < U; ++u) {
+    float wave_off = 0.0f, slab_total = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kSumWaves; ++w) {
-        const float v = part->approx[u][w];
-        if (w < wave) wave_off = wave_off + v;
-        slab_total = slab_total + v;
-      }
-      P[u] = before_slab + wave_off + (wincl[u] - c4[u]);
-      before_slab = before_slab + slab_total;
+    for (int w = 0; w < kSumWaves; ++w) {
+      const float v = part->approx[u][w];
+      if (w < wave) wave_off = wave_off + v;
+      slab_total = slab_total + v;
     }
+    P[u] = ptotal + wave_off + (wincl[u] - c4[u]);
+    ptotal = ptotal + slab_total;
   }
-  // classification; an ordinary chunk's exact increment D = A u
-  bool sp[U], zero[U];
+  const int ea = ptotal >= 0x1p-120f ? exp_of(ptotal) : -1000;
+  // ---- classification; an ordinary chunk's exact increment D = A 2^(E-23)
+  bool sp[U], live[U];
   double D[U];
   int E[U];
-  int emin = 1 << 20, emax = -(1 << 20);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int c = tid + kSumThreads * u;
     sp[u] = false;
-    zero[u] = true;  // adds exactly 0 wherever it starts
+    live[u] = false;  // a chunk past the row or of zeros adds exactly 0 wherever it starts
     D[u] = 0.0;
     E[u] = 0;
-    if (c >= NC || (c > 0 && c4[u] == 0.0f)) continue;  // past the row, or all terms 0
-    zero[u] = false;
-    bool s = c == 0 || !(P[u] >= 0x1p-120f);
+    if (c >= NC || (c > 0 && c4[u] == 0.0f)) continue;
+    live[u] = true;
     const int e = exp_of(P[u]);
+    bool s = c == 0 || !(P[u] >= 0x1p-120f) || e < ea - 26 || e > ea + 1;
     const float lo = __builtin_ldexpf(1.0f, e), hi = __builtin_ldexpf(1.0f, e + 1);
     s |= P[u] < lo * (1.0f + 0x1p-9f) || P[u] + c4[u] > hi * (1.0f - 0x1p-9f);
     const float y0 = __builtin_ldexpf(t[u].x, 23 - e), y1 = __builtin_ldexpf(t[u].y, 23 - e);
@@ -215,45 +233,32 @@ __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K,
     if (!s) {
       E[u] = e;
       D[u] = __builtin_ldexp((double)((r0 + r1) + (r2 + r3)), e - 23);  // integers below 2^24: exact
-      emin = min(emin, e);
-      emax = max(emax, e);
     }
   }
-  // exact exclusive prefix of D over chunks, special counts, guards
+  // ---- exact prefix of D within the wave; specials ranked by ballot
   double dincl[U];
-  int cincl[U];
+  int wrank[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     dincl[u] = wave_incl_scan(D[u]);
-    cincl[u] = wave_incl_scan(sp[u] ? 1 : 0);
-    if (lane == kWave - 1) {
-      part->exact[u][wave] = dincl[u];
-      part->count[u][wave] = cincl[u];
-    }
+    const unsigned long long m = __ballot(sp[u]);
+    wrank[u] = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+    if (lane == kWave - 1) part->exact[u][wave] = dincl[u];
+    if (lane == 0) part->count[u][wave] = __popcll(m);
   }
-  emin = wave_min(emin);
-  emax = -wave_min(-emax);
-  const bool wbad = __any(bad);
-  if (lane == 0) {
-    part->emin[wave] = emin;
-    part->emax[wave] = emax;
-    part->bad[wave] = wbad;
-    if (wave == 0) part->fail = 0;
+  {
+    const unsigned long long mb = __ballot(bad);
+    if (lane == 0) part->bad[0][wave] = mb != 0ull;
   }
   sync.sync();
-  bool anybad = false;
-  emin = 1 << 20;
-  emax = -(1 << 20);
-#pragma unroll
-  for (int w = 0; w < kSumWaves; ++w) {
-    anybad |= part->bad[w] != 0;
-    emin = min(emin, part->emin[w]);
-    emax = max(emax, part->emax[w]);
-  }
+  // ---- global exact prefix Sp, rank, totals (every thread reads the same partials)
   double Sp[U];
   int rank[U];
   double total_d = 0.0;
   int nspecial = 0;
+  bool anybad = false;
+#pragma unroll
+  for (int w = 0; w < kSumWaves; ++w) anybad |= part->bad[0][w] != 0;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     double doff = 0.0, dslab = 0.0;
@@ -269,17 +274,13 @@ __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K,
       dslab = dslab + dv;
       cslab += cv;
     }
-    Sp[u] = total_d + doff + (dincl[u] - D[u]);  // exact: the same multiples of 2^(emin-23)
-    rank[u] = nspecial + coff + cincl[u] - (sp[u] ? 1 : 0);
+    Sp[u] = total_d + doff + (dincl[u] - D[u]);
+    rank[u] = nspecial + coff + wrank[u];
     total_d = total_d + dslab;
     nspecial += cslab;
   }
-  // Uniform across the workgroup: every thread read the same partials.  The increments are
-  // multiples of 2^(emin-23); with their total below 2^(emin+29) every partial sum of them, in
-  // any order, is exact in f64 (a checked bound: the computed total cannot undershoot a true
-  // total of 2^(emin+30) by that much).  Spread and total hold for any row that can verify.
   const bool ok = !anybad && (K & 3) == 0 && K <= kSlab * U && nspecial >= 1 && nspecial <= cap &&
-                  !(emax >= emin && (emax - emin > 28 || !(total_d < __builtin_ldexp(1.0, emin + 29))));
+                  total_d < __builtin_ldexp(1.0, ea + 3);
   if (ok) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -289,58 +290,60 @@ __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K,
       }
   }
   sync.sync();
+  bool fail = !ok;
   if (ok && wave == 0) {
-    // serial pass: a special's start is the previous special's end plus the ordinary chunks
-    // between them, end_{k-1} + gap_k, gap_k = Sp_k - Sp_{k-1}.  Those chunks all lie in one binade
-    // E (an edge would have made one of them special), so gap_k is a multiple of 2^(E-23) below
-    // 2^(E+1) -- an f32 -- and end_{k-1} + gap_k is an exact f32 add: the chain is five dependent
-    // f32 adds per special.  The exactness of each start is checked afterwards, in parallel.
+    // ---- serial pass: a special's start is the previous special's end plus the ordinary chunks
+    // between them, end_{k-1} + gap_k, gap_k = Sp_k - Sp_{k-1}.  Those chunks lie in one binade
+    // (an edge would have made one of them special), so gap_k is a multiple of its ulp below
+    // 2^(E+1) -- an f32 -- and end_{k-1} + gap_k is an exact f32 add (checked below).  Lane j
+    // holds special base + j; the chain reads the operands with readlane (lanes past the list
+    // hold zeros: adding +0 leaves the sum unchanged).
     float end = 0.0f;
-    double prev = 0.0;
-    constexpr int kBatch = 8;
-    for (int k0 = 0; k0 < nspecial; k0 += kBatch) {
-      sum_v4 tv[kBatch];
-      float gp[kBatch];
+    double carry_sp = 0.0;
+    float carry_end = 0.0f;
+    for (int base = 0; base < nspecial; base += kWave) {
+      const int j = base + lane;
+      const bool in = j < nspecial;
+      const sum_v4 tv = in ? list[j].t : sum_v4{0.0f, 0.0f, 0.0f, 0.0f};
+      const double spj = list[in ? j : nspecial - 1].sp;  // past the list: gap 0
+      double spp = shfl_up1_f64(spj);
+      if (lane == 0) spp = carry_sp;
+      const double gap = spj - spp;
+      const float gapf = (float)gap;
+      float my_end = 0.0f;
+      const int n_here = min(kWave, nspecial - base);
+      for (int k = 0; k < n_here; k += 8) {
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const int k = min(k0 + i, nspecial - 1);
-        tv[i] = list[k].t;
-        const double spk = list[k].sp;
-        gp[i] = (float)(spk - prev);
-        prev = k0 + i < nspecial ? spk : prev;
-      }
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        if (k0 + i < nspecial) {  // uniform
-          float s = end + gp[i];
-          s = s + tv[i].x;
-          s = s + tv[i].y;
-          s = s + tv[i].z;
-          s = s + tv[i].w;
-          if (lane == 0) list[k0 + i].end = s;
+        for (int i = 0; i < 8; ++i) {
+          float s = end + readlane_f32(gapf, k + i);
+          s = s + readlane_f32(tv.x, k + i);
+          s = s + readlane_f32(tv.y, k + i);
+          s = s + readlane_f32(tv.z, k + i);
+          s = s + readlane_f32(tv.w, k + i);
+          my_end = lane == k + i ? s : my_end;
           end = s;
         }
       }
+      // each special's start was an exact f32 add (the f64 sum is exact when the previous end's
+      // lowest bit is >= 2^(Ea-49); the gap is nonzero only right after an ordinary chunk)
+      float pe = shfl_up1_f32(my_end);
+      if (lane == 0) pe = carry_end;
+      if (in) {
+        if (gap != 0.0 && pe != 0.0f && !(pe >= 0x1p-126f && exp_of(pe) >= ea - 26)) fail = true;
+        fail |= (double)gapf != gap || (double)(pe + gapf) != (double)pe + gap;
+        list[j].end = my_end;
+      }
+      carry_sp = readlane_f64(spj, kWave - 1);
+      carry_end = readlane_f32(my_end, kWave - 1);
     }
   }
-  sync.sync_long();
-  bool fail = !ok;
+  sync.sync();
   if (ok) {
-    // each special's start was an exact f32 add (the f64 sum is exact when the previous end's lowest
-    // bit is >= 2^(emax-51); the gap is nonzero only right after an ordinary chunk, below 2^(emax+1))
-    for (int k = tid; k < nspecial; k += kSumThreads) {
-      const double spk = list[k].sp, spp = k ? list[k - 1].sp : 0.0;
-      const float pe = k ? list[k - 1].end : 0.0f;
-      const double gap = spk - spp;
-      const float gapf = (float)gap;
-      if (gap != 0.0 && pe != 0.0f && !(pe >= 0x1p-126f && exp_of(pe) >= emax - 28)) fail = true;
-      fail |= (double)gapf != gap || (double)(pe + gapf) != (double)pe + gap;
-    }
-    // every ordinary chunk against its exact start: the last special's end plus the ordinary
-    // chunks since (chunk 0 is always special, so rank >= 1); exact whenever it can pass
+    // ---- every ordinary chunk against its exact start: the last special's end plus the
+    // ordinary chunks since (chunk 0 is always special, so rank >= 1); exact whenever it can pass
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (sp[u] || zero[u]) continue;
+      if (sp[u] || !live[u]) continue;
       const SumEntry& last = list[rank[u] - 1];
       const double st = (double)last.end + (Sp[u] - last.sp);
       const double lo = __builtin_ldexp(1.0, E[u]), hi = __builtin_ldexp(1.0, E[u] + 1);
@@ -355,7 +358,7 @@ __device__ __forceinline__ float block_exact_sum_squares(const float* sq, int K,
     const float out = (float)S;
     if ((double)out == S) return out;  // uniform: every thread computed the same S
   }
-  // fallback: the plain sequential chain by wave 0, published through the scratch
+  // ---- fallback: the plain sequential chain by wave 0, published through the scratch
   if (wave == 0) {
     const float acc = ordered_sum_from(sq, K, 0.0f);
     if (lane == 0) part->result = acc;

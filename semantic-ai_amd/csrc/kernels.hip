@@ -177,7 +177,8 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, Ste
     }
     return;
   }
-  RowSync rs{&ws, 0u};
+  // the weight waves have ended unless the unit is a split GEMV (they wait in LDS meanwhile)
+  RowSync rs{&ws, 0u, !is_split_gemv(d_ph)};
   unsigned item = 0;
   // Units read the positions from memory where they need them: only the step's last phase that
   // reads them advances them, and launches are ordered on the stream.
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* h
     lds_signal(&ws.t_parts);
     return;
   }
-  RowSync rs{&ws, 0u};
+  RowSync rs{&ws, 0u};  // LDS barriers: the weight waves stream meanwhile
   GemvArgs a = ph.g;
   a.x = hx;
   a.x_stride = hxs;
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(kStepThreads) void attn_phase_kernel(const float* h
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) return;
-  RowSync rs{&ws, 0u};
+  RowSync rs{&ws, 0u, true};
   const int unit = blockIdx.x;
   if (unit < hheads) {
     AttnArgs a = ph.at;
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(kStepThreads) void batch_phase_kernel(const void* h
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   if (threadIdx.x >= kRowThreads) return;
-  RowSync rs{&ws, 0u};
+  RowSync rs{&ws, 0u, true};
   GemvArgs a = ph.g;
   const int epi = hepn & 0xff;
   a.L.in = hin;
@@ -893,7 +894,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* x, 
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ WgSync ws;
   init_wg_sync(&ws);
-  RowSync rs{&ws, 0u};
+  RowSync rs{&ws, 0u, true};  // a workgroup of row waves only
   float v[KP];
   load_row(x + (size_t)blockIdx.x * K, K, v);
   NormW<KP> nw;

@@ -114,10 +114,12 @@ template <bool LONG = false>
 __device__ __forceinline__ bool lds_wait(const unsigned* ctr, unsigned target, unsigned* stop) {
   unsigned spins = 0;
   while ((int)(lds_ld(ctr) - target) < 0) {
-    if (lds_ld(stop)) return false;
-    if (++spins > kLdsSpinLimit) {
-      __hip_atomic_store(stop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      return false;
+    if ((++spins & 15) == 0) {  // one LDS round trip per poll; the abort flag every 16th
+      if (lds_ld(stop)) return false;
+      if (spins > kLdsSpinLimit) {
+        __hip_atomic_store(stop, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return false;
+      }
     }
     if (LONG) __builtin_amdgcn_s_sleep(2);
   }
@@ -139,11 +141,28 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Barrier of the row waves.  Every row wave calls sync() the same number of times.
+// The hardware workgroup barrier after this wave's LDS accesses (outstanding global loads,
+// direct-to-LDS ones included, stay in flight).  It waits for every wave of the workgroup that
+// has not ended.
+__device__ __forceinline__ void hw_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+
+// Barrier of the row waves.  Every row wave calls sync() the same number of times.  Two kinds:
+//   * hw: the hardware barrier (~50 cycles), which every wave of the workgroup that has not ended
+//     must pass: for launches whose weight waves have ended (or that have none).
+//   * otherwise a counter in LDS (~500 cycles), for launches whose weight waves stream weights
+//     meanwhile: they are held up by their own requests for as long as the bytes take to arrive,
+//     and could not take part in a hardware barrier promptly.
 struct RowSync {
   WgSync* ws;
   unsigned epoch;
+  bool hw = false;
   __device__ __forceinline__ void sync() {
+    if (hw) {
+      hw_barrier();
+      return;
+    }
     lds_signal(&ws->r_arrive);
     epoch += kRowWaves;
     lds_wait(&ws->r_arrive, epoch, &ws->stop);
@@ -151,6 +170,10 @@ struct RowSync {
   // The same barrier for waits of microseconds: waiting waves sleep between polls, leaving the
   // SIMD to the wave that works.
   __device__ __forceinline__ void sync_long() {
+    if (hw) {
+      hw_barrier();
+      return;
+    }
     lds_signal(&ws->r_arrive);
     epoch += kRowWaves;
     lds_wait<true>(&ws->r_arrive, epoch, &ws->stop);
@@ -1098,6 +1121,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(
 // wait for the direct loads in flight before them (it cannot tell the counters from the stages).
 // Prior LDS reads of the wave have completed (gemm_read waits for them).
 __device__ __forceinline__ void gemm_sync(RowSync& rs) {
+  if (rs.hw) {
+    asm volatile("s_barrier" : : : "memory");
+    return;
+  }
   const uint32_t ctr = lds_addr(&rs.ws->r_arrive), stop = lds_addr(&rs.ws->stop);
   if ((threadIdx.x & (kWave - 1)) == 0) {
     const uint32_t one = 1;
