@@ -52,6 +52,9 @@ typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4
 typedef enum { SVL_NORM_LAYER = 0, SVL_NORM_RMS = 1 } svl_norm;          /* transformer.rs:12-16 */
 typedef enum { SVL_FF_PLAIN_GELU = 0, SVL_FF_GATED_SILU = 1 } svl_ff;    /* transformer.rs:18-24 */
 typedef enum { SVL_MODEL_TRANSFORMER = 0, SVL_MODEL_STT = 1, SVL_MODEL_TTS = 2 } svl_model_kind;
+/* FlowKind (SVL/tts/config.rs:170-195): LSD (two flow times), flow matching (one), drifting and
+ * pointwise (none). */
+typedef enum { SVL_FLOW_LSD = 0, SVL_FLOW_MATCHING = 1, SVL_FLOW_DRIFTING = 2, SVL_FLOW_POINTWISE = 3 } svl_flow_kind;
 
 /* TransformerConfig (SVL/nn/transformer.rs:26-41) plus the heads of the two backbones
  * (SttConfig, SVL/stt/model.rs:16-34; FlowLmConfig's latent/z dims, SVL/tts/flow_lm.rs:45-126). */
@@ -74,6 +77,10 @@ typedef struct {
                               extra_heads_num_heads / extra_heads_dim (SVL/stt/model.rs:217-222):
                               dense "extra_heads.{i}.weight" [dim][d_model], never quantized;
                               0 = none */
+    int32_t flow_dim, flow_depth, flow_kind;  /* TTS flow head (FlowHeadConfig dim / depth /
+                              type, SVL/tts/config.rs:197-204) and end-of-speech head: tensors
+                              "flow_net.*" and "out_eos.*" (SVL/tts/flow_lm.rs:107-113, 232-251),
+                              dense; flow_dim 0 = backbone only */
 } svl_config;
 
 /* One named tensor (the reference's safetensors names, e.g.
@@ -188,6 +195,23 @@ int svl_stt_recognize_noalloc(const svl_model* model, svl_state* state, int64_t 
  * [batch][latent_dim] f32, or NULL for the learnt `bos_emb` -> z [batch][z_dim or d_model]. */
 int svl_tts_backbone_step(const svl_model* model, svl_state* state, const float* latent,
                           float* out_z);
+
+/* FlowLm::step (SVL/tts/flow_lm.rs:162-185) for every stream: the backbone on latent
+ * [batch][latent_dim] (NULL: the learnt bos_emb), the end-of-speech logit out_eos(z) and the
+ * flow head's decode of `noise` [batch][latent_dim] in `decode_steps` steps (<= 0 counts as 1)
+ * -> out_latent [batch][latent_dim], out_eos_logit [batch] (may be NULL) and out_eos [batch]
+ * (logit > eos_threshold; may be NULL).  The noise is the caller's draw (Sampling's temperature
+ * and clamp, `sample_noise`, :187-203), so that the caller's RNG stream is kept.  Host pointers.
+ * The first call with a given decode_steps computes and keeps that count's time conditioning
+ * (it waits for the state's stream once). */
+int svl_tts_step(const svl_model* model, svl_state* state, const float* latent, const float* noise,
+                 int32_t decode_steps, float eos_threshold, float* out_latent, float* out_eos_logit,
+                 int32_t* out_eos);
+/* The same with device pointers, enqueued on the state's stream: no host round trip per frame
+ * (the reference reads the logit back with to_vec1, :181).  d_latent may be the previous call's
+ * d_out_latent; d_out_eos_logit may be NULL. */
+int svl_tts_step_async(const svl_model* model, svl_state* state, const float* d_latent, const float* d_noise,
+                       int32_t decode_steps, float* d_out_latent, float* d_out_eos_logit);
 
 #ifdef __cplusplus
 }

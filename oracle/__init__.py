@@ -24,6 +24,7 @@ F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN, FF_GATED = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
+FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 
 Q8_0_BLOCK_BYTES = 34
 Q4K_BLOCK_BYTES = 144
@@ -52,6 +53,7 @@ class Config(C.Structure):
         ("card", C.c_int32), ("n_q", C.c_int32), ("text_card", C.c_int32),
         ("latent_dim", C.c_int32), ("z_dim", C.c_int32),
         ("extra_heads_num", C.c_int32), ("extra_heads_dim", C.c_int32),
+        ("flow_dim", C.c_int32), ("flow_depth", C.c_int32), ("flow_kind", C.c_int32),
     ]
 
 
@@ -128,6 +130,20 @@ def lib():
             L.svlo_stt_step.argtypes = [vp, vp, C.c_uint32, vp, C.POINTER(C.c_uint32), vp, vp]
             L.svlo_stt_step.restype = C.c_int
             L.svlo_stt_greedy.argtypes = [vp, vp, C.c_int64, vp, vp, vp, vp]
+            L.svlo_tts_step.argtypes = [vp, vp, vp, vp, C.c_int, vp, vp]
+            L.svlo_tts_step.restype = C.c_int
+            L.svlo_model_flow.argtypes = [vp]
+            L.svlo_model_flow.restype = vp
+            L.svlo_flow_time_embed.argtypes = [vp, C.c_int, C.c_float, vp]
+            L.svlo_flow_time_embed.restype = None
+            L.svlo_flow_time_mean.argtypes = [vp, vp, vp]
+            L.svlo_flow_time_mean.restype = None
+            L.svlo_flow_forward.argtypes = [vp, vp, vp, vp, vp, vp]
+            L.svlo_flow_forward.restype = None
+            L.svlo_flow_decode.argtypes = [vp, vp, vp, C.c_int, vp]
+            L.svlo_flow_decode.restype = None
+            L.svlo_flow_eos_logit.argtypes = [vp, vp]
+            L.svlo_flow_eos_logit.restype = C.c_float
             L.svlo_softmax_first.argtypes = [vp, sz]
             L.svlo_softmax_first.restype = C.c_float
             L.svlo_stt_greedy.restype = C.c_int
@@ -393,6 +409,43 @@ class Model:
             raise ValueError(lib().svlo_last_error().decode())
         return w
 
+    # -- flow head (FlowHead / TimestepEmbedder / out_eos, SVL/tts/flow_lm.rs:181-387) --------
+    def _flow(self):
+        f = lib().svlo_model_flow(self.h)
+        if not f:
+            raise ValueError("the model has no flow head")
+        return f
+
+    def flow_time_embed(self, i: int, t: float) -> np.ndarray:
+        out = np.empty(self.cfg["flow_dim"], dtype=np.float32)
+        lib().svlo_flow_time_embed(self._flow(), i, t, _p(out))
+        return out
+
+    def flow_time_mean(self, times) -> np.ndarray:
+        t = np.ascontiguousarray(times, dtype=np.float32)
+        out = np.empty(self.cfg["flow_dim"], dtype=np.float32)
+        lib().svlo_flow_time_mean(self._flow(), _p(t), _p(out))
+        return out
+
+    def flow_forward(self, cond, times, xs) -> np.ndarray:
+        cond = np.ascontiguousarray(cond, dtype=np.float32)
+        xs = np.ascontiguousarray(xs, dtype=np.float32)
+        t = None if times is None else np.ascontiguousarray(times, dtype=np.float32)
+        out = np.empty(self.cfg["latent_dim"], dtype=np.float32)
+        lib().svlo_flow_forward(self._flow(), _p(cond), None if t is None else _p(t), None, _p(xs), _p(out))
+        return out
+
+    def flow_decode(self, cond, noise, steps: int) -> np.ndarray:
+        cond = np.ascontiguousarray(cond, dtype=np.float32)
+        noise = np.ascontiguousarray(noise, dtype=np.float32)
+        out = np.empty(self.cfg["latent_dim"], dtype=np.float32)
+        lib().svlo_flow_decode(self._flow(), _p(cond), _p(noise), steps, _p(out))
+        return out
+
+    def eos_logit(self, z) -> float:
+        z = np.ascontiguousarray(z, dtype=np.float32)
+        return float(lib().svlo_flow_eos_logit(self._flow(), _p(z)))
+
     def new_state(self, batch: int = 1) -> "State":
         return State(self, lib().svlo_state_create(self.h, batch))
 
@@ -478,3 +531,15 @@ class State:
         if lib().svlo_tts_backbone_step(self.model.h, self.h, None if lat is None else _p(lat), _p(z)):
             raise ValueError(lib().svlo_last_error().decode())
         return z
+
+    def tts_full_step(self, latent, noise, decode_steps: int = 1):
+        """FlowLm::step with the sampler's noise -> (next latent [latent_dim], eos logit)."""
+        cfg = self.model.cfg
+        out = np.empty(cfg["latent_dim"], dtype=np.float32)
+        eos = C.c_float()
+        lat = None if latent is None else np.ascontiguousarray(latent, dtype=np.float32)
+        nz = np.ascontiguousarray(noise, dtype=np.float32)
+        if lib().svlo_tts_step(self.model.h, self.h, None if lat is None else _p(lat), _p(nz), decode_steps,
+                               _p(out), C.byref(eos)):
+            raise ValueError(lib().svlo_last_error().decode())
+        return out, eos.value

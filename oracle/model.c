@@ -8,6 +8,7 @@
  *   LanguageModel::step (STT)       SVL/stt/model.rs:196-276
  *   Recognizer::step token feedback SVL/stt/mod.rs:551-566
  *   FlowLm::step backbone (TTS)     SVL/tts/flow_lm.rs:45-126, 162-181
+ *   FlowLm::step heads (TTS)        SVL/tts/flow_lm.rs:181-185 (flow.c)
  */
 #include <math.h>
 #include <stdarg.h>
@@ -183,7 +184,10 @@ struct svlo_model {
     /* TTS */
     linear_t input_linear, z_proj;
     float* bos;
+    svlo_flow* flow; /* flow head + out_eos, or NULL (flow_dim 0) */
 };
+
+const svlo_flow* svlo_model_flow(const svlo_model* m) { return m->flow; }
 
 void svlo_model_destroy(svlo_model* m) {
     if (!m) return;
@@ -211,6 +215,7 @@ void svlo_model_destroy(svlo_model* m) {
     linear_free(&m->input_linear);
     linear_free(&m->z_proj);
     free(m->bos);
+    svlo_flow_destroy(m->flow);
     free(m);
 }
 
@@ -311,6 +316,14 @@ int svlo_model_create(const svlo_config* cfg, const svlo_tensor* tensors, size_t
             if ((rc = load_linear(&ts, "z_proj.weight", (size_t)c->z_dim, d, 0, &m->z_proj))) goto done;
         m->bos = load_f32(&ts, "bos_emb", (size_t)c->latent_dim, &rc);
         if (!m->bos) goto done;
+        if (c->flow_dim > 0) {
+            /* SVL/tts/flow_lm.rs:107-113: the heads read z, of width z_dim or d_model */
+            int cond = c->z_dim > 0 ? c->z_dim : c->d_model;
+            if (svlo_flow_create(c->flow_dim, c->flow_depth, c->flow_kind, c->latent_dim, cond, tensors, n, &m->flow)) {
+                rc = fail("%s", svlo_flow_last_error());
+                goto done;
+            }
+        }
     }
 done:
     if (rc) {
@@ -657,5 +670,23 @@ int svlo_tts_backbone_step(const svlo_model* m, svlo_state* s, const float* late
     }
     free(x);
     free(y);
+    return rc;
+}
+
+/* FlowLm::step (SVL/tts/flow_lm.rs:162-185) after the sampler's noise draw (:187-203, the
+ * caller's): the backbone's z, the end-of-speech logit of out_eos(z), the flow head's decode
+ * of the noise conditioned on z. */
+int svlo_tts_step(const svlo_model* m, svlo_state* s, const float* latent, const float* noise, int decode_steps,
+                  float* out_latent, float* out_eos_logit) {
+    if (!m->flow) return fail("the model has no flow head");
+    const svlo_config* c = &m->cfg;
+    size_t zd = (size_t)(c->z_dim > 0 ? c->z_dim : c->d_model);
+    float* z = (float*)malloc(sizeof(float) * zd);
+    int rc = svlo_tts_backbone_step(m, s, latent, z);
+    if (rc == 0) {
+        if (out_eos_logit) *out_eos_logit = svlo_flow_eos_logit(m->flow, z);
+        svlo_flow_decode(m->flow, z, noise, decode_steps, out_latent);
+    }
+    free(z);
     return rc;
 }

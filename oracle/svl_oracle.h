@@ -94,6 +94,8 @@ enum { SVLO_F32 = 0, SVLO_BF16 = 1, SVLO_F16 = 2, SVLO_Q8_0 = 3, SVLO_Q4K = 4 };
 enum { SVLO_NORM_LAYER = 0, SVLO_NORM_RMS = 1 };
 enum { SVLO_FF_PLAIN = 0, SVLO_FF_GATED = 1 };
 enum { SVLO_MODEL_TRANSFORMER = 0, SVLO_MODEL_STT = 1, SVLO_MODEL_TTS = 2 };
+/* FlowKind (SVL/tts/config.rs:170-185) */
+enum { SVLO_FLOW_LSD = 0, SVLO_FLOW_MATCHING = 1, SVLO_FLOW_DRIFTING = 2, SVLO_FLOW_POINTWISE = 3 };
 
 typedef struct {
     int32_t kind;          /* SVLO_MODEL_* */
@@ -110,6 +112,7 @@ typedef struct {
     /* TTS */
     int32_t latent_dim, z_dim; /* z_dim 0 = no z_proj */
     int32_t extra_heads_num, extra_heads_dim; /* STT VAD heads (0: none) */
+    int32_t flow_dim, flow_depth, flow_kind;  /* TTS flow head (0 = none), SVLO_FLOW_* */
 } svlo_config;
 
 typedef struct {
@@ -153,6 +156,27 @@ int svlo_stt_greedy(const svlo_model* m, svlo_state* s, int64_t n, const uint32_
                     uint32_t* out_tokens, float* out_last_logits, float* out_probs /* [n][heads] */);
 /* latent [latent_dim] or NULL (bos) -> z [z_dim or d_model] */
 int svlo_tts_backbone_step(const svlo_model* m, svlo_state* s, const float* latent, float* out_z);
+/* FlowLm::step (SVL/tts/flow_lm.rs:162-185) with the noise the sampler drew: latent or NULL
+ * (bos), noise [latent_dim] -> next latent [latent_dim] and the end-of-speech logit. */
+int svlo_tts_step(const svlo_model* m, svlo_state* s, const float* latent, const float* noise, int decode_steps,
+                  float* out_latent, float* out_eos_logit);
+
+/* ---- flow head (flow.c): FlowHead / TimestepEmbedder / ResBlock / out_eos -------------- */
+typedef struct svlo_flow svlo_flow;
+int svlo_flow_create(int dim, int depth, int kind, int latent, int cond, const svlo_tensor* ts, size_t n,
+                     svlo_flow** out);
+void svlo_flow_destroy(svlo_flow* f);
+const char* svlo_flow_last_error(void);
+const svlo_flow* svlo_model_flow(const svlo_model* m);
+/* TimestepEmbedder i at time t -> [dim]; the mean of the embeddings of `times` -> [dim] */
+void svlo_flow_time_embed(const svlo_flow* f, int i, float t, float* out);
+void svlo_flow_time_mean(const svlo_flow* f, const float* times, float* out);
+/* FlowHead::forward: cond [cond], times, tmean [dim] or NULL, xs [latent] -> out [latent] */
+void svlo_flow_forward(const svlo_flow* f, const float* cond, const float* times, const float* tmean,
+                       const float* xs, float* out);
+/* FlowHead::decode: noise [latent] -> latent [latent] */
+void svlo_flow_decode(const svlo_flow* f, const float* cond, const float* noise, int steps, float* out);
+float svlo_flow_eos_logit(const svlo_flow* f, const float* z);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,7 @@
 //   Linear::from_weight (quantize at load)               SVL/nn/mod.rs:76-87
 //   LanguageModel::step / Recognizer::step               SVL/stt/model.rs:239-276, SVL/stt/mod.rs:551-566
 //   FlowLm::step backbone                                SVL/tts/flow_lm.rs:162-181
+//   FlowLm::step heads: out_eos, FlowHead::decode         SVL/tts/flow_lm.rs:181-185, 206-387
 //   TransformerState duplicate / from_layer_caches       SVL/nn/transformer.rs:58-104
 // The KV cache is a ring of `context` slots per layer (or `capacity` slots without a window):
 // key j of a stream lives in slot j % slots.  The reference's compacting cache
@@ -13,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -27,6 +29,7 @@
 
 #include "../../include/svl.h"
 #include "../../include/svl_bench.h"
+#include "flow_head.h"
 #include "kernels.h"
 
 using namespace svl;
@@ -108,6 +111,23 @@ struct svl_model {
   // TTS
   LinearDev input_linear, z_proj;
   float* bos = nullptr;
+  // TTS flow head (FlowHead, SVL/tts/flow_lm.rs:206-387) and out_eos (:109-112), f32
+  struct Flow {
+    int dim = 0, depth = 0, kind = 0, n_time = 0, latent = 0, cond = 0;
+    int mod_rows = 0;           // depth * 3 dim (ResBlock modulations) + 2 dim (final layer)
+    FhLinear ce;                // cond_embed rows [0, dim) and out_eos row dim, stacked
+    FhLinear in;                // input_proj
+    FhLinear mod;               // every adaLN_modulation.1 stacked (they share the input silu(y))
+    std::vector<FhLinear> m1, m2;
+    std::vector<float*> lnw, lnb;
+    FhLinear fl;                // final_layer.linear
+    FhLinear t1[2], t2[2];      // TimestepEmbedder mlp.0 / mlp.2
+    float* talpha[2] = {nullptr, nullptr};
+    std::vector<float> freqs[2];  // host copies: the embedders' cos/sin are computed on the host
+    // time conditioning of each flow step, by step count: [steps][dim] (computed on first use)
+    std::map<int, float*> tmean;
+  } flow;
+  mutable std::mutex flow_mu;
   hipStream_t stream = nullptr;  // used at creation only
 
   ~svl_model() {
@@ -145,6 +165,9 @@ struct svl_state {
   uint32_t* fb_tok = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr, *z = nullptr;
   float* in = nullptr;        // TTS latent staging [B][latent_dim]
+  // TTS flow head: cond_embed + out_eos [B][dim + 1], modulations [B][mod_rows], residual stream
+  // and MLP hidden [B][dim], the sample and the noise [B][latent_dim]
+  float *fh_ce = nullptr, *fh_mod = nullptr, *fh_h = nullptr, *fh_a = nullptr, *fh_x = nullptr, *fh_noise = nullptr;
   float* xlogits = nullptr;   // STT extra heads: logits [B][nh * hd]
   float* xprob = nullptr;     //                  first-class probabilities [B][nh]
   float* fwd = nullptr;       // transformer forward staging (input then output)
@@ -187,13 +210,12 @@ struct svl_state {
 
 namespace {
 
-// Uploads a dense tensor as f32 (converted on the GPU from bf16/f16).
-int upload_f32(svl_model* m, const svl_tensor* t, size_t n, float** out) {
+// Copies a dense tensor of n elements to device memory dst as f32 (converted on the GPU from
+// bf16/f16).
+int copy_f32(svl_model* m, const svl_tensor* t, size_t n, void* dst) {
   if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor");
   if (numel(t) != n)
     return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: %zu elements, expected %zu", t->name, numel(t), n);
-  void* dst;
-  TRY(m->alloc(&dst, n * 4));
   if (t->dtype == SVL_F32) {
     HIP_TRY(hipMemcpy(dst, t->data, n * 4, hipMemcpyHostToDevice));
   } else if (t->dtype == SVL_BF16 || t->dtype == SVL_F16) {
@@ -209,6 +231,17 @@ int upload_f32(svl_model* m, const svl_tensor* t, size_t n, float** out) {
   } else {
     return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: dense dtype expected", t->name);
   }
+  return 0;
+}
+
+// Uploads a dense tensor as f32 into a new model allocation.
+int upload_f32(svl_model* m, const svl_tensor* t, size_t n, float** out) {
+  if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor");
+  if (numel(t) != n)
+    return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: %zu elements, expected %zu", t->name, numel(t), n);
+  void* dst;
+  TRY(m->alloc(&dst, n * 4));
+  TRY(copy_f32(m, t, n, dst));
   *out = (float*)dst;
   return 0;
 }
@@ -460,6 +493,92 @@ int load_extra_heads(svl_model* m, const svl_tensor* ts, size_t n) {
   return load_linear(m, &all, 1, "extra_heads", nh * hd, d, 0, &m->extra_heads);
 }
 
+// Dense f32 linears with bias, stacked row-wise in the order of `parts` ({prefix, rows}: tensors
+// prefix + ".weight" [rows][in] and prefix + ".bias" [rows]), chain-packed when in % 64 == 0.
+int load_fh_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::vector<std::pair<std::string, int>>& parts,
+                   int in, FhLinear* L) {
+  int rows = 0;
+  for (const auto& p : parts) rows += p.second;
+  const size_t count = (size_t)rows * in;
+  void *rm = nullptr, *bias = nullptr;
+  TRY(m->alloc(&bias, (size_t)rows * 4));
+  HIP_TRY(hipMalloc(&rm, count * 4));
+  std::unique_ptr<void, void (*)(void*)> rm_guard(rm, [](void* p) { hipFree(p); });
+  size_t r0 = 0;
+  for (const auto& p : parts) {
+    const std::string wn = p.first + ".weight", bn = p.first + ".bias";
+    const svl_tensor* w = find_tensor(ts, n, wn);
+    if (!w) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", wn.c_str());
+    if (w->ndim != 2 || w->shape[0] != p.second || w->shape[1] != in)
+      return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: shape mismatch (expected [%d, %d])", wn.c_str(), p.second, in);
+    TRY(copy_f32(m, w, (size_t)p.second * in, (float*)rm + r0 * in));
+    const svl_tensor* b = find_tensor(ts, n, bn);
+    if (!b) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", bn.c_str());
+    TRY(copy_f32(m, b, (size_t)p.second, (float*)bias + r0));
+    r0 += (size_t)p.second;
+  }
+  void* w;
+  TRY(m->alloc(&w, count * 4));
+  if (in % 64 == 0) {
+    HIP_TRY(launch_chain_pack(rm, 0, rows, in, w, 0, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    L->packed = 1;
+  } else {
+    HIP_TRY(hipMemcpy(w, rm, count * 4, hipMemcpyDeviceToDevice));
+    L->packed = 0;
+  }
+  L->w = (const float*)w;
+  L->b = (const float*)bias;
+  L->out = rows;
+  L->in = in;
+  return 0;
+}
+
+// FlowHead::new (SVL/tts/flow_lm.rs:232-251) with its TimestepEmbedders (:322-331) and ResBlocks
+// (:359-368), and out_eos (:109-112), which reads the same z as cond_embed.
+int load_flow(svl_model* m, const svl_tensor* ts, size_t n) {
+  const svl_config& c = m->cfg;
+  svl_model::Flow& F = m->flow;
+  F.dim = c.flow_dim;
+  F.depth = c.flow_depth;
+  F.kind = c.flow_kind;
+  F.n_time = c.flow_kind == SVL_FLOW_LSD ? 2 : (c.flow_kind == SVL_FLOW_MATCHING ? 1 : 0);
+  F.latent = c.latent_dim;
+  F.cond = c.z_dim > 0 ? c.z_dim : c.d_model;
+  const int D = F.dim;
+  F.mod_rows = F.depth * 3 * D + 2 * D;
+  const std::string p = "flow_net.";
+  TRY(load_fh_linear(m, ts, n, {{p + "cond_embed", D}, {"out_eos", 1}}, F.cond, &F.ce));
+  TRY(load_fh_linear(m, ts, n, {{p + "input_proj", D}}, F.latent, &F.in));
+  std::vector<std::pair<std::string, int>> mods;
+  for (int j = 0; j < F.depth; ++j) mods.push_back({p + "res_blocks." + std::to_string(j) + ".adaLN_modulation.1", 3 * D});
+  mods.push_back({p + "final_layer.adaLN_modulation.1", 2 * D});
+  TRY(load_fh_linear(m, ts, n, mods, D, &F.mod));
+  F.m1.resize(F.depth);
+  F.m2.resize(F.depth);
+  F.lnw.resize(F.depth);
+  F.lnb.resize(F.depth);
+  for (int j = 0; j < F.depth; ++j) {
+    const std::string r = p + "res_blocks." + std::to_string(j) + ".";
+    TRY(load_fh_linear(m, ts, n, {{r + "mlp.0", D}}, D, &F.m1[j]));
+    TRY(load_fh_linear(m, ts, n, {{r + "mlp.2", D}}, D, &F.m2[j]));
+    TRY(load_vec(m, ts, n, r + "in_ln.weight", D, &F.lnw[j]));
+    TRY(load_vec(m, ts, n, r + "in_ln.bias", D, &F.lnb[j]));
+  }
+  TRY(load_fh_linear(m, ts, n, {{p + "final_layer.linear", F.latent}}, D, &F.fl));
+  for (int i = 0; i < F.n_time; ++i) {
+    const std::string t = p + "time_embed." + std::to_string(i) + ".";
+    TRY(load_fh_linear(m, ts, n, {{t + "mlp.0", D}}, 256, &F.t1[i]));
+    TRY(load_fh_linear(m, ts, n, {{t + "mlp.2", D}}, D, &F.t2[i]));
+    TRY(load_vec(m, ts, n, t + "mlp.3.alpha", D, &F.talpha[i]));
+    float* fr = nullptr;
+    TRY(load_vec(m, ts, n, t + "freqs", 128, &fr));
+    F.freqs[i].resize(128);
+    HIP_TRY(hipMemcpy(F.freqs[i].data(), fr, 128 * 4, hipMemcpyDeviceToHost));
+  }
+  return 0;
+}
+
 // Configuration errors (what the reference itself rejects or cannot build) are SVL_ERR_CONFIG;
 // valid configurations outside what these kernels cover are SVL_UNSUPPORTED, for the caller to
 // run the reference's own path (the reference's kernels return None: SVL/nn/kernels/matvec.rs:12-17).
@@ -488,6 +607,13 @@ int check_config(const svl_config* c) {
   if (c->context > kMaxRingSlots) return set_error(SVL_UNSUPPORTED, "context must be <= %d", kMaxRingSlots);
   if (c->kind == SVL_MODEL_STT && c->n_q > 64) return set_error(SVL_UNSUPPORTED, "n_q must be <= 64");
   if (c->kind == SVL_MODEL_TTS && c->latent_dim % 4) return set_error(SVL_UNSUPPORTED, "latent_dim must be a multiple of 4");
+  if (c->kind == SVL_MODEL_TTS && c->flow_dim != 0) {
+    if (c->flow_dim < 0 || c->flow_depth < 0 || c->flow_kind < SVL_FLOW_LSD || c->flow_kind > SVL_FLOW_POINTWISE)
+      return set_error(SVL_ERR_CONFIG, "invalid flow head config");
+    const int cond = c->z_dim > 0 ? c->z_dim : c->d_model;
+    if (c->flow_dim > kFhMaxWidth || cond > kFhMaxWidth || c->latent_dim > kFhMaxWidth)
+      return set_error(SVL_UNSUPPORTED, "flow head widths must be <= %d", kFhMaxWidth);
+  }
   return 0;
 }
 
@@ -555,6 +681,7 @@ int create_model(const svl_config* cfg, const svl_tensor* ts, size_t n, svl_mode
     TRY(load_vec(m, ts, n, "out_norm.bias", d, &m->out_norm_b));
     if (c.z_dim > 0) TRY(load_linear(m, ts, n, "z_proj.weight", c.z_dim, d, 0, &m->z_proj));
     TRY(load_vec(m, ts, n, "bos_emb", c.latent_dim, &m->bos));
+    if (c.flow_dim > 0) TRY(load_flow(m, ts, n));
   }
   HIP_TRY(hipDeviceSynchronize());
   return 0;
@@ -1060,6 +1187,17 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
     rc = s->alloc(&p, (size_t)batch * wmax), s->xqb = (int8_t*)p;
     if (!rc) rc = s->alloc(&p, (size_t)batch * (wmax / 32) * 4), s->xdqb = (float*)p;
   }
+  if (!rc && c.kind == SVL_MODEL_TTS && c.flow_dim > 0) {
+    const svl_model::Flow& F = m->flow;
+    rc = s->alloc(&p, (size_t)batch * (F.dim + 1) * 4), s->fh_ce = (float*)p;
+    // the modulation rows also hold the time embedders' outputs while a step count's time
+    // conditioning is computed (n_time * dim <= 2 dim <= mod_rows)
+    if (!rc) rc = s->alloc(&p, (size_t)batch * F.mod_rows * 4), s->fh_mod = (float*)p;
+    if (!rc) rc = s->alloc(&p, (size_t)batch * F.dim * 4), s->fh_h = (float*)p;
+    if (!rc) rc = s->alloc(&p, (size_t)batch * F.dim * 4), s->fh_a = (float*)p;
+    if (!rc) rc = s->alloc(&p, (size_t)batch * F.latent * 4), s->fh_x = (float*)p;
+    if (!rc) rc = s->alloc(&p, (size_t)batch * F.latent * 4), s->fh_noise = (float*)p;
+  }
   if (!rc) rc = s->alloc(&p, (size_t)(batch + 1) * 4), s->tok_out = (uint32_t*)p;
   if (!rc) rc = s->alloc(&p, (size_t)batch * sizeof(int)), s->rope_delta = (int*)p;
   if (!rc) rc = s->alloc(&p, sizeof(SyncState)), s->sync = (SyncState*)p;
@@ -1080,6 +1218,156 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
       hipStreamSynchronize(s->stream) != hipSuccess)
     return fail(set_error(SVL_ERR_DEVICE, "state initialisation failed"));
   *out = holder.release();
+  return 0;
+}
+
+// The time conditioning of every flow step for `steps` steps (SVL/tts/flow_lm.rs:256-266,
+// 286-309): [steps][dim], computed once per step count on the state's stream and kept in the
+// model.  The embedders' cos/sin rows are the C library's cosf/sinf of freqs * t, as Rust's
+// f32::cos / f32::sin compute them on the host (:333-337).
+int flow_tmean(svl_state* s, int steps, const float** out) {
+  svl_model* m = const_cast<svl_model*>(s->m);  // the cache is guarded by flow_mu
+  svl_model::Flow& F = m->flow;
+  std::lock_guard<std::mutex> lock(m->flow_mu);
+  auto it = F.tmean.find(steps);
+  if (it != F.tmean.end()) {
+    *out = it->second;
+    return 0;
+  }
+  const int D = F.dim;
+  std::vector<float> emb((size_t)steps * F.n_time * 256);
+  for (int i = 0; i < steps; ++i) {
+    // LSD: (s, t) = (i / steps, (i + 1) / steps); flow matching: t = i / steps
+    const float times[2] = {(float)i / (float)steps, (float)(i + 1) / (float)steps};
+    for (int e = 0; e < F.n_time; ++e) {
+      float* row = emb.data() + ((size_t)i * F.n_time + e) * 256;
+      for (int k = 0; k < 128; ++k) {
+        const float pr = F.freqs[e][k] * times[e];
+        const float a = pr + 0.0f;
+        row[k] = cosf(a);
+        row[128 + k] = sinf(a);
+      }
+    }
+  }
+  void *dtab = nullptr, *demb = nullptr;
+  HIP_TRY(hipMalloc(&dtab, (size_t)steps * D * 4));
+  std::unique_ptr<void, void (*)(void*)> tab_guard(dtab, [](void* p) { hipFree(p); });
+  HIP_TRY(hipMalloc(&demb, emb.size() * 4));
+  std::unique_ptr<void, void (*)(void*)> emb_guard(demb, [](void* p) { hipFree(p); });
+  HIP_TRY(hipMemcpyAsync(demb, emb.data(), emb.size() * 4, hipMemcpyHostToDevice, s->stream));
+  for (int i = 0; i < steps; ++i) {
+    for (int e = 0; e < F.n_time; ++e) {
+      FhArgs a{};
+      a.B = 1;
+      a.L = F.t1[e];
+      a.x = (const float*)demb + ((size_t)i * F.n_time + e) * 256;
+      a.x_stride = 256;
+      a.y = s->fh_a;
+      a.y_stride = D;
+      HIP_TRY(launch_fh_gemv(a, FH_PLAIN, FH_BIAS_SILU, s->stream));
+      a = FhArgs{};
+      a.B = 1;
+      a.L = F.t2[e];
+      a.x = s->fh_a;
+      a.x_stride = D;
+      a.y = s->fh_mod + (size_t)e * D;
+      a.y_stride = D;
+      HIP_TRY(launch_fh_gemv(a, FH_PLAIN, FH_BIAS, s->stream));
+    }
+    HIP_TRY(launch_fh_time_norm(s->fh_mod, F.talpha, F.n_time, D, (float)(1.0 / D), (float)(1.0 / (D - 1.0)),
+                                (float)(1.0 / F.n_time), (float*)dtab + (size_t)i * D, s->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(s->stream));  // the host table is released on return
+  F.tmean[steps] = (float*)dtab;
+  m->allocs.push_back(tab_guard.release());
+  *out = (const float*)dtab;
+  return 0;
+}
+
+// FlowLm::step after the backbone (SVL/tts/flow_lm.rs:181-185): z (s->z) -> the end-of-speech
+// logits (s->fh_ce[b][dim]) and the decoded sample (s->fh_x) from the noise in s->fh_noise.
+int run_flow_head(svl_state* s, int steps) {
+  const svl_model::Flow& F = s->m->flow;
+  steps = std::max(steps, 1);  // FlowHead::decode: steps.max(1)
+  const float* tmean = nullptr;
+  if (F.n_time > 0) TRY(flow_tmean(s, steps, &tmean));
+  const int D = F.dim, B = s->B;
+  FhArgs a{};
+  a.B = B;
+  a.L = F.ce;
+  a.x = s->z;
+  a.x_stride = F.cond;
+  a.y = s->fh_ce;
+  a.y_stride = D + 1;
+  HIP_TRY(launch_fh_gemv(a, FH_PLAIN, FH_BIAS, s->stream));
+  HIP_TRY(hipMemcpyAsync(s->fh_x, s->fh_noise, (size_t)B * F.latent * 4, hipMemcpyDeviceToDevice, s->stream));
+  // LSD and flow matching integrate `steps` Euler steps; drifting and pointwise run the head once
+  const bool euler = F.kind == SVL_FLOW_LSD || F.kind == SVL_FLOW_MATCHING;
+  const int n = euler ? steps : 1;
+  for (int i = 0; i < n; ++i) {
+    FhArgs g{};
+    g.B = B;
+    g.L = F.mod;
+    g.x = s->fh_ce;
+    g.x_stride = D + 1;
+    g.x2 = tmean ? tmean + (size_t)i * D : nullptr;
+    g.y = s->fh_mod;
+    g.y_stride = F.mod_rows;
+    HIP_TRY(launch_fh_gemv(g, FH_SILU_Y, FH_BIAS, s->stream));
+    g = FhArgs{};
+    g.B = B;
+    g.L = F.in;
+    g.x = s->fh_x;
+    g.x_stride = F.latent;
+    g.y = s->fh_h;
+    g.y_stride = D;
+    HIP_TRY(launch_fh_gemv(g, FH_PLAIN, FH_BIAS, s->stream));
+    for (int j = 0; j < F.depth; ++j) {
+      const float* mj = s->fh_mod + (size_t)j * 3 * D;  // chunk(3): shift, scale, gate
+      g = FhArgs{};
+      g.B = B;
+      g.L = F.m1[j];
+      g.x = s->fh_h;
+      g.x_stride = D;
+      g.lnw = F.lnw[j];
+      g.lnb = F.lnb[j];
+      g.shift = mj;
+      g.scale = mj + D;
+      g.mod_stride = F.mod_rows;
+      g.eps = 1e-6f;  // SVL/tts/flow_lm.rs:378
+      g.y = s->fh_a;
+      g.y_stride = D;
+      HIP_TRY(launch_fh_gemv(g, FH_LN_MOD, FH_BIAS_SILU, s->stream));
+      g = FhArgs{};
+      g.B = B;
+      g.L = F.m2[j];
+      g.x = s->fh_a;
+      g.x_stride = D;
+      g.gate = mj + 2 * D;
+      g.mod_stride = F.mod_rows;
+      g.y = s->fh_h;
+      g.y_stride = D;
+      HIP_TRY(launch_fh_gemv(g, FH_PLAIN, FH_GATE_RES, s->stream));
+    }
+    const float* mf = s->fh_mod + (size_t)F.depth * 3 * D;  // chunk(2): shift, scale
+    g = FhArgs{};
+    g.B = B;
+    g.L = F.fl;
+    g.x = s->fh_h;
+    g.x_stride = D;
+    g.shift = mf;
+    g.scale = mf + D;
+    g.mod_stride = F.mod_rows;
+    g.eps = 1e-6f;  // SVL/tts/flow_lm.rs:277
+    g.inv_k = (float)(1.0 / D);
+    g.y = s->fh_x;
+    g.y_stride = F.latent;
+    g.inv_steps = (float)(1.0 / steps);
+    g.noise = s->fh_noise;
+    g.noise_stride = F.latent;
+    const int epi = euler ? FH_FLOW : (F.kind == SVL_FLOW_DRIFTING ? FH_BIAS : FH_POINTWISE);
+    HIP_TRY(launch_fh_gemv(g, FH_LN0_MOD, epi, s->stream));
+  }
   return 0;
 }
 
@@ -1631,6 +1919,52 @@ static int tts_backbone_step_impl(const svl_model* m, svl_state* s, const float*
   return check_abort(s);
 }
 
+// FlowLm::step (SVL/tts/flow_lm.rs:162-185).  `host`: the pointers are host memory and the
+// call returns with the outputs there; otherwise device pointers, enqueued only.
+static int tts_step_impl(const svl_model* m, svl_state* s, const float* latent, const float* noise, int32_t steps,
+                         bool host, float* out_latent, float* out_eos_logit) {
+  if (!m || !s || !noise || !out_latent) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
+  const svl_config& c = m->cfg;
+  if (c.kind != SVL_MODEL_TTS) return set_error(SVL_ERR_CONFIG, "not a TTS model");
+  if (c.flow_dim <= 0) return set_error(SVL_ERR_CONFIG, "the model has no flow head (flow_dim 0)");
+  TRY(check_room(s, 1));
+  HIP_TRY(hipSetDevice(m->device));
+  const int ld = c.latent_dim;
+  const size_t lb = (size_t)s->B * ld * 4;
+  const hipMemcpyKind in_kind = host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+  const hipMemcpyKind out_kind = host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+  if (latent) {
+    HIP_TRY(hipMemcpyAsync(s->in, latent, lb, in_kind, s->stream));
+  } else {
+    for (int b = 0; b < s->B; ++b)
+      HIP_TRY(hipMemcpyAsync(s->in + (size_t)b * ld, m->bos, (size_t)ld * 4, hipMemcpyDeviceToDevice, s->stream));
+  }
+  HIP_TRY(hipMemcpyAsync(s->fh_noise, noise, lb, in_kind, s->stream));
+  TRY(run_program(s, s->tts, StepParams{}, 1));
+  TRY(run_flow_head(s, steps));
+  HIP_TRY(hipMemcpyAsync(out_latent, s->fh_x, lb, out_kind, s->stream));
+  if (out_eos_logit)
+    HIP_TRY(hipMemcpy2DAsync(out_eos_logit, 4, s->fh_ce + m->flow.dim, (size_t)(m->flow.dim + 1) * 4, 4, s->B, out_kind,
+                             s->stream));
+  if (!host) return 0;
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  return check_abort(s);
+}
+
+static int tts_step_sync_impl(const svl_model* m, svl_state* s, const float* latent, const float* noise, int32_t steps,
+                              float eos_threshold, float* out_latent, float* out_eos_logit, int32_t* out_eos) {
+  if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  std::vector<float> logits((size_t)s->B);
+  TRY(tts_step_impl(m, s, latent, noise, steps, true, out_latent, logits.data()));
+  for (int b = 0; b < s->B; ++b) {
+    if (out_eos_logit) out_eos_logit[b] = logits[b];
+    if (out_eos) out_eos[b] = logits[b] > eos_threshold ? 1 : 0;  // SVL/tts/flow_lm.rs:184
+  }
+  return 0;
+}
+
+
 
 // The C entry points: no C++ exception crosses the boundary.
 int svl_device_count(int* count) {
@@ -1729,6 +2063,20 @@ int svl_bench_phase(const svl_model* m, svl_state* s, int program, int phase, in
 int svl_stt_recognize_noalloc(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                               uint32_t* out_tokens) {
   return guarded([&] { return stt_recognize_noalloc_impl(m, s, n_steps, audio_tokens, out_tokens); });
+}
+
+int svl_tts_step(const svl_model* m, svl_state* s, const float* latent, const float* noise, int32_t decode_steps,
+                 float eos_threshold, float* out_latent, float* out_eos_logit, int32_t* out_eos) {
+  return guarded([&] {
+    return tts_step_sync_impl(m, s, latent, noise, decode_steps, eos_threshold, out_latent, out_eos_logit, out_eos);
+  });
+}
+
+int svl_tts_step_async(const svl_model* m, svl_state* s, const float* d_latent, const float* d_noise,
+                       int32_t decode_steps, float* d_out_latent, float* d_out_eos_logit) {
+  return guarded([&] {
+    return tts_step_impl(m, s, d_latent, d_noise, decode_steps, false, d_out_latent, d_out_eos_logit);
+  });
 }
 
 }  // extern "C"

@@ -11,6 +11,7 @@ The classes mirror the reference crate's step API (crates/semantic-voice-local/s
   * ``Model.step``                  LanguageModel::step              (SVL/stt/model.rs:239-276)
   * ``Model.recognize``             Recognizer::step's token loop    (SVL/stt/mod.rs:551-566)
   * ``Model.backbone_step``         FlowLm::step, backbone part      (SVL/tts/flow_lm.rs:162-181)
+  * ``Model.tts_step``              FlowLm::step with the sampler's noise (SVL/tts/flow_lm.rs:162-185)
 
 Errors raise ``SvlError`` carrying the library's status code (the reference's
 ``Result<_, Error>``, SVL/error.rs).  There is no CPU fallback: without the built library or a
@@ -31,6 +32,7 @@ F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN_GELU, FF_GATED_SILU = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
+FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 
 ERR_CONFIG, ERR_INVALID_INPUT, ERR_DEVICE, ERR_IO = -1, -2, -3, -4
 UNSUPPORTED = 1  # valid for the reference, outside these kernels: run the reference's path
@@ -43,6 +45,7 @@ EXPORTS = [
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
     "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase",
+    "svl_tts_step", "svl_tts_step_async",
 ]
 
 
@@ -71,6 +74,7 @@ class Config(C.Structure):
         ("latent_dim", C.c_int32), ("z_dim", C.c_int32),
         ("kv_dtype", C.c_int32),
         ("extra_heads_num", C.c_int32), ("extra_heads_dim", C.c_int32),
+        ("flow_dim", C.c_int32), ("flow_depth", C.c_int32), ("flow_kind", C.c_int32),
     ]
 
 
@@ -119,6 +123,8 @@ def load_library(path: str = LIB_PATH):
     L.svl_stt_recognize_async.argtypes = [vp, vp, i64, vp, vp]
     L.svl_tts_backbone_step.argtypes = [vp, vp, vp, vp]
     L.svl_stt_recognize_noalloc.argtypes = [vp, vp, i64, vp, vp]
+    L.svl_tts_step.argtypes = [vp, vp, vp, vp, i32, C.c_float, vp, vp, vp]
+    L.svl_tts_step_async.argtypes = [vp, vp, vp, vp, i32, vp, vp]
     L.svl_bench_phase.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int)]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
     L.svl_bench_row_stats.argtypes = [C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp]
@@ -293,6 +299,25 @@ class Model:
         lat = None if latent is None else np.ascontiguousarray(latent, dtype=np.float32)
         _check(load_library().svl_tts_backbone_step(self.h, state.h, None if lat is None else _p(lat), _p(z)))
         return z
+
+    def tts_step(self, latent, noise, state: "State", decode_steps: int = 1, eos_threshold: float = -4.0):
+        """FlowLm::step for every stream with the sampler's noise [batch, latent_dim] ->
+        (latents [batch, latent_dim], eos logits [batch], eos flags [batch])."""
+        ld = self.cfg["latent_dim"]
+        nz = np.ascontiguousarray(noise, dtype=np.float32).reshape(state.batch, ld)
+        lat = None if latent is None else np.ascontiguousarray(latent, dtype=np.float32).reshape(state.batch, ld)
+        out = np.empty((state.batch, ld), dtype=np.float32)
+        logits = np.empty(state.batch, dtype=np.float32)
+        flags = np.empty(state.batch, dtype=np.int32)
+        _check(load_library().svl_tts_step(self.h, state.h, None if lat is None else _p(lat), _p(nz), decode_steps,
+                                           eos_threshold, _p(out), _p(logits), _p(flags)))
+        return out, logits, flags
+
+    def tts_step_async(self, d_latent: int, d_noise: int, decode_steps: int, d_out: int, d_eos: int,
+                       state: "State") -> None:
+        """Device-pointer variant (d_latent 0: bos); enqueues on the state's stream."""
+        _check(load_library().svl_tts_step_async(self.h, state.h, C.c_void_p(d_latent or None), C.c_void_p(d_noise),
+                                                 decode_steps, C.c_void_p(d_out), C.c_void_p(d_eos or None)))
 
 
 class State:

@@ -26,6 +26,7 @@ F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN, FF_GATED = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
+FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 
 
 @dataclass
@@ -51,6 +52,9 @@ class Shape:
     z_dim: int = 0
     extra_heads_num: int = 0   # STT VAD heads (SVL/stt/model.rs:217-222)
     extra_heads_dim: int = 0
+    flow_dim: int = 0          # TTS flow head (FlowHeadConfig, SVL/tts/config.rs:197-204); 0 = none
+    flow_depth: int = 0
+    flow_kind: int = 0         # FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE
 
     def config(self, quantize: int = 0) -> dict:
         return dict(kind=self.kind, d_model=self.d_model, num_layers=self.num_layers,
@@ -61,7 +65,8 @@ class Shape:
                     max_period=self.max_period, quantize=quantize, card=self.card,
                     n_q=self.n_q, text_card=self.text_card, latent_dim=self.latent_dim,
                     z_dim=self.z_dim, extra_heads_num=self.extra_heads_num,
-                    extra_heads_dim=self.extra_heads_dim)
+                    extra_heads_dim=self.extra_heads_dim, flow_dim=self.flow_dim,
+                    flow_depth=self.flow_depth, flow_kind=self.flow_kind)
 
 
 def stt_shape(name, dim, layers, heads, hidden_scale, context, card=2048, n_q=32, text_card=8000):
@@ -71,20 +76,23 @@ def stt_shape(name, dim, layers, heads, hidden_scale, context, card=2048, n_q=32
                  NORM_RMS, 1e-8, context, card=card, n_q=n_q, text_card=text_card)
 
 
-def tts_shape(name, dim, layers, heads, hidden, latent=32, z_dim=0):
-    """SVL/tts/flow_lm.rs:52-71."""
+def tts_shape(name, dim, layers, heads, hidden, latent=32, z_dim=0, flow_dim=0, flow_depth=0,
+              flow_kind=FLOW_LSD):
+    """SVL/tts/flow_lm.rs:52-71; the flow head of configs/tts/english.yaml:16-19 (dim 512,
+    depth 6, LSD)."""
     return Shape(name, MODEL_TTS, dim, layers, heads, heads, dim // heads, FF_PLAIN, hidden,
-                 NORM_LAYER, 1e-5, 0, latent_dim=latent, z_dim=z_dim)
+                 NORM_LAYER, 1e-5, 0, latent_dim=latent, z_dim=z_dim, flow_dim=flow_dim,
+                 flow_depth=flow_depth, flow_kind=flow_kind)
 
 
 # The five benchmark shapes.
 S1 = stt_shape("stt-1b", 2048, 16, 16, 4.125, 750)          # hidden 5632
 S2 = stt_shape("stt-2.6b", 2560, 24, 20, 4.05, 3000)         # hidden 6912
-T1 = tts_shape("pocket-tts", 1024, 6, 16, 4096)
+T1 = tts_shape("pocket-tts", 1024, 6, 16, 4096, flow_dim=512, flow_depth=6)
 # Reduced shapes with the same structure, for parity tests the oracle finishes in seconds.
 S1_SMALL = stt_shape("stt-small", 256, 3, 4, 4.125, 24, card=64, n_q=4, text_card=100)  # hidden 704
 S2_SMALL = stt_shape("stt-small-q4k", 512, 2, 4, 4.5, 40, card=64, n_q=4, text_card=96)  # hidden 1536
-T1_SMALL = tts_shape("tts-small", 256, 2, 4, 1024)
+T1_SMALL = tts_shape("tts-small", 256, 2, 4, 1024, flow_dim=64, flow_depth=2)
 
 assert S1.ff_hidden == 5632 and S2.ff_hidden == 6912
 
@@ -155,6 +163,41 @@ def tensor_names(s: Shape):
         if s.z_dim:
             out.append(("z_proj.weight", (s.z_dim, d), "dense_linear"))
         out.append(("bos_emb", (s.latent_dim,), "vec"))
+        out += flow_tensor_names(s)
+    return out
+
+
+def flow_tensor_names(s: Shape):
+    """The flow head and end-of-speech head (SVL/tts/flow_lm.rs:107-113, 232-251, 322-331,
+    359-368): (name, shape, role); roles "flow_linear" (weights) and "vec" (biases),
+    "norm_w" / "norm_b", "freqs" (the timestep embedders' frequencies)."""
+    if not s.flow_dim:
+        return []
+    D, L = s.flow_dim, s.latent_dim
+    cond = s.z_dim or s.d_model
+    n_time = {FLOW_LSD: 2, FLOW_MATCHING: 1}.get(s.flow_kind, 0)
+    p = "flow_net."
+    out = []
+    for i in range(n_time):
+        t = f"{p}time_embed.{i}."
+        out += [(t + "freqs", (128,), "freqs"),
+                (t + "mlp.0.weight", (D, 256), "flow_linear"), (t + "mlp.0.bias", (D,), "vec"),
+                (t + "mlp.2.weight", (D, D), "flow_linear"), (t + "mlp.2.bias", (D,), "vec"),
+                (t + "mlp.3.alpha", (D,), "norm_w")]
+    out += [(p + "cond_embed.weight", (D, cond), "flow_linear"), (p + "cond_embed.bias", (D,), "vec"),
+            (p + "input_proj.weight", (D, L), "flow_linear"), (p + "input_proj.bias", (D,), "vec")]
+    for j in range(s.flow_depth):
+        r = f"{p}res_blocks.{j}."
+        out += [(r + "in_ln.weight", (D,), "norm_w"), (r + "in_ln.bias", (D,), "norm_b"),
+                (r + "mlp.0.weight", (D, D), "flow_linear"), (r + "mlp.0.bias", (D,), "vec"),
+                (r + "mlp.2.weight", (D, D), "flow_linear"), (r + "mlp.2.bias", (D,), "vec"),
+                (r + "adaLN_modulation.1.weight", (3 * D, D), "flow_linear"),
+                (r + "adaLN_modulation.1.bias", (3 * D,), "vec")]
+    f = p + "final_layer."
+    out += [(f + "adaLN_modulation.1.weight", (2 * D, D), "flow_linear"),
+            (f + "adaLN_modulation.1.bias", (2 * D,), "vec"),
+            (f + "linear.weight", (L, D), "flow_linear"), (f + "linear.bias", (L,), "vec"),
+            ("out_eos.weight", (1, cond), "flow_linear"), ("out_eos.bias", (1,), "vec")]
     return out
 
 
@@ -170,13 +213,18 @@ def make_weights(s: Shape, dtype: str, seed: int = 0, threads: int | None = None
 
     def one(item):
         name, shape, role = item
+        if role == "freqs":
+            # the timestep embedders' frequencies, exp(-ln(10000) k / 128) as the checkpoints
+            # hold them
+            x = np.exp(-np.log(10000.0) * np.arange(128) / 128).astype(np.float32)
+            return name, (F32, shape, x)
         if role == "norm_w":
             x = normal(seed, name, shape, 0.02, 1.0)
         elif role == "vec":
             x = normal(seed, name, shape, 0.02, 1.0 if "layer_scale" in name else 0.0)
         else:
             x = normal(seed, name, shape, 0.02)
-        if dtype == "f32" or (dtype in ("q8_0", "q4k") and role in ("linear", "dense_linear")):
+        if dtype == "f32" or role == "flow_linear" or (dtype in ("q8_0", "q4k") and role in ("linear", "dense_linear")):
             return name, (F32, shape, x)
         return name, (BF16, shape, to_bf16_bits(x))
 
