@@ -46,8 +46,10 @@ typedef enum {
 
 /* Weight dtypes: dense, or candle QTensor block formats (GgmlDType::Q8_0 = 34-byte blocks
  * {f16 d; i8 qs[32]}, GgmlDType::Q4K = 144-byte blocks {f16 d, dmin; u8 scales[12];
- * u8 qs[128]}), row-major [out][in / block]. */
-typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4 } svl_dtype;
+ * u8 qs[128]}, GgmlDType::Q4_0 = 18-byte blocks {f16 d; u8 qs[16]}: byte j holds the 4-bit code
+ * of element j (low nibble) and of element j + 16 (high nibble), value (code - 8) * d),
+ * row-major [out][in / block]. */
+typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4, SVL_Q4_0 = 5 } svl_dtype;
 
 typedef enum { SVL_NORM_LAYER = 0, SVL_NORM_RMS = 1 } svl_norm;          /* transformer.rs:12-16 */
 typedef enum { SVL_FF_PLAIN_GELU = 0, SVL_FF_GATED_SILU = 1 } svl_ff;    /* transformer.rs:18-24 */
@@ -68,8 +70,9 @@ typedef struct {
     int32_t layer_scale;   /* 0/1: layers.{i}.layer_scale_{1,2}.scale */
     int32_t context;       /* attention window; 0 = unlimited */
     double max_period;     /* RoPE base */
-    int32_t quantize;      /* 0, SVL_Q8_0 or SVL_Q4K: dense linears are quantized on the GPU at
-                              creation (Linear::from_weight, SVL/nn/mod.rs:76-87) */
+    int32_t quantize;      /* 0, SVL_Q8_0, SVL_Q4_0 or SVL_Q4K: dense linears are quantized on the
+                              GPU at creation (Linear::from_weight, SVL/nn/mod.rs:76-87, with
+                              the block type chosen here instead of its fixed Q8_0) */
     int32_t card, n_q, text_card;    /* STT */
     int32_t latent_dim, z_dim;       /* TTS (z_dim 0: no z_proj) */
     int32_t kv_dtype;      /* SVL_F32 (default) or SVL_BF16: element type of the KV ring buffers */

@@ -20,13 +20,14 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
+F32, BF16, F16, Q8_0, Q4K, Q4_0 = 0, 1, 2, 3, 4, 5
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN, FF_GATED = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
 FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 
 Q8_0_BLOCK_BYTES = 34
+Q4_0_BLOCK_BYTES = 18
 Q4K_BLOCK_BYTES = 144
 Q8K_BLOCK_BYTES = 292
 
@@ -79,13 +80,16 @@ def lib():
             L.svlo_f32_to_bf16.argtypes = [C.c_float]
             for name in ["svlo_f32_to_f16_n", "svlo_f32_to_bf16_n", "svlo_bf16_to_f32_n",
                          "svlo_quantize_q8_0", "svlo_dequantize_q8_0", "svlo_quantize_q4k",
-                         "svlo_dequantize_q4k", "svlo_quantize_q8k"]:
+                         "svlo_dequantize_q4k", "svlo_quantize_q8k", "svlo_quantize_q4_0",
+                         "svlo_dequantize_q4_0"]:
                 getattr(L, name).argtypes = [vp, vp, sz]
                 getattr(L, name).restype = None
             L.svlo_vec_dot_q8_0.argtypes = [sz, vp, vp]
             L.svlo_vec_dot_q8_0.restype = C.c_float
             L.svlo_vec_dot_q4k_q8k.argtypes = [sz, vp, vp]
             L.svlo_vec_dot_q4k_q8k.restype = C.c_float
+            L.svlo_vec_dot_q4_0_q8_0.argtypes = [sz, vp, vp]
+            L.svlo_vec_dot_q4_0_q8_0.restype = C.c_float
             L.svlo_set_fma.argtypes = [C.c_int]
             L.svlo_set_threads.argtypes = [C.c_int]
             L.svlo_set_norm_order.argtypes = [C.c_int]
@@ -232,6 +236,30 @@ def vec_dot_q8_0(w_blocks, x_blocks, n: int) -> float:
     w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
     x = np.ascontiguousarray(x_blocks, dtype=np.uint8)
     return lib().svlo_vec_dot_q8_0(n, _p(w), _p(x))
+
+
+def quantize_q4_0(x) -> np.ndarray:
+    """[rows, k] f32 -> [rows, k/32 * 18] uint8 candle Q4_0 blocks."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    assert k % 32 == 0
+    out = np.empty(x.shape[:-1] + (k // 32 * Q4_0_BLOCK_BYTES,), dtype=np.uint8)
+    lib().svlo_quantize_q4_0(_p(x), _p(out), x.size)
+    return out
+
+
+def dequantize_q4_0(blocks, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    rows = blocks.size // (k // 32 * Q4_0_BLOCK_BYTES)
+    out = np.empty(blocks.shape[:-1] + (k,), dtype=np.float32)
+    lib().svlo_dequantize_q4_0(_p(blocks), _p(out), rows * k)
+    return out
+
+
+def vec_dot_q4_0_q8_0(w_blocks, x_blocks, n: int) -> float:
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x_blocks, dtype=np.uint8)
+    return lib().svlo_vec_dot_q4_0_q8_0(n, _p(w), _p(x))
 
 
 def quantize_q4k(x) -> np.ndarray:

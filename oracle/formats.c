@@ -1,5 +1,5 @@
 /*
- * formats.c -- f16/bf16 conversion and the candle GGML block formats (Q8_0, Q4K, Q8K).
+ * formats.c -- f16/bf16 conversion and the candle GGML block formats (Q8_0, Q4_0, Q4K, Q8K).
  *
  * TEST INFRASTRUCTURE ONLY (see svl_oracle.h).
  *
@@ -133,6 +133,74 @@ float svlo_vec_dot_q8_0(size_t n, const svlo_block_q8_0* w, const svlo_block_q8_
     for (size_t i = 0; i < nb; ++i) {
         int32_t s = 0;
         for (int j = 0; j < SVLO_QK8_0; ++j) s += (int32_t)w[i].qs[j] * (int32_t)x[i].qs[j];
+        float t = (float)s * svlo_f16_to_f32(w[i].d);
+        t = t * svlo_f16_to_f32(x[i].d);
+        sumf += t;
+    }
+    return sumf;
+}
+
+/* ---- Q4_0 ---------------------------------------------------------------------------
+ * [candle hypothesis] BlockQ4_0 (GGML quantize_row_q4_0 / dequantize_row_q4_0 as candle's
+ * k_quants restate them): per 32 values, `max` = the value of largest magnitude (the first one
+ * on ties: `if amax < |x|`), d = max / -8, id = 1 / d (0 if d = 0), d stored as f16; the code
+ * of x is min(15, (x * id + 8.5) as u8) (Rust's saturating, truncating cast); byte j holds
+ * element j in its low nibble and element j + 16 in its high nibble; value = (code - 8) * d. */
+
+/* Rust `v as u8`: NaN -> 0, saturating to [0, 255], truncation toward zero. */
+static inline uint8_t cast_u8(float v) {
+    if (v != v || v <= 0.0f) return 0;
+    if (v >= 255.0f) return 255;
+    return (uint8_t)v;
+}
+
+void svlo_quantize_q4_0(const float* x, svlo_block_q4_0* y, size_t k) {
+    size_t nb = k / SVLO_QK4_0;
+    for (size_t i = 0; i < nb; ++i) {
+        const float* xs = x + i * SVLO_QK4_0;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < SVLO_QK4_0; ++j) {
+            float a = fabsf(xs[j]);
+            if (amax < a) {
+                amax = a;
+                max = xs[j];
+            }
+        }
+        float d = max / -8.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = svlo_f32_to_f16(d);
+        for (int j = 0; j < SVLO_QK4_0 / 2; ++j) {
+            float x0 = xs[j] * id, x1 = xs[SVLO_QK4_0 / 2 + j] * id;
+            uint8_t q0 = cast_u8(x0 + 8.5f), q1 = cast_u8(x1 + 8.5f);
+            if (q0 > 15) q0 = 15;
+            if (q1 > 15) q1 = 15;
+            y[i].qs[j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+void svlo_dequantize_q4_0(const svlo_block_q4_0* x, float* y, size_t k) {
+    size_t nb = k / SVLO_QK4_0;
+    for (size_t i = 0; i < nb; ++i) {
+        float d = svlo_f16_to_f32(x[i].d);
+        for (int j = 0; j < SVLO_QK4_0 / 2; ++j) {
+            y[i * SVLO_QK4_0 + j] = (float)((x[i].qs[j] & 0x0F) - 8) * d;
+            y[i * SVLO_QK4_0 + j + SVLO_QK4_0 / 2] = (float)((x[i].qs[j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* [candle hypothesis] BlockQ4_0::vec_dot_unopt against Q8_0 activations: the exact i32 sum of
+ * (code - 8) * q over the block, then sumf += ((f32)sum * d_w) * d_x in block order. */
+float svlo_vec_dot_q4_0_q8_0(size_t n, const svlo_block_q4_0* w, const svlo_block_q8_0* x) {
+    size_t nb = n / SVLO_QK4_0;
+    float sumf = 0.0f;
+    for (size_t i = 0; i < nb; ++i) {
+        int32_t s = 0;
+        for (int j = 0; j < SVLO_QK4_0 / 2; ++j) {
+            int32_t v0 = (int32_t)(w[i].qs[j] & 0x0F) - 8, v1 = (int32_t)(w[i].qs[j] >> 4) - 8;
+            s += v0 * (int32_t)x[i].qs[j] + v1 * (int32_t)x[i].qs[j + SVLO_QK4_0 / 2];
+        }
         float t = (float)s * svlo_f16_to_f32(w[i].d);
         t = t * svlo_f16_to_f32(x[i].d);
         sumf += t;

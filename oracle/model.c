@@ -35,7 +35,7 @@ static int fail(const char* fmt, ...) {
 
 /* ---- linear ------------------------------------------------------------------------- */
 
-enum { LIN_NONE = 0, LIN_DENSE = 1, LIN_Q8_0 = 2, LIN_Q4K = 3 };
+enum { LIN_NONE = 0, LIN_DENSE = 1, LIN_Q8_0 = 2, LIN_Q4K = 3, LIN_Q4_0 = 4 };
 
 typedef struct {
     int kind;
@@ -43,12 +43,14 @@ typedef struct {
     float* w;
     svlo_block_q8_0* q8;
     svlo_block_q4k* q4;
+    svlo_block_q4_0* q40;
 } linear_t;
 
 static void linear_free(linear_t* l) {
     free(l->w);
     free(l->q8);
     free(l->q4);
+    free(l->q40);
     memset(l, 0, sizeof(*l));
 }
 
@@ -68,6 +70,17 @@ static void linear_forward(const linear_t* L, const float* x, size_t rows, float
             float* yr = y + r * L->out;
 #pragma omp parallel for schedule(static, 128) num_threads(threads)
             for (long o = 0; o < (long)L->out; ++o) yr[o] = svlo_vec_dot_q8_0(L->in, L->q8 + (size_t)o * nb, xb);
+        }
+        free(xb);
+    } else if (L->kind == LIN_Q4_0) {
+        /* BlockQ4_0's VecDotType is BlockQ8_0: the row is quantized as for Q8_0 weights */
+        size_t nb = L->in / SVLO_QK8_0;
+        svlo_block_q8_0* xb = (svlo_block_q8_0*)malloc(sizeof(svlo_block_q8_0) * nb);
+        for (size_t r = 0; r < rows; ++r) {
+            svlo_quantize_q8_0(x + r * L->in, xb, L->in);
+            float* yr = y + r * L->out;
+#pragma omp parallel for schedule(static, 128) num_threads(threads)
+            for (long o = 0; o < (long)L->out; ++o) yr[o] = svlo_vec_dot_q4_0_q8_0(L->in, L->q40 + (size_t)o * nb, xb);
         }
         free(xb);
     } else if (L->kind == LIN_Q4K) {
@@ -132,6 +145,14 @@ static int load_linear(const tensors_t* ts, const char* name, size_t out, size_t
         memcpy(L->q8, t->data, sizeof(svlo_block_q8_0) * nb);
         return 0;
     }
+    if (t->dtype == SVLO_Q4_0) {
+        if (in % SVLO_QK4_0) return fail("tensor %s: Q4_0 needs in %% 32 == 0", name);
+        size_t nb = out * in / SVLO_QK4_0;
+        L->kind = LIN_Q4_0;
+        L->q40 = (svlo_block_q4_0*)malloc(sizeof(svlo_block_q4_0) * nb);
+        memcpy(L->q40, t->data, sizeof(svlo_block_q4_0) * nb);
+        return 0;
+    }
     if (t->dtype == SVLO_Q4K) {
         if (in % SVLO_QK_K) return fail("tensor %s: Q4K needs in %% 256 == 0", name);
         size_t nb = out * in / SVLO_QK_K;
@@ -148,6 +169,12 @@ static int load_linear(const tensors_t* ts, const char* name, size_t out, size_t
         L->q8 = (svlo_block_q8_0*)malloc(sizeof(svlo_block_q8_0) * out * in / SVLO_QK8_0);
 #pragma omp parallel for schedule(static) num_threads(svlo_get_threads())
         for (long r = 0; r < (long)out; ++r) svlo_quantize_q8_0(w + r * in, L->q8 + r * (in / SVLO_QK8_0), in);
+        free(w);
+    } else if (quantize == SVLO_Q4_0 && in % SVLO_QK4_0 == 0) {
+        L->kind = LIN_Q4_0;
+        L->q40 = (svlo_block_q4_0*)malloc(sizeof(svlo_block_q4_0) * out * in / SVLO_QK4_0);
+#pragma omp parallel for schedule(static) num_threads(svlo_get_threads())
+        for (long r = 0; r < (long)out; ++r) svlo_quantize_q4_0(w + r * in, L->q40 + r * (in / SVLO_QK4_0), in);
         free(w);
     } else if (quantize == SVLO_Q4K && in % SVLO_QK_K == 0) {
         L->kind = LIN_Q4K;
@@ -351,6 +378,7 @@ int svlo_model_linear_weight(const svlo_model* m, const char* name, float* out, 
     if (n != L->out * L->in) return fail("size mismatch");
     if (L->kind == LIN_DENSE) memcpy(out, L->w, sizeof(float) * n);
     else if (L->kind == LIN_Q8_0) svlo_dequantize_q8_0(L->q8, out, n);
+    else if (L->kind == LIN_Q4_0) svlo_dequantize_q4_0(L->q40, out, n);
     else svlo_dequantize_q4k(L->q4, out, n);
     return 0;
 }

@@ -25,10 +25,12 @@ extern "C" {
 /* ---- formats (candle-core quantized k_quants; half 2.7.1) ------------------------------ */
 
 #define SVLO_QK8_0 32
+#define SVLO_QK4_0 32
 #define SVLO_QK_K 256
 
 #pragma pack(push, 1)
 typedef struct { uint16_t d; int8_t qs[32]; } svlo_block_q8_0;                 /* 34 B */
+typedef struct { uint16_t d; uint8_t qs[16]; } svlo_block_q4_0;                /* 18 B */
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128]; } svlo_block_q4k; /* 144 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } svlo_block_q8k;   /* 292 B */
 #pragma pack(pop)
@@ -44,6 +46,9 @@ void svlo_bf16_to_f32_n(const uint16_t* x, float* y, size_t n);
 void svlo_quantize_q8_0(const float* x, svlo_block_q8_0* y, size_t k);
 void svlo_dequantize_q8_0(const svlo_block_q8_0* x, float* y, size_t k);
 float svlo_vec_dot_q8_0(size_t n, const svlo_block_q8_0* w, const svlo_block_q8_0* x);
+void svlo_quantize_q4_0(const float* x, svlo_block_q4_0* y, size_t k);
+void svlo_dequantize_q4_0(const svlo_block_q4_0* x, float* y, size_t k);
+float svlo_vec_dot_q4_0_q8_0(size_t n, const svlo_block_q4_0* w, const svlo_block_q8_0* x);
 
 void svlo_quantize_q4k(const float* x, svlo_block_q4k* y, size_t k);
 void svlo_dequantize_q4k(const svlo_block_q4k* x, float* y, size_t k);
@@ -90,7 +95,7 @@ float svlo_softmax_first(const float* x, size_t n);
 
 /* ---- model ------------------------------------------------------------------------------ */
 
-enum { SVLO_F32 = 0, SVLO_BF16 = 1, SVLO_F16 = 2, SVLO_Q8_0 = 3, SVLO_Q4K = 4 };
+enum { SVLO_F32 = 0, SVLO_BF16 = 1, SVLO_F16 = 2, SVLO_Q8_0 = 3, SVLO_Q4K = 4, SVLO_Q4_0 = 5 };
 enum { SVLO_NORM_LAYER = 0, SVLO_NORM_RMS = 1 };
 enum { SVLO_FF_PLAIN = 0, SVLO_FF_GATED = 1 };
 enum { SVLO_MODEL_TRANSFORMER = 0, SVLO_MODEL_STT = 1, SVLO_MODEL_TTS = 2 };

@@ -19,7 +19,13 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 // widening and round-to-nearest-even narrowing, f16 subnormals kept -- the `half` crate's
 // f16::to_f32 / from_f32 for every non-NaN value).
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// The empty asm keeps the f32 value opaque: otherwise the compiler folds a preceding product into
+// a mixed-precision FMA with a +0 addend (v_fma_mixlo_f16 x, c, 0), which turns a -0 product
+// (candle's Q4_0 scale 0 / -8 of an all-zero block) into +0.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  __asm__ volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 

@@ -6,7 +6,7 @@
 
 namespace svl {
 
-enum WeightFmt { FMT_F32 = 0, FMT_BF16 = 1, FMT_Q8_0 = 3, FMT_Q4K = 4, FMT_F32C = 5, FMT_BF16C = 6 };
+enum WeightFmt { FMT_F32 = 0, FMT_BF16 = 1, FMT_Q8_0 = 3, FMT_Q4K = 4, FMT_F32C = 5, FMT_BF16C = 6, FMT_Q4_0 = 7 };
 enum NormKind { NORM_NONE = 0, NORM_LAYER = 1, NORM_RMS = 2 };
 enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 3, EPI_GELU = 4 };
 
@@ -17,6 +17,9 @@ enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 
 //     ((row * in / (16 E) + c / E) * 16 + l) * E + c % E, i.e. the 16 lane chains of a row are
 //     interleaved 16 bytes at a time.
 //   FMT_Q8_0: w = int8 quants [out][in]; scale = f16 block scales [out][in/32].
+//   FMT_Q4_0: w = candle's Q4_0 code bytes [out][in/2]: the 16 bytes of block blk of a row at
+//     byte 16 blk, byte j holding the code of element j in its low nibble and of element j + 16
+//     in its high nibble (value = (code - 8) * d); scale = f16 block scales [out][in/32].
 //   FMT_Q4K: w = 144-byte super-blocks [out][in/256]: f16 d, f16 dmin and the 12 bytes of packed
 //     6-bit sub-block scales and mins exactly as candle's BlockQ4K holds them, then the 128 quant
 //     bytes with each 32-byte group lane-grouped: byte 4 l + g of a group is candle's byte
@@ -208,7 +211,7 @@ constexpr int kAttnVmWait = vm_wait_imm(2 * (kAttnStages - 2 * kSyncChunks));  /
 // Unit families of a step program.  The persistent kernel is compiled for a few family sets, so
 // that a program is run by a kernel holding only the registers of the units it has.
 enum UnitFamily : unsigned {
-  FAM_Q8 = 1,     // Q8_0 GEMV (row waves + weight waves)
+  FAM_Q8 = 1,     // Q8_0 and Q4_0 GEMV (row waves + weight waves)
   FAM_Q4K = 2,    // Q4K GEMV (row waves + weight waves)
   FAM_DENSE = 4,  // f32 / bf16 GEMV
   FAM_BATCH = 8,  // batched Q8_0: activation quantization + MFMA GEMM
@@ -228,6 +231,9 @@ void plan_qgemm(GemvArgs& g, int grid, int* units);
 hipError_t launch_q8_quantize(const float* w, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_from_blocks(const uint8_t* blocks, int rows, int K, int8_t* qs, uint16_t* d, hipStream_t s);
 hipError_t launch_q8_to_blocks(const int8_t* qs, const uint16_t* d, int rows, int K, uint8_t* blocks, hipStream_t s);
+hipError_t launch_q4_0_quantize(const float* w, int rows, int K, uint8_t* qs, uint16_t* d, hipStream_t s);
+hipError_t launch_q4_0_from_blocks(const uint8_t* blocks, int rows, int K, uint8_t* qs, uint16_t* d, hipStream_t s);
+hipError_t launch_q4_0_to_blocks(const uint8_t* qs, const uint16_t* d, int rows, int K, uint8_t* blocks, hipStream_t s);
 hipError_t launch_q4k_quantize(const float* w, int rows, int K, uint8_t* blocks, hipStream_t s);
 hipError_t launch_q4k_from_blocks(const uint8_t* candle, int rows, int K, uint8_t* blocks, hipStream_t s);
 hipError_t launch_q4k_to_blocks(const uint8_t* blocks, int rows, int K, uint8_t* candle, hipStream_t s);

@@ -189,8 +189,9 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, Ste
 // with the fields its first loads depend on as leading scalar arguments, which the hardware
 // preloads into SGPRs (-amdgpu-kernarg-preload-count): the input row and the weight requests go
 // out at wave start instead of after a scalar load of the argument segment.  `hx` input rows,
-// `hw` / `hsc` weights and Q8_0 block scales, `hnw` norm weights, `hepn` = epilogue | norm kind
-// << 8 | blocks per weight thread << 16 | bf16 dense weights << 24, `hxs` input row stride.
+// `hw` / `hsc` weights and Q8_0 / Q4_0 block scales, `hnw` norm weights, `hepn` = epilogue | norm
+// kind << 8 | blocks per weight thread << 16 | (bf16 dense weights, or Q4_0 codes) << 24, `hxs`
+// input row stride.
 template <unsigned F, int V>
 __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* hx, const void* hw, const void* hsc,
                                                                   const float* hnw, int hin, int hipw, int hparts,
@@ -204,7 +205,8 @@ __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* h
     if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
     if constexpr (F == FAM_Q8) {
       WItem it;
-      w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, maxb, epi, blockIdx.x, it);
+      w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, maxb, epi, blockIdx.x, it,
+                 (hepn >> 24) & 1);
       if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
       w_terms(it, smem);
     } else if constexpr (F == FAM_Q4K) {
@@ -323,7 +325,8 @@ unsigned program_families(const Phase* phases, int n) {
   unsigned f = 0;
   for (int i = 0; i < n; ++i) {
     const Phase& ph = phases[i];
-    if (ph.kind == PH_GEMV) f |= ph.g.L.fmt == FMT_Q8_0 ? FAM_Q8 : (ph.g.L.fmt == FMT_Q4K ? FAM_Q4K : FAM_DENSE);
+    if (ph.kind == PH_GEMV)
+      f |= ph.g.L.fmt == FMT_Q8_0 || ph.g.L.fmt == FMT_Q4_0 ? FAM_Q8 : (ph.g.L.fmt == FMT_Q4K ? FAM_Q4K : FAM_DENSE);
     if (ph.kind == PH_QUANT || ph.kind == PH_QGEMM) f |= FAM_BATCH;
   }
   return f;
@@ -376,16 +379,16 @@ void (*attn_kernel_at(int v))(const Phase, StepParams, int) {
 hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s) {
   if (ph.units <= 0) return hipSuccess;
   void (*k)(const Phase, StepParams, int);
-  if (ph.kind == PH_GEMV && (ph.g.L.fmt == FMT_Q8_0 || ph.g.L.fmt == FMT_Q4K || ph.g.L.fmt == FMT_F32C ||
-                             ph.g.L.fmt == FMT_BF16C)) {
+  if (ph.kind == PH_GEMV && (ph.g.L.fmt == FMT_Q8_0 || ph.g.L.fmt == FMT_Q4_0 || ph.g.L.fmt == FMT_Q4K ||
+                             ph.g.L.fmt == FMT_F32C || ph.g.L.fmt == FMT_BF16C)) {
     const GemvArgs& g = ph.g;
     void (*kq)(const float*, const void*, const void*, const float*, int, int, int, int, int, int, const Phase,
                StepParams, int);
-    if (g.L.fmt == FMT_Q8_0) kq = gemv_slots_kernel<FAM_Q8>(row_slots(g.L.in));
+    if (g.L.fmt == FMT_Q8_0 || g.L.fmt == FMT_Q4_0) kq = gemv_slots_kernel<FAM_Q8>(row_slots(g.L.in));
     else if (g.L.fmt == FMT_Q4K) kq = gemv_slots_kernel<FAM_Q4K>(row_slots(g.L.in));
     else kq = gemv_slots_kernel<FAM_DENSE>(row_slots(g.L.in));
     const int items = g.epi == EPI_SILU_GATE ? g.ff_hidden : g.L.out;
-    const int epn = g.epi | (g.norm << 8) | (g.maxb << 16) | ((g.L.fmt == FMT_BF16C ? 1 : 0) << 24);
+    const int epn = g.epi | (g.norm << 8) | (g.maxb << 16) | ((g.L.fmt == FMT_BF16C || g.L.fmt == FMT_Q4_0 ? 1 : 0) << 24);
     hipLaunchKernelGGL(kq, dim3(ph.units), dim3(kStepThreads), smem, s, g.x, (const void*)g.L.w, (const void*)g.L.scale,
                        g.nw, g.L.in, g.ipw, g.parts, items, epn, g.x_stride, ph, p, step);
     return hipGetLastError();
@@ -419,7 +422,7 @@ hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t s
   }
   switch (ph.kind) {
     case PH_GEMV:
-      if (ph.g.L.fmt == FMT_Q8_0) k = slots_kernel<FAM_Q8, 0u>(row_slots(ph.g.L.in));
+      if (ph.g.L.fmt == FMT_Q8_0 || ph.g.L.fmt == FMT_Q4_0) k = slots_kernel<FAM_Q8, 0u>(row_slots(ph.g.L.in));
       else if (ph.g.L.fmt == FMT_Q4K) k = slots_kernel<FAM_Q4K, 0u>(row_slots(ph.g.L.in));
       else k = slots_kernel<FAM_DENSE, kind_bit(PH_GEMV)>(row_slots(ph.g.L.in));
       break;
@@ -449,7 +452,7 @@ int step_program_grid(int device) {
 void plan_gemv(GemvArgs& g, int grid, int* units) {
   const bool silu = g.epi == EPI_SILU_GATE;
   const int items = silu ? g.ff_hidden : g.L.out;
-  if (g.L.fmt == FMT_Q8_0) {
+  if (g.L.fmt == FMT_Q8_0 || g.L.fmt == FMT_Q4_0) {
     const int nb = g.L.in / 32;
     // About one unit per workgroup and batch row; at most kWBlocks weight blocks per weight-wave
     // thread and one row-wave thread per row for the row sums.
@@ -513,9 +516,9 @@ size_t phase_smem(const Phase& ph) {
     case PH_GEMV: {
       const GemvArgs& g = ph.g;
       const int K = g.L.in;
-      if (g.L.fmt == FMT_Q8_0) {
+      if (g.L.fmt == FMT_Q8_0 || g.L.fmt == FMT_Q4_0) {
         const int nb = K / 32, nb4 = (nb + 3) & ~3;
-        return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 4 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
+        return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 8 + (size_t)2 * g.ipw * q8_row_stride(nb) * 4 +
                (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_Q4K) {
@@ -595,6 +598,74 @@ __global__ void q8_to_blocks_kernel(const int8_t* qs, const uint16_t* d, size_t 
 hipError_t launch_q8_to_blocks(const int8_t* qs, const uint16_t* d, int rows, int K, uint8_t* blocks, hipStream_t s) {
   size_t nb = (size_t)rows * (K / 32);
   hipLaunchKernelGGL(q8_to_blocks_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, qs, d, nb, blocks);
+  return hipGetLastError();
+}
+
+// ---- Q4_0 ---------------------------------------------------------------------------------------
+// candle BlockQ4_0::from_float on the GPU: one thread per 32-value block.  max = the value of
+// largest magnitude (the first on ties), d = max / -8, id = 1 / d (0 if d = 0), code =
+// min(15, (x * id + 8.5) as u8) with Rust's saturating truncation.
+__device__ __forceinline__ uint32_t cast_u8(float v) {
+  if (v != v || v <= 0.0f) return 0u;
+  if (v >= 255.0f) return 255u;
+  return (uint32_t)v;
+}
+
+__global__ void q4_0_quantize_kernel(const float* w, size_t nblocks, uint8_t* qs, uint16_t* d) {
+  size_t blk = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (blk >= nblocks) return;
+  const float* x = w + blk * 32;
+  float amax = 0.0f, mx = 0.0f;
+  for (int j = 0; j < 32; ++j) {
+    const float a = fabsf(x[j]);
+    if (amax < a) {
+      amax = a;
+      mx = x[j];
+    }
+  }
+  const float dd = mx / -8.0f;
+  const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+  d[blk] = f32_to_f16(dd);
+  for (int j = 0; j < 16; ++j) {
+    const float x0 = x[j] * id, x1 = x[j + 16] * id;
+    const uint32_t q0 = min(15u, cast_u8(x0 + 8.5f)), q1 = min(15u, cast_u8(x1 + 8.5f));
+    qs[blk * 16 + j] = (uint8_t)(q0 | (q1 << 4));
+  }
+}
+
+hipError_t launch_q4_0_quantize(const float* w, int rows, int K, uint8_t* qs, uint16_t* d, hipStream_t s) {
+  size_t nb = (size_t)rows * (K / 32);
+  hipLaunchKernelGGL(q4_0_quantize_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, w, nb, qs, d);
+  return hipGetLastError();
+}
+
+// 18-byte candle blocks <-> split codes and scales.
+__global__ void q4_0_from_blocks_kernel(const uint8_t* blocks, size_t nblocks, uint8_t* qs, uint16_t* d) {
+  size_t blk = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (blk >= nblocks) return;
+  const uint8_t* p = blocks + blk * 18;
+  d[blk] = (uint16_t)(p[0] | (p[1] << 8));
+  for (int j = 0; j < 16; ++j) qs[blk * 16 + j] = p[2 + j];
+}
+
+hipError_t launch_q4_0_from_blocks(const uint8_t* blocks, int rows, int K, uint8_t* qs, uint16_t* d, hipStream_t s) {
+  size_t nb = (size_t)rows * (K / 32);
+  hipLaunchKernelGGL(q4_0_from_blocks_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, blocks, nb, qs, d);
+  return hipGetLastError();
+}
+
+__global__ void q4_0_to_blocks_kernel(const uint8_t* qs, const uint16_t* d, size_t nblocks, uint8_t* blocks) {
+  size_t blk = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (blk >= nblocks) return;
+  uint8_t* p = blocks + blk * 18;
+  p[0] = (uint8_t)(d[blk] & 0xff);
+  p[1] = (uint8_t)(d[blk] >> 8);
+  for (int j = 0; j < 16; ++j) p[2 + j] = qs[blk * 16 + j];
+}
+
+hipError_t launch_q4_0_to_blocks(const uint8_t* qs, const uint16_t* d, int rows, int K, uint8_t* blocks, hipStream_t s) {
+  size_t nb = (size_t)rows * (K / 32);
+  hipLaunchKernelGGL(q4_0_to_blocks_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, qs, d, nb, blocks);
   return hipGetLastError();
 }
 
@@ -812,6 +883,13 @@ __global__ void dequant_kernel(LinearDev L, float* out) {
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   if (L.fmt == FMT_Q8_0) out[i] = (float)((const int8_t*)L.w)[i] * f16_to_f32(L.scale[i / 32]);
+  else if (L.fmt == FMT_Q4_0) {
+    const size_t blk = i / 32;
+    const int e = (int)(i % 32);
+    const uint8_t byte = ((const uint8_t*)L.w)[blk * 16 + (e & 15)];
+    const int code = e < 16 ? (byte & 0xF) : (byte >> 4);
+    out[i] = (float)(code - 8) * f16_to_f32(L.scale[blk]);
+  }
   else if (L.fmt == FMT_Q4K) out[i] = q4k_value((const uint8_t*)L.w + (i / 256) * 144, (int)(i % 256));
   else if (L.fmt == FMT_BF16) out[i] = bf16_to_f32(((const uint16_t*)L.w)[i]);
   else if (L.fmt == FMT_BF16C) out[i] = bf16_to_f32(((const uint16_t*)L.w)[chain_index(i / L.in, (int)(i % L.in), L.in, 8)]);

@@ -401,8 +401,10 @@ __device__ __forceinline__ void norm_row4(v4f (&v)[KU], int K, int norm, const N
 // q_i = round(x_i * id).  The block maximum runs over 8 lanes (after each lane's maximum of its
 // four elements); every lane then computes its block's d and id and writes its four quantized
 // elements as one word; lane 0 of the 8 writes the block scale.
+// With `xsum` (Q4_0 weights), lane 0 of the 8 also writes the block's sum of quantized values
+// (exact), which the Q4_0 dot subtracts 8 times: sum (code - 8) q = sum code q - 8 sum q.
 template <int KU>
-__device__ __forceinline__ void quantize_row4(const v4f (&v)[KU], int K, int8_t* xq, float* xdq) {
+__device__ __forceinline__ void quantize_row4(const v4f (&v)[KU], int K, int8_t* xq, float* xdq, int* xsum = nullptr) {
   const int nc = K / 4;
   uint32_t m[KU];
 #pragma unroll
@@ -428,7 +430,15 @@ __device__ __forceinline__ void quantize_row4(const v4f (&v)[KU], int K, int8_t*
     const uint32_t q1 = (uint32_t)sat_i8(roundf(v[u].y * idm)) & 0xffu;
     const uint32_t q2 = (uint32_t)sat_i8(roundf(v[u].z * idm)) & 0xffu;
     const uint32_t q3 = (uint32_t)sat_i8(roundf(v[u].w * idm)) & 0xffu;
-    ((uint32_t*)xq)[c] = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+    const uint32_t word = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+    ((uint32_t*)xq)[c] = word;
+    if (xsum) {  // uniform
+      int bs = __builtin_amdgcn_sdot4((int)word, 0x01010101, 0, false);
+      bs += __builtin_amdgcn_update_dpp(0, bs, 0xB1, 0xf, 0xf, false);
+      bs += __builtin_amdgcn_update_dpp(0, bs, 0x4E, 0xf, 0xf, false);
+      bs += __builtin_amdgcn_update_dpp(0, bs, 0x141, 0xf, 0xf, false);
+      if ((c & 7) == 0) xsum[c / 8] = bs;
+    }
   }
 }
 
@@ -600,12 +610,13 @@ __device__ __forceinline__ Q8Geom q8_geom(int K, int items, int ipw, int parts, 
   return g;
 }
 
-// LDS of a Q8_0 unit: xs [norm_scratch_floats(K)] f32 | xq [K] int8 | xdq [nb, padded to 4] f32 |
-// T [2 ipw][q8_row_stride(nb)] f32 | Y [2 ipw] f32.
+// LDS of a Q8_0 / Q4_0 unit: xs [norm_scratch_floats(K)] f32 | xq [K] int8 | xdq [nb, padded to 4]
+// f32 | xsum [nb, padded to 4] i32 (Q4_0) | T [2 ipw][q8_row_stride(nb)] f32 | Y [2 ipw] f32.
 struct Q8Lds {
   float* xs;
   int8_t* xq;
   float* xdq;
+  int* xsum;
   float* T;
   float* Y;
 };
@@ -615,7 +626,8 @@ __device__ __forceinline__ Q8Lds q8_lds(unsigned char* smem, int K, int nb, int 
   l.xs = (float*)smem;
   l.xq = (int8_t*)(l.xs + norm_scratch_floats(K));
   l.xdq = (float*)(l.xq + K);
-  l.T = l.xdq + ((nb + 3) & ~3);
+  l.xsum = (int*)(l.xdq + ((nb + 3) & ~3));
+  l.T = (float*)(l.xsum + ((nb + 3) & ~3));
   l.Y = l.T + 2 * ipw * q8_row_stride(nb);
   return l;
 }
@@ -641,7 +653,7 @@ __device__ __forceinline__ void gemv_q8_rows(const GemvArgs& a, int unit, const 
   }
   // the weight waves have read the previous item's quantized row
   lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
-  quantize_row4(v, g.K, l.xq, l.xdq);
+  quantize_row4(v, g.K, l.xq, l.xdq, a.L.fmt == FMT_Q4_0 ? l.xsum : nullptr);
   lds_signal(&rs.ws->xq_parts);
   // one thread per row adds the row's terms in block order once every term is written
   const bool many = g.NR > kWave;  // uniform
@@ -665,6 +677,7 @@ struct WItem {
   Q8Geom g;
   int ipw;
   int maxb;
+  int q4;  // Q4_0 weights: one 16-byte load of codes per block (wa)
   v4i wa[kWBlocks], wb[kWBlocks];
   uint32_t wd[kWBlocks];
 };
@@ -674,10 +687,11 @@ struct WItem {
 // The geometry the requests need: K, items (output rows, or gate/value pairs: then also the offset
 // of the value rows), rows per unit, units per batch row, blocks per thread, the epilogue kind.
 __device__ __forceinline__ void w_issue_at(const int8_t* wq, const uint16_t* sc, int K, int items, int ipw, int parts,
-                                           int maxb, int epi, int unit, WItem& it) {
+                                           int maxb, int epi, int unit, WItem& it, int q4 = 0) {
   const int ff_hidden = items;  // read by gemv_phys_row for the SiLU gate only, where items = ff_hidden
   it.ipw = ipw;
   it.maxb = maxb;
+  it.q4 = q4;
   it.g = q8_geom(K, items, ipw, parts, epi == EPI_SILU_GATE, unit);
   const int nb = it.g.nb;
   const int w = threadIdx.x - kRowThreads;
@@ -688,9 +702,13 @@ __device__ __forceinline__ void w_issue_at(const int8_t* wq, const uint16_t* sc,
     if (k >= it.maxb) break;  // uniform
     if (w + k * kWeightThreads < it.g.total) {
       const size_t row = (size_t)gemv_phys_row(epi, ff_hidden, it.g.i0, it.g.ni, r);
-      const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
-      it.wa[k] = ldg_stream(wp);
-      it.wb[k] = ldg_stream(wp + 1);
+      if (q4) {  // uniform
+        it.wa[k] = ldg_stream((const v4i*)(wq + row * (K / 2) + (size_t)blk * 16));
+      } else {
+        const v4i* wp = (const v4i*)(wq + row * K + (size_t)blk * 32);
+        it.wa[k] = ldg_stream(wp);
+        it.wb[k] = ldg_stream(wp + 1);
+      }
       it.wd[k] = ldg(sc + row * nb + blk);
     }
     r += dr;
@@ -706,10 +724,12 @@ __device__ __forceinline__ void w_issue(const Phase* ph, int unit, WItem& it) {
   const int epi = ld_const(&ph->g.epi);
   const int items = epi == EPI_SILU_GATE ? ld_const(&ph->g.ff_hidden) : ld_const(&ph->g.L.out);
   w_issue_at((const int8_t*)ld_const(&ph->g.L.w), (const uint16_t*)ld_const(&ph->g.L.scale), ld_const(&ph->g.L.in),
-             items, ld_const(&ph->g.ipw), ld_const(&ph->g.parts), ld_const(&ph->g.maxb), epi, unit, it);
+             items, ld_const(&ph->g.ipw), ld_const(&ph->g.parts), ld_const(&ph->g.maxb), epi, unit, it,
+             ld_const(&ph->g.L.fmt) == FMT_Q4_0);
 }
 
-// The item's block terms T[r][blk] = ((f32)(sum qw * qx) * d_w) * d_x into LDS.
+// The item's block terms T[r][blk] = ((f32)(sum qw * qx) * d_w) * d_x into LDS; for Q4_0 weights
+// qw = code - 8, and the exact sum is sum code * qx - 8 sum qx.
 __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
   const Q8Lds l = q8_lds(smem, it.g.K, it.g.nb, it.ipw);
   const int rs = q8_row_stride(it.g.nb);
@@ -723,14 +743,28 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
     if (w + k * kWeightThreads < it.g.total) {
       const v4i xa = *(const v4i*)(l.xq + blk * 32);
       const v4i xb = *(const v4i*)(l.xq + blk * 32 + 16);
-      int s = sdot4(it.wa[k].x, xa.x, 0);
-      s = sdot4(it.wa[k].y, xa.y, s);
-      s = sdot4(it.wa[k].z, xa.z, s);
-      s = sdot4(it.wa[k].w, xa.w, s);
-      s = sdot4(it.wb[k].x, xb.x, s);
-      s = sdot4(it.wb[k].y, xb.y, s);
-      s = sdot4(it.wb[k].z, xb.z, s);
-      s = sdot4(it.wb[k].w, xb.w, s);
+      int s;
+      if (it.q4) {  // uniform: low nibbles are elements 0-15, high nibbles 16-31
+        const int m = 0x0F0F0F0F;
+        s = sdot4(it.wa[k].x & m, xa.x, 0);
+        s = sdot4(it.wa[k].y & m, xa.y, s);
+        s = sdot4(it.wa[k].z & m, xa.z, s);
+        s = sdot4(it.wa[k].w & m, xa.w, s);
+        s = sdot4((it.wa[k].x >> 4) & m, xb.x, s);
+        s = sdot4((it.wa[k].y >> 4) & m, xb.y, s);
+        s = sdot4((it.wa[k].z >> 4) & m, xb.z, s);
+        s = sdot4((it.wa[k].w >> 4) & m, xb.w, s);
+        s -= 8 * l.xsum[blk];
+      } else {
+        s = sdot4(it.wa[k].x, xa.x, 0);
+        s = sdot4(it.wa[k].y, xa.y, s);
+        s = sdot4(it.wa[k].z, xa.z, s);
+        s = sdot4(it.wa[k].w, xa.w, s);
+        s = sdot4(it.wb[k].x, xb.x, s);
+        s = sdot4(it.wb[k].y, xb.y, s);
+        s = sdot4(it.wb[k].z, xb.z, s);
+        s = sdot4(it.wb[k].w, xb.w, s);
+      }
       const float t = (float)s * f16_to_f32((uint16_t)it.wd[k]);
       l.T[r * rs + blk] = t * l.xdq[blk];
     }
@@ -1024,7 +1058,7 @@ __device__ __forceinline__ void w_terms_q4k(const WItemQ4& it, unsigned char* sm
 __device__ __forceinline__ bool is_split_gemv(const Phase* ph) {
   if (ld_const(&ph->kind) != PH_GEMV) return false;
   const int fmt = ld_const(&ph->g.L.fmt);
-  return fmt == FMT_Q8_0 || fmt == FMT_Q4K || fmt == FMT_F32C || fmt == FMT_BF16C;
+  return fmt == FMT_Q8_0 || fmt == FMT_Q4_0 || fmt == FMT_Q4K || fmt == FMT_F32C || fmt == FMT_BF16C;
 }
 
 // ---- batched Q8_0 GEMM (lockstep batches; row waves) ----------------------------------------------
@@ -1987,7 +2021,7 @@ constexpr unsigned kMiscKinds = kind_bit(PH_EMBED) | kind_bit(PH_ARGMAX) | kind_
 template <unsigned F, unsigned KM = kAllKinds, int V = 0>
 __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, int step, int unit, const int* spos,
                                          unsigned char* smem, RowSync& rs, unsigned& item) {
-  if ((F & FAM_Q8) && ph.kind == PH_GEMV && ph.g.L.fmt == FMT_Q8_0) {
+  if ((F & FAM_Q8) && ph.kind == PH_GEMV && (ph.g.L.fmt == FMT_Q8_0 || ph.g.L.fmt == FMT_Q4_0)) {
     if constexpr (V != 0) gemv_q8_rows<V>(ph.g, unit, spos, smem, rs, item);
     else switch (row_slots(ph.g.L.in)) {
       case 2: gemv_q8_rows<2>(ph.g, unit, spos, smem, rs, item); break;

@@ -280,6 +280,23 @@ int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string&
     L->w = w;
     return 0;
   }
+  if (t->dtype == SVL_Q4_0) {
+    if (in_f % 32) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: Q4_0 needs in %% 32 == 0", name.c_str());
+    void *qs, *d, *tmp;
+    TRY(m->alloc(&qs, count / 2));
+    TRY(m->alloc(&d, count / 32 * 2));
+    HIP_TRY(hipMalloc(&tmp, count / 32 * 18));
+    HIP_TRY(hipMemcpy(tmp, t->data, count / 32 * 18, hipMemcpyHostToDevice));
+    hipError_t e = launch_q4_0_from_blocks((const uint8_t*)tmp, out_f, in_f, (uint8_t*)qs, (uint16_t*)d, m->stream);
+    hipError_t e2 = hipStreamSynchronize(m->stream);
+    hipFree(tmp);
+    HIP_TRY(e);
+    HIP_TRY(e2);
+    L->fmt = FMT_Q4_0;
+    L->w = qs;
+    L->scale = (uint16_t*)d;
+    return 0;
+  }
   if (t->dtype == SVL_Q8_0) {
     if (in_f % 32) return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: Q8_0 needs in %% 32 == 0", name.c_str());
     void *qs, *d, *tmp;
@@ -313,6 +330,26 @@ int load_linear(svl_model* m, const svl_tensor* ts, size_t n, const std::string&
     m->allocs.push_back(w);
     L->fmt = FMT_Q4K;
     L->w = w;
+    return 0;
+  }
+  if (quantize == SVL_Q4_0 && in_f % 32 == 0) {
+    float* f = nullptr;
+    TRY(upload_f32(m, t, count, &f));
+    void *qs, *d;
+    TRY(m->alloc(&qs, count / 2));
+    TRY(m->alloc(&d, count / 32 * 2));
+    HIP_TRY(launch_q4_0_quantize(f, out_f, in_f, (uint8_t*)qs, (uint16_t*)d, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    // the f32 staging copy is released right away
+    m->allocs.pop_back();
+    m->allocs.pop_back();
+    m->allocs.pop_back();
+    hipFree(f);
+    m->allocs.push_back(qs);
+    m->allocs.push_back(d);
+    L->fmt = FMT_Q4_0;
+    L->w = qs;
+    L->scale = (uint16_t*)d;
     return 0;
   }
   if (quantize == SVL_Q8_0 && in_f % 32 == 0) {
@@ -591,6 +628,8 @@ int check_config(const svl_config* c) {
   if (c->ff_kind != SVL_FF_PLAIN_GELU && c->ff_kind != SVL_FF_GATED_SILU) return set_error(SVL_ERR_CONFIG, "unknown feed-forward");
   if (c->context < 0) return set_error(SVL_ERR_CONFIG, "context must be >= 0");
   if (c->kv_dtype != SVL_F32 && c->kv_dtype != SVL_BF16) return set_error(SVL_ERR_CONFIG, "kv_dtype must be F32 or BF16");
+  if (c->quantize != 0 && c->quantize != SVL_Q8_0 && c->quantize != SVL_Q4_0 && c->quantize != SVL_Q4K)
+    return set_error(SVL_ERR_CONFIG, "quantize must be 0, Q8_0, Q4_0 or Q4K");
   if (c->kind == SVL_MODEL_STT && (c->n_q <= 0 || c->card <= 0 || c->text_card <= 0))
     return set_error(SVL_ERR_CONFIG, "invalid STT heads");
   if (c->kind == SVL_MODEL_TTS && c->latent_dim <= 0) return set_error(SVL_ERR_CONFIG, "invalid TTS latent_dim");
@@ -1500,6 +1539,15 @@ static int model_linear_weight_impl(const svl_model* m, const char* name, float*
     uint8_t* tmp;
     HIP_TRY(hipMalloc(&tmp, block_bytes));
     hipError_t e = launch_q4k_to_blocks((const uint8_t*)L->w, L->out, L->in, tmp, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e == hipSuccess) e = hipMemcpy(blocks, tmp, block_bytes, hipMemcpyDeviceToHost);
+    hipFree(tmp);
+    HIP_TRY(e);
+  } else if (blocks && L->fmt == FMT_Q4_0) {
+    if (block_bytes != n / 32 * 18) return set_error(SVL_ERR_INVALID_INPUT, "block buffer size mismatch");
+    uint8_t* tmp;
+    HIP_TRY(hipMalloc(&tmp, block_bytes));
+    hipError_t e = launch_q4_0_to_blocks((const uint8_t*)L->w, L->scale, L->out, L->in, tmp, m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (e == hipSuccess) e = hipMemcpy(blocks, tmp, block_bytes, hipMemcpyDeviceToHost);
     hipFree(tmp);

@@ -28,7 +28,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB_PATH = os.environ.get("SVL_LIBRARY") or os.path.join(PKG, "lib", "libsvl.so")
 
-F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
+F32, BF16, F16, Q8_0, Q4K, Q4_0 = 0, 1, 2, 3, 4, 5
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN_GELU, FF_GATED_SILU = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
@@ -208,13 +208,13 @@ class Model:
         self.close()
 
     def linear_weight(self, name: str):
-        """(dequantized f32 [out, in], candle Q8_0 or Q4K block bytes [out, ...] or None) as held
-        on the GPU."""
+        """(dequantized f32 [out, in], candle Q8_0, Q4_0 or Q4K block bytes [out, ...] or None)
+        as held on the GPU."""
         out, inp = self._linear_shape(name)
         w = np.empty((out, inp), dtype=np.float32)
         L = load_library()
         _check(L.svl_model_linear_weight(self.h, name.encode(), _p(w), w.size, None, 0))
-        for values, nbytes in ((32, 34), (256, 144)):  # Q8_0, Q4K
+        for values, nbytes in ((32, 34), (32, 18), (256, 144)):  # Q8_0, Q4_0, Q4K
             if inp % values:
                 continue
             b = np.empty(out * inp // values * nbytes, dtype=np.uint8)

@@ -22,7 +22,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-F32, BF16, F16, Q8_0, Q4K = 0, 1, 2, 3, 4
+F32, BF16, F16, Q8_0, Q4K, Q4_0 = 0, 1, 2, 3, 4, 5
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN, FF_GATED = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
@@ -205,7 +205,7 @@ def make_weights(s: Shape, dtype: str, seed: int = 0, threads: int | None = None
     """name -> (dtype code, shape, ndarray) for the oracle and for libsvl.
 
     dtype "f32": everything f32.  "bf16": everything bf16 (stored as bf16 bits).
-    "q8_0"/"q4k": linear weights f32 (quantized by the model), the rest bf16.
+    "q8_0"/"q4_0"/"q4k": linear weights f32 (quantized by the model), the rest bf16.
     Tensors are drawn in parallel threads (each has its own generator, so the result does not
     depend on the thread count)."""
     from concurrent.futures import ThreadPoolExecutor
@@ -224,7 +224,7 @@ def make_weights(s: Shape, dtype: str, seed: int = 0, threads: int | None = None
             x = normal(seed, name, shape, 0.02, 1.0 if "layer_scale" in name else 0.0)
         else:
             x = normal(seed, name, shape, 0.02)
-        if dtype == "f32" or role == "flow_linear" or (dtype in ("q8_0", "q4k") and role in ("linear", "dense_linear")):
+        if dtype == "f32" or role == "flow_linear" or (dtype in ("q8_0", "q4_0", "q4k") and role in ("linear", "dense_linear")):
             return name, (F32, shape, x)
         return name, (BF16, shape, to_bf16_bits(x))
 
@@ -235,7 +235,7 @@ def make_weights(s: Shape, dtype: str, seed: int = 0, threads: int | None = None
 
 
 def quantize_code(dtype: str) -> int:
-    return {"f32": 0, "bf16": 0, "q8_0": Q8_0, "q4k": Q4K}[dtype]
+    return {"f32": 0, "bf16": 0, "q8_0": Q8_0, "q4_0": Q4_0, "q4k": Q4K}[dtype]
 
 
 def audio_tokens(s: Shape, steps: int, seed: int = 1, batch: int = 1) -> np.ndarray:
@@ -270,6 +270,8 @@ def linear_bytes(s: Shape, dtype: str) -> int:
             total += n * (2 if dtype == "bf16" else 4)
         elif dtype == "q8_0" and shape[1] % 32 == 0:
             total += n // 32 * 34
+        elif dtype == "q4_0" and shape[1] % 32 == 0:
+            total += n // 32 * 18
         elif dtype == "q4k" and shape[1] % 256 == 0:
             total += n // 256 * 144
         elif dtype == "bf16":

@@ -323,3 +323,75 @@ def test_q4k_codes_are_nearest_grid_points():
             best = dist.min(axis=1)
             got = np.abs(xs[b, j] - deq[b, j])
             assert np.all(got <= best + 1e-6 * step), (b, j)
+
+
+# ---- Q4_0 (candle BlockQ4_0; SVL/nn/mod.rs:76-87 quantizes with the block type chosen there) ----
+# Each expected block below is derived by hand from the GGML rule (max = the first value of
+# largest magnitude, d = max / -8 kept as f16, code = min(15, trunc(x / d + 8.5)), byte j = code
+# of element j | code of element j + 16 << 4), in the comments.
+
+def _q40(x):
+    return oracle.quantize_q4_0(np.asarray(x, dtype=np.float32).reshape(1, 32))[0]
+
+
+def _block(d_bits, codes):
+    codes = list(codes)
+    qs = [codes[j] | (codes[j + 16] << 4) for j in range(16)]
+    return np.array([d_bits & 0xFF, d_bits >> 8] + qs, dtype=np.uint8)
+
+
+def test_q4_0_known_answer_blocks():
+    # all zero: max = 0, d = 0 / -8 = -0.0 (f16 0x8000), id = 0, every code trunc(8.5) = 8
+    assert np.array_equal(_q40(np.zeros(32)), _block(0x8000, [8] * 32))
+    # integers -8..7 then 7..-8: max = -8 (element 0; element 31 ties later), d = 1, code = x + 8
+    x = [j - 8 for j in range(16)] + [7 - j for j in range(16)]
+    assert np.array_equal(_q40(x), _block(0x3C00, [j for j in range(16)] + [15 - j for j in range(16)]))
+    # ties of magnitude: the first wins.  8 then -8: d = -1, codes 0 and trunc(16.5) -> 15
+    x = [8.0, -8.0] + [0.0] * 30
+    assert np.array_equal(_q40(x), _block(0xBC00, [0, 15] + [8] * 30))
+    # -8 then 8: d = +1, codes 0 and 15 (16 clamped): the same codes, the other scale
+    x = [-8.0, 8.0] + [0.0] * 30
+    assert np.array_equal(_q40(x), _block(0x3C00, [0, 15] + [8] * 30))
+    # truncation, not rounding (d = 1): -0.5 -> trunc(8.0) = 8, -1.5 -> 7, 0.5 -> 9, 0.49 -> 8,
+    # -0.51 -> 7, 7.6 -> trunc(16.1) = 16 -> 15, 6.4 -> 14
+    x = [-8.0, -0.5, -1.5, 0.5, 0.49, -0.51, 7.6, 6.4] + [0.0] * 24
+    assert np.array_equal(_q40(x), _block(0x3C00, [0, 8, 7, 9, 8, 7, 15, 14] + [8] * 24))
+    # a fractional scale: max = 3 -> d = -0.375 (f16 0xB600), id = -8/3 in f32; 3 -> code 0,
+    # -1.5 -> trunc(4 + 8.5) = 12, 0 -> 8
+    x = [3.0, -1.5] + [0.0] * 30
+    assert np.array_equal(_q40(x), _block(0xB600, [0, 12] + [8] * 30))
+
+
+def test_q4_0_dequantize_closed_form():
+    rng = np.random.default_rng(40)
+    x = rng.standard_normal((8, 64)).astype(np.float32)
+    b = oracle.quantize_q4_0(x).reshape(8, 2, 18)
+    d = b[:, :, :2].copy().view(np.float16).astype(np.float32)  # [8, 2, 1]
+    qs = b[:, :, 2:]
+    codes = np.concatenate([qs & 0xF, qs >> 4], axis=-1).astype(np.float32)  # [8, 2, 32]
+    want = ((codes - 8) * d).reshape(8, 64)
+    assert np.array_equal(oracle.dequantize_q4_0(b.reshape(8, 36), 64), want)
+    # every code is the nearest-or-truncated point of its block's grid: |x - value| <= |d|
+    assert np.all(np.abs(x - want) <= np.abs(d).repeat(32, axis=-1).reshape(8, 64) * 1.0000001)
+
+
+def test_q4_0_vec_dot_is_the_exact_block_sum():
+    """vec_dot = sum over blocks of ((sum (code - 8) q) * d_w) * d_x: with power-of-two scales and
+    small integers every product and partial sum is exact, so it equals the dot of the
+    dequantized blocks in float64."""
+    rng = np.random.default_rng(41)
+    nb = 6
+    codes = rng.integers(0, 16, size=(nb, 32))
+    w = np.zeros((nb, 18), np.uint8)
+    x = np.zeros((nb, 34), np.uint8)
+    wd = rng.choice([0.25, 0.5, 1.0, 2.0], nb).astype(np.float16)
+    xd = rng.choice([0.125, 0.5, 1.0], nb).astype(np.float16)
+    xq = rng.integers(-127, 128, size=(nb, 32)).astype(np.int8)
+    w[:, :2] = wd.view(np.uint8).reshape(nb, 2)
+    w[:, 2:] = (codes[:, :16] | (codes[:, 16:] << 4)).astype(np.uint8)
+    x[:, :2] = xd.view(np.uint8).reshape(nb, 2)
+    x[:, 2:] = xq.view(np.uint8)
+    want = float(np.sum((codes - 8) * wd[:, None].astype(np.float64) * xq * xd[:, None].astype(np.float64)))
+    assert oracle.vec_dot_q4_0_q8_0(w, x, nb * 32) == want
+    # the offset matters: codes read without "- 8" give another value
+    assert want != float(np.sum(codes * wd[:, None].astype(np.float64) * xq * xd[:, None].astype(np.float64)))
