@@ -184,6 +184,33 @@ int svl_stt_recognize_heads_async(const svl_model* model, svl_state* state, int6
                                   const uint32_t* d_audio_tokens, uint32_t* d_out_tokens,
                                   float* d_out_probs);
 
+/* TurnDetector's parameters (SVL/stt/mod.rs:283-325): `threshold` (default 0.5), `frames`
+ * (consecutive frames above it that end a turn; default 1, values below 1 count as 1) and `head`
+ * (the extra head whose first-class probability is read; TurnDetector::HEAD = 2). */
+typedef struct {
+    float threshold;
+    int32_t frames;
+    int32_t head;
+} svl_turn_config;
+
+/* svl_stt_recognize_heads with the end-of-turn signal computed on the device: for every step and
+ * stream, out_turn_ends [n_steps][batch] = TurnDetector::update (SVL/stt/mod.rs:327-350) over
+ * the step's events in the recognizer's order (:566-589): the VoiceActivity event of the extra
+ * heads' probabilities (when the model has extra heads), then the Word events -- a padding token
+ * (0 = end of padding, 3 = padding) after pending word tokens (ids above 3) emits them; the
+ * tokenizer is taken to decode such a run to at least one word.  The recognizer's pending word
+ * tokens and the detector's state are kept per stream in the state (cleared by svl_state_reset);
+ * the detector's part changes only in calls that ask for turn ends.  out_probs may be NULL.  The
+ * probabilities are within a few ulp of the C library's softmax, so a frame whose probability is
+ * that close to the threshold may count differently.  Host pointers. */
+int svl_stt_recognize_turns(const svl_model* model, svl_state* state, int64_t n_steps, const uint32_t* audio_tokens,
+                            const svl_turn_config* turn, uint32_t* out_tokens, float* out_probs,
+                            int32_t* out_turn_ends);
+/* The same with device pointers, enqueued on the state's stream; d_out_probs may be NULL. */
+int svl_stt_recognize_turns_async(const svl_model* model, svl_state* state, int64_t n_steps,
+                                  const uint32_t* d_audio_tokens, const svl_turn_config* turn,
+                                  uint32_t* d_out_tokens, float* d_out_probs, int32_t* d_out_turn_ends);
+
 /* svl_stt_recognize without any allocation: no counterpart in the reference; for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  The device copies of the audio and output tokens go through a

@@ -135,6 +135,11 @@ def lib():
             L.svlo_stt_step.restype = C.c_int
             L.svlo_stt_greedy.argtypes = [vp, vp, C.c_int64, vp, vp, vp, vp]
             L.svlo_tts_step.argtypes = [vp, vp, vp, vp, C.c_int, vp, vp]
+            L.svlo_turn_init.argtypes = [vp, C.c_float, C.c_int, C.c_int]
+            L.svlo_turn_init.restype = None
+            L.svlo_turn_word.argtypes = [vp]
+            L.svlo_turn_activity.argtypes = [vp, vp, C.c_int]
+            L.svlo_turn_step.argtypes = [vp, C.c_uint32, vp, C.c_int]
             L.svlo_tts_step.restype = C.c_int
             L.svlo_model_flow.argtypes = [vp]
             L.svlo_model_flow.restype = vp
@@ -388,6 +393,33 @@ def softmax_first(x) -> float:
 def argmax(x) -> int:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return int(lib().svlo_argmax(_p(x), x.size))
+
+
+# ---- turns (the recognizer's word events and TurnDetector, SVL/stt/mod.rs:283-351, 564-590) ------
+
+class _Turn(C.Structure):
+    _fields_ = [("threshold", C.c_float), ("frames", C.c_int32), ("head", C.c_int32),
+                ("above", C.c_int64), ("in_turn", C.c_int32), ("pending", C.c_int32)]
+
+
+class TurnDetector:
+    """TurnDetector (threshold 0.5, frames 1, HEAD 2 by default) with the recognizer's pending
+    word tokens."""
+
+    def __init__(self, threshold: float = 0.5, frames: int = 1, head: int = 2):
+        self.t = _Turn()
+        lib().svlo_turn_init(C.byref(self.t), threshold, frames, head)
+
+    def word(self) -> bool:
+        return bool(lib().svlo_turn_word(C.byref(self.t)))
+
+    def activity(self, probs) -> bool:
+        p = np.ascontiguousarray(probs, dtype=np.float32)
+        return bool(lib().svlo_turn_activity(C.byref(self.t), _p(p), p.size))
+
+    def step(self, token: int, probs) -> bool:
+        p = np.ascontiguousarray(probs, dtype=np.float32)
+        return bool(lib().svlo_turn_step(C.byref(self.t), token, _p(p) if p.size else None, p.size))
 
 
 # ---- model -------------------------------------------------------------------------------------

@@ -166,6 +166,19 @@ int svlo_tts_backbone_step(const svlo_model* m, svlo_state* s, const float* late
 int svlo_tts_step(const svlo_model* m, svlo_state* s, const float* latent, const float* noise, int decode_steps,
                   float* out_latent, float* out_eos_logit);
 
+/* ---- turns (turns.c): the recognizer's word events and TurnDetector ---------------------- */
+typedef struct {
+    float threshold;
+    int32_t frames, head;
+    int64_t above;        /* consecutive frames above the threshold */
+    int32_t in_turn;      /* words came since the last end of turn */
+    int32_t pending;      /* the recognizer holds word tokens not yet emitted */
+} svlo_turn;
+void svlo_turn_init(svlo_turn* t, float threshold, int frames, int head);
+int svlo_turn_word(svlo_turn* t);
+int svlo_turn_activity(svlo_turn* t, const float* probs, int n);
+int svlo_turn_step(svlo_turn* t, uint32_t token, const float* probs, int n);
+
 /* ---- flow head (flow.c): FlowHead / TimestepEmbedder / ResBlock / out_eos -------------- */
 typedef struct svlo_flow svlo_flow;
 int svlo_flow_create(int dim, int depth, int kind, int latent, int cond, const svlo_tensor* ts, size_t n,

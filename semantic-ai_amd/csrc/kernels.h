@@ -108,6 +108,10 @@ struct ArgmaxArgs {
   const float* xlogits;     // [B][nh * hd]
   int nh, hd;
   float* xprob;             // [B][nh], the last step's probabilities
+  // per stream: bit 0 = the recognizer holds word tokens not yet emitted, bit 1 = the turn
+  // detector's in_turn, bits 2.. = its count of consecutive frames above the threshold; then the
+  // detector's parameters of the current call: threshold (f32 bits), frames (>= 1), head
+  uint32_t* turn_state;     // [B + 3]
 };
 
 struct NormArgs {           // y[b] = norm(x[b]) (TTS out_norm without z_proj)
@@ -174,6 +178,7 @@ struct StepParams {
   const float* fwd_in;           // [B][T][d], step s reads column s
   float* fwd_out;
   int fwd_T;
+  int32_t* out_turn;             // step s: out_turn + s * B (turn ends), or null: no turn detector
 };
 
 constexpr int kStepThreads = 1024;                       // workgroup of the step kernels

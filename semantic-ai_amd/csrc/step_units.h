@@ -1912,8 +1912,39 @@ __device__ __forceinline__ void gather_unit(const EmbedArgs& a, const uint32_t* 
 }
 
 // argmax over logits[b] (first index of the maximum); unit = stream.
+// The recognizer's word events and TurnDetector::update (SVL/stt/mod.rs:327-350, 566-589) for one
+// step of stream b: the step's VoiceActivity event (when the model has extra heads), then its Word
+// events -- a padding token (END_OF_PADDING 0 or PADDING 3) after pending word tokens (> 3) emits
+// them (the tokenizer is taken to decode a pending run to at least one word).  `prob` is the
+// probability at the detector's head.  Returns whether the step ends a turn.  The detector's part
+// of the state changes only when `turns` (a call that reads turn ends), the recognizer's always.
+__device__ __forceinline__ int turn_update(uint32_t& st, uint32_t token, bool turns, bool activity, float prob,
+                                           float threshold, int frames) {
+  bool pending = st & 1u, in_turn = (st >> 1) & 1u;
+  uint32_t above = st >> 2;
+  int end = 0;
+  if (turns && activity) {
+    above = prob > threshold ? min(above + 1u, 0x3fffffffu) : 0u;
+    if (in_turn && above >= (uint32_t)frames) {
+      in_turn = false;
+      end = 1;
+    }
+  }
+  if (token == 0u || token == 3u) {
+    if (pending) {
+      pending = false;
+      if (turns) in_turn = true;
+    }
+  } else if (token > 3u) {
+    pending = true;
+  }
+  st = (pending ? 1u : 0u) | (in_turn ? 2u : 0u) | (above << 2);
+  return end;
+}
+
+
 __device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, float* out_prob, int unit,
-                                            unsigned char* smem, RowSync& rs) {
+                                            unsigned char* smem, RowSync& rs, int32_t* turn_out = nullptr) {
   float* sv = (float*)smem;
   int* si = (int*)(sv + kRowWaves);
   const int b = unit;
@@ -1964,6 +1995,7 @@ __device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, 
     if (bi == 0x7fffffff) bi = 0;
     st_co(a.fb_tok + b, (uint32_t)bi);
     if (out) st_co(out + b, (uint32_t)bi);
+    ((int*)(si + kRowWaves))[1] = bi;  // for the turn update below
   }
   // Extra heads (SVL/stt/model.rs:259-271): thread kWave + h takes head h's logits through
   // candle-nn's softmax_last_dim as the oracle restates it -- the maximum in index order from
@@ -1982,6 +2014,21 @@ __device__ __forceinline__ void argmax_unit(const ArgmaxArgs& a, uint32_t* out, 
     const float p = first / sum;
     st_co(a.xprob + (size_t)b * a.nh + h, p);
     if (out_prob) st_co(out_prob + (size_t)b * a.nh + h, p);
+    if (turn_out && h == (int)ld_const(a.turn_state + a.B + 2)) ((float*)(si + kRowWaves))[0] = p;
+  }
+  if (a.turn_state) {
+    rs.sync();  // the token and the head's probability are in LDS (after si)
+    if (threadIdx.x == 0) {
+      uint32_t st = ld_co(a.turn_state + b);
+      const float threshold = __uint_as_float(ld_const(a.turn_state + a.B));
+      const int frames = (int)ld_const(a.turn_state + a.B + 1), head = (int)ld_const(a.turn_state + a.B + 2);
+      const bool activity = a.nh > 0, at_head = head >= 0 && head < a.nh;
+      const float* tp = (const float*)(si + kRowWaves);
+      const int end = turn_update(st, (uint32_t)((const int*)tp)[1], turn_out != nullptr, activity,
+                                  at_head ? tp[0] : 0.0f, threshold, frames);
+      st_co(a.turn_state + b, st);
+      if (turn_out) st_co(turn_out + b, (int32_t)end);
+    }
   }
 }
 
@@ -2109,7 +2156,8 @@ __device__ __forceinline__ void run_unit(const Phase& ph, const StepParams& P, i
     case PH_ARGMAX:
       if constexpr (!(KM & kind_bit(PH_ARGMAX))) break;
       argmax_unit(ph.am, P.out_tok ? P.out_tok + (size_t)step * P.out_stride : nullptr,
-                  P.out_prob ? P.out_prob + (size_t)step * P.prob_stride : nullptr, unit, smem, rs);
+                  P.out_prob ? P.out_prob + (size_t)step * P.prob_stride : nullptr, unit, smem, rs,
+                  P.out_turn ? P.out_turn + (size_t)step * P.B : nullptr);
       break;
     case PH_NORM:
       if constexpr (!(KM & kind_bit(PH_NORM))) break;

@@ -170,6 +170,8 @@ struct svl_state {
   float *fh_ce = nullptr, *fh_mod = nullptr, *fh_h = nullptr, *fh_a = nullptr, *fh_x = nullptr, *fh_noise = nullptr;
   float* xlogits = nullptr;   // STT extra heads: logits [B][nh * hd]
   float* xprob = nullptr;     //                  first-class probabilities [B][nh]
+  uint32_t* turn_state = nullptr;  // STT: pending word tokens and turn detector per stream [B], then
+                                   // the detector's threshold, frames and head of the current call
   float* fwd = nullptr;       // transformer forward staging (input then output)
   size_t fwd_cap = 0;
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
@@ -964,6 +966,7 @@ int build_programs(const svl_model* m, svl_state* s) {
     am.am.nh = c.extra_heads_num;
     am.am.hd = c.extra_heads_dim;
     am.am.xprob = s->xprob;
+    am.am.turn_state = s->turn_state;
     am.units = s->B;
     P.push_back(am);
     TRY(upload_program(s, s->stt));
@@ -1217,6 +1220,7 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * (1 + std::max(c.n_q, 0)) * 4), s->tok_in = (uint32_t*)p;
   if (!rc && c.kind == SVL_MODEL_STT)
     rc = s->alloc(&p, (size_t)batch * c.n_q * c.d_model * (m->tables_bf16 ? 2 : 4)), s->stage = p;
+  if (!rc && c.kind == SVL_MODEL_STT) rc = s->alloc(&p, (size_t)(batch + 3) * 4), s->turn_state = (uint32_t*)p;
   if (!rc && c.kind == SVL_MODEL_STT && c.extra_heads_num > 0) {
     rc = s->alloc(&p, (size_t)batch * c.extra_heads_num * c.extra_heads_dim * 4), s->xlogits = (float*)p;
     if (!rc) rc = s->alloc(&p, (size_t)batch * c.extra_heads_num * 4), s->xprob = (float*)p;
@@ -1253,6 +1257,7 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (launch_fill_i32(s->pos, 0, batch, s->stream) != hipSuccess ||
       launch_fill_i32(s->rope_delta, 0, batch, s->stream) != hipSuccess ||
       launch_fill_u32(s->tok_out, 0u, batch + 1, s->stream) != hipSuccess ||
+      (s->turn_state && launch_fill_u32(s->turn_state, 0u, batch + 3, s->stream) != hipSuccess) ||
       launch_fill_u32(s->fb_tok, (uint32_t)std::max(c.text_card, 0), batch, s->stream) != hipSuccess ||
       hipStreamSynchronize(s->stream) != hipSuccess)
     return fail(set_error(SVL_ERR_DEVICE, "state initialisation failed"));
@@ -1411,8 +1416,9 @@ int run_flow_head(svl_state* s, int steps) {
 }
 
 StepParams stt_params(const svl_state* s, const uint32_t* d_audio, const uint32_t* d_text, uint32_t* d_out,
-                       float* d_prob = nullptr) {
+                       float* d_prob = nullptr, int32_t* d_turn = nullptr) {
   StepParams P{};
+  P.out_turn = d_turn;
   P.out_prob = d_prob;
   P.prob_stride = (size_t)s->B * std::max(s->m->cfg.extra_heads_num, 0);
   P.audio = d_audio;
@@ -1585,6 +1591,8 @@ static int state_duplicate_impl(const svl_state* s, svl_state** out) {
   }
   if (e == hipSuccess) e = hipMemcpyAsync(c->pos, s->pos, s->B * sizeof(int), hipMemcpyDeviceToDevice, c->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(c->fb_tok, s->fb_tok, s->B * 4, hipMemcpyDeviceToDevice, c->stream);
+  if (e == hipSuccess && s->turn_state)
+    e = hipMemcpyAsync(c->turn_state, s->turn_state, s->B * 4, hipMemcpyDeviceToDevice, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) {
     delete c;
@@ -1685,6 +1693,7 @@ static int state_reset_impl(svl_state* s) {
   HIP_TRY(launch_fill_i32(s->pos, 0, s->B, s->stream));
   HIP_TRY(launch_fill_u32(s->fb_tok, (uint32_t)std::max(s->m->cfg.text_card, 0), s->B, s->stream));
   HIP_TRY(launch_fill_u32(s->tok_out + s->B, 0u, 1, s->stream));
+  if (s->turn_state) HIP_TRY(launch_fill_u32(s->turn_state, 0u, s->B, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
   s->pos_host.assign(s->B, 0);
   return 0;
@@ -1794,8 +1803,20 @@ static int stt_recognize_async_impl(const svl_model* m, svl_state* s, int64_t n_
   return svl_stt_recognize_heads_async(m, s, n_steps, d_audio_tokens, d_out_tokens, nullptr);
 }
 
+// The turn detector's parameters of a call, written after the streams' states (kernel arguments
+// carry the values: nothing on the host has to outlive the call).
+int set_turn_config(svl_state* s, const svl_turn_config* turn) {
+  uint32_t th;
+  memcpy(&th, &turn->threshold, 4);
+  HIP_TRY(launch_fill_u32(s->turn_state + s->B, th, 1, s->stream));
+  HIP_TRY(launch_fill_u32(s->turn_state + s->B + 1, (uint32_t)std::max(turn->frames, 1), 1, s->stream));  // frames.max(1)
+  HIP_TRY(launch_fill_u32(s->turn_state + s->B + 2, (uint32_t)turn->head, 1, s->stream));
+  return 0;
+}
+
 static int stt_recognize_heads_async_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
-                                  uint32_t* d_out_tokens, float* d_out_probs) {
+                                  uint32_t* d_out_tokens, float* d_out_probs, const svl_turn_config* turn = nullptr,
+                                  int32_t* d_out_turn = nullptr) {
   if (!m || !s || (n_steps > 0 && (!d_audio_tokens || !d_out_tokens)))
     return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
@@ -1804,8 +1825,10 @@ static int stt_recognize_heads_async_impl(const svl_model* m, svl_state* s, int6
   if (n_steps == 0) return 0;
   TRY(check_room(s, n_steps));
   HIP_TRY(hipSetDevice(m->device));
+  if (d_out_turn) TRY(set_turn_config(s, turn));
   return run_program(s, s->stt,
-                     stt_params(s, d_audio_tokens, nullptr, d_out_tokens, m->cfg.extra_heads_num > 0 ? d_out_probs : nullptr),
+                     stt_params(s, d_audio_tokens, nullptr, d_out_tokens, m->cfg.extra_heads_num > 0 ? d_out_probs : nullptr,
+                                d_out_turn),
                      n_steps);
 }
 
@@ -1815,7 +1838,8 @@ static int stt_recognize_impl(const svl_model* m, svl_state* s, int64_t n_steps,
 }
 
 static int stt_recognize_heads_impl(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
-                            uint32_t* out_tokens, float* out_probs) {
+                            uint32_t* out_tokens, float* out_probs, const svl_turn_config* turn = nullptr,
+                            int32_t* out_turn = nullptr) {
   if (!m || !s || (n_steps > 0 && (!audio_tokens || !out_tokens))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
   const svl_config& c = m->cfg;
@@ -1830,8 +1854,12 @@ static int stt_recognize_heads_impl(const svl_model* m, svl_state* s, int64_t n_
   const size_t np = out_probs ? (size_t)n_steps * s->B * std::max(c.extra_heads_num, 0) : 0;
   uint32_t *da, *dout;
   float* dprob = nullptr;
+  const size_t nt = (size_t)n_steps * s->B;
+  if (out_turn) TRY(set_turn_config(s, turn));
   HIP_TRY(hipMalloc(&da, na * 4));
-  hipError_t e = hipMalloc(&dout, (size_t)n_steps * s->B * 4);
+  // the output tokens, then the turn ends when asked for
+  hipError_t e = hipMalloc(&dout, nt * 4 * (out_turn ? 2 : 1));
+  int32_t* dturn = out_turn ? (int32_t*)(dout + nt) : nullptr;
   if (e == hipSuccess && np) {
     e = hipMalloc(&dprob, np * 4);
     if (e != hipSuccess) hipFree(dout);
@@ -1842,9 +1870,9 @@ static int stt_recognize_heads_impl(const svl_model* m, svl_state* s, int64_t n_
   }
   int rc = 0;
   e = hipMemcpyAsync(da, audio_tokens, na * 4, hipMemcpyHostToDevice, s->stream);
-  if (e == hipSuccess) rc = run_program(s, s->stt, stt_params(s, da, nullptr, dout, dprob), n_steps);
-  if (e == hipSuccess && rc == 0)
-    e = hipMemcpyAsync(out_tokens, dout, (size_t)n_steps * s->B * 4, hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess) rc = run_program(s, s->stt, stt_params(s, da, nullptr, dout, dprob, dturn), n_steps);
+  if (e == hipSuccess && rc == 0) e = hipMemcpyAsync(out_tokens, dout, nt * 4, hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess && rc == 0 && dturn) e = hipMemcpyAsync(out_turn, dturn, nt * 4, hipMemcpyDeviceToHost, s->stream);
   if (e == hipSuccess && rc == 0 && np) e = hipMemcpyAsync(out_probs, dprob, np * 4, hipMemcpyDeviceToHost, s->stream);
   hipError_t e2 = hipStreamSynchronize(s->stream);
   hipFree(da);
@@ -2111,6 +2139,24 @@ int svl_bench_phase(const svl_model* m, svl_state* s, int program, int phase, in
 int svl_stt_recognize_noalloc(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
                               uint32_t* out_tokens) {
   return guarded([&] { return stt_recognize_noalloc_impl(m, s, n_steps, audio_tokens, out_tokens); });
+}
+
+int svl_stt_recognize_turns(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* audio_tokens,
+                            const svl_turn_config* turn, uint32_t* out_tokens, float* out_probs, int32_t* out_turn_ends) {
+  return guarded([&] {
+    if (!turn || !out_turn_ends) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+    return stt_recognize_heads_impl(m, s, n_steps, audio_tokens, out_tokens, out_probs, turn, out_turn_ends);
+  });
+}
+
+int svl_stt_recognize_turns_async(const svl_model* m, svl_state* s, int64_t n_steps, const uint32_t* d_audio_tokens,
+                                  const svl_turn_config* turn, uint32_t* d_out_tokens, float* d_out_probs,
+                                  int32_t* d_out_turn_ends) {
+  return guarded([&] {
+    if (!turn || !d_out_turn_ends) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+    return stt_recognize_heads_async_impl(m, s, n_steps, d_audio_tokens, d_out_tokens, d_out_probs, turn,
+                                          d_out_turn_ends);
+  });
 }
 
 int svl_tts_step(const svl_model* m, svl_state* s, const float* latent, const float* noise, int32_t decode_steps,

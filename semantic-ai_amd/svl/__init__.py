@@ -45,7 +45,7 @@ EXPORTS = [
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
     "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase",
-    "svl_tts_step", "svl_tts_step_async",
+    "svl_tts_step", "svl_tts_step_async", "svl_stt_recognize_turns", "svl_stt_recognize_turns_async",
 ]
 
 
@@ -76,6 +76,11 @@ class Config(C.Structure):
         ("extra_heads_num", C.c_int32), ("extra_heads_dim", C.c_int32),
         ("flow_dim", C.c_int32), ("flow_depth", C.c_int32), ("flow_kind", C.c_int32),
     ]
+
+
+class TurnConfig(C.Structure):
+    """TurnDetector's parameters (SVL/stt/mod.rs:283-325)."""
+    _fields_ = [("threshold", C.c_float), ("frames", C.c_int32), ("head", C.c_int32)]
 
 
 class Tensor(C.Structure):
@@ -124,6 +129,8 @@ def load_library(path: str = LIB_PATH):
     L.svl_tts_backbone_step.argtypes = [vp, vp, vp, vp]
     L.svl_stt_recognize_noalloc.argtypes = [vp, vp, i64, vp, vp]
     L.svl_tts_step.argtypes = [vp, vp, vp, vp, i32, C.c_float, vp, vp, vp]
+    L.svl_stt_recognize_turns.argtypes = [vp, vp, i64, vp, C.POINTER(TurnConfig), vp, vp, vp]
+    L.svl_stt_recognize_turns_async.argtypes = [vp, vp, i64, vp, C.POINTER(TurnConfig), vp, vp, vp]
     L.svl_tts_step_async.argtypes = [vp, vp, vp, vp, i32, vp, vp]
     L.svl_bench_phase.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int)]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
@@ -287,6 +294,21 @@ class Model:
         probs = np.empty((n, state.batch, self.cfg.get("extra_heads_num", 0)), dtype=np.float32)
         _check(load_library().svl_stt_recognize_heads(self.h, state.h, n, _p(a), _p(out), _p(probs)))
         return out, probs
+
+    def recognize_turns(self, audio_tokens, state: "State", threshold: float = 0.5, frames: int = 1,
+                        head: int = 2):
+        """audio_tokens [n_steps, batch, n_q] -> (tokens [n_steps, batch], the extra heads'
+        probabilities [n_steps, batch, extra_heads_num], turn ends [n_steps, batch])."""
+        a = np.ascontiguousarray(audio_tokens, dtype=np.uint32)
+        n = a.shape[0]
+        out = np.empty((n, state.batch), dtype=np.uint32)
+        nh = self.cfg.get("extra_heads_num", 0)
+        probs = np.empty((n, state.batch, nh), dtype=np.float32)
+        ends = np.empty((n, state.batch), dtype=np.int32)
+        cfg = TurnConfig(threshold, frames, head)
+        _check(load_library().svl_stt_recognize_turns(self.h, state.h, n, _p(a), C.byref(cfg), _p(out),
+                                                      _p(probs) if nh else None, _p(ends)))
+        return out, probs, ends
 
     def recognize_async(self, n_steps: int, d_audio: int, d_out: int, state: "State") -> None:
         """Device-pointer variant: enqueues on the state's stream and returns."""
