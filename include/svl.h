@@ -48,8 +48,8 @@ typedef enum {
  * {f16 d; i8 qs[32]}, GgmlDType::Q4K = 144-byte blocks {f16 d, dmin; u8 scales[12];
  * u8 qs[128]}, GgmlDType::Q4_0 = 18-byte blocks {f16 d; u8 qs[16]}: byte j holds the 4-bit code
  * of element j (low nibble) and of element j + 16 (high nibble), value (code - 8) * d),
- * row-major [out][in / block]. */
-typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4, SVL_Q4_0 = 5 } svl_dtype;
+ * row-major [out][in / block].  SVL_I64: integer metadata (voice states' offsets). */
+typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4, SVL_Q4_0 = 5, SVL_I64 = 6 } svl_dtype;
 
 typedef enum { SVL_NORM_LAYER = 0, SVL_NORM_RMS = 1 } svl_norm;          /* transformer.rs:12-16 */
 typedef enum { SVL_FF_PLAIN_GELU = 0, SVL_FF_GATED_SILU = 1 } svl_ff;    /* transformer.rs:18-24 */
@@ -91,8 +91,8 @@ typedef struct {
 typedef struct {
     const char* name;
     int32_t dtype;         /* svl_dtype */
-    int32_t ndim;
-    int64_t shape[4];
+    int32_t ndim;          /* <= 5 */
+    int64_t shape[5];
     const void* data;      /* host pointer */
 } svl_tensor;
 
@@ -128,6 +128,13 @@ int svl_state_duplicate(const svl_state* state, svl_state** out);
  * per layer keys/values [num_kv_heads][len][head_dim] f32 covering positions 0..len. */
 int svl_state_load_stream(svl_state* state, int32_t stream, int64_t len, const float* const* keys,
                           const float* const* values);
+/* Voice::load (SVL/tts/voice.rs:103-143): a voice state in upstream Pocket TTS's safetensors
+ * layout -- per layer i, "transformer.layers.{i}.self_attn/cache" f32 or bf16 [2, 1, time,
+ * num_kv_heads, head_dim] (keys then values), "/offset" SVL_I64 [1] (the cached length; older
+ * exports: the length of "/current_end", else `time`) and "/pad" SVL_I64 (must be 0) -- loaded
+ * into stream `stream` as by svl_state_load_stream.  Batched (batch > 1) states are
+ * SVL_UNSUPPORTED. */
+int svl_state_load_voice(svl_state* state, int32_t stream, const svl_tensor* tensors, size_t count);
 /* TransformerState::layer_caches (SVL/nn/transformer.rs:76-78) for one stream and layer: the
  * visible keys/values [num_kv_heads][*len][head_dim] f32 (pass NULL buffers to query *len and
  * *first, the absolute position of the first one). */
@@ -143,7 +150,10 @@ int svl_state_synchronize(svl_state* state);
 void* svl_state_stream(const svl_state* state);
 
 /* Transformer::forward (SVL/nn/transformer.rs:139-154): xs [batch][t][d_model] f32 ->
- * ys [batch][t][d_model] f32 (host). */
+ * ys [batch][t][d_model] f32 (host).  With an unlimited context (a prompt prefill, as
+ * FlowLm::prompt_text / prompt_voice, SVL/tts/flow_lm.rs:137-158) up to 256 positions run as one
+ * pass of the step's kernels (each position a row, attending causally within the block); a
+ * windowed model runs one position at a time. */
 int svl_transformer_forward(const svl_model* model, svl_state* state, const float* xs, int64_t t,
                             float* ys);
 

@@ -64,6 +64,8 @@ struct GemvArgs {
   void* vc;
   int cap;
   int kv_bf16;
+  int kv_group;        // > 1: batch rows b share the ring of stream b / kv_group (positions of one
+                       // stream processed together, prefill); 0 or 1: one ring per batch row
   int advance_pos;
   // batched Q8_0 path (PH_QUANT / PH_QGEMM): the quantized input rows of the whole batch
   int8_t* xq;          // [B][L.in]
@@ -81,6 +83,7 @@ struct AttnArgs {
   float* out;          // [B][H*hd]
   int hpu;             // heads per unit (1 or 2); units = B * H / hpu
   const int* order;    // [B] the stream of units k H / hpu .. (k + 1) H / hpu - 1
+  int kv_group;        // as GemvArgs::kv_group
 };
 
 struct EmbedArgs {

@@ -118,35 +118,36 @@ __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P
 // the argument segment, with no dependent load of a descriptor pointer first.  F and KM select
 // the unit code compiled in (one GEMV family, or a group of phase kinds), so that each launch
 // runs a compact kernel.
-// Requests every 64-byte line of the first 704 bytes of the kernel arguments at once and waits for
+// Requests every 64-byte line of the first 832 bytes of the kernel arguments at once and waits for
 // them, so that the scalar loads of descriptor fields that follow hit the scalar cache instead of
 // going to memory one after another.
 __device__ __forceinline__ void touch_kernel_args() {
   const void* k = (const void*)__builtin_amdgcn_kernarg_segment_ptr();
-  unsigned d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11;
+  unsigned d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11, d12;
   asm volatile(
-      "s_load_dword %0, %12, 0x0\n\t"
-      "s_load_dword %1, %12, 0x40\n\t"
-      "s_load_dword %2, %12, 0x80\n\t"
-      "s_load_dword %3, %12, 0xc0\n\t"
-      "s_load_dword %4, %12, 0x100\n\t"
-      "s_load_dword %5, %12, 0x140\n\t"
-      "s_load_dword %6, %12, 0x180\n\t"
-      "s_load_dword %7, %12, 0x1c0\n\t"
-      "s_load_dword %8, %12, 0x200\n\t"
-      "s_load_dword %9, %12, 0x240\n\t"
-      "s_load_dword %10, %12, 0x280\n\t"
-      "s_load_dword %11, %12, 0x2c0\n\t"
+      "s_load_dword %0, %13, 0x0\n\t"
+      "s_load_dword %1, %13, 0x40\n\t"
+      "s_load_dword %2, %13, 0x80\n\t"
+      "s_load_dword %3, %13, 0xc0\n\t"
+      "s_load_dword %4, %13, 0x100\n\t"
+      "s_load_dword %5, %13, 0x140\n\t"
+      "s_load_dword %6, %13, 0x180\n\t"
+      "s_load_dword %7, %13, 0x1c0\n\t"
+      "s_load_dword %8, %13, 0x200\n\t"
+      "s_load_dword %9, %13, 0x240\n\t"
+      "s_load_dword %10, %13, 0x280\n\t"
+      "s_load_dword %11, %13, 0x2c0\n\t"
+      "s_load_dword %12, %13, 0x300\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7), "=&s"(d8),
-        "=&s"(d9), "=&s"(d10), "=&s"(d11)
+        "=&s"(d9), "=&s"(d10), "=&s"(d11), "=&s"(d12)
       : "s"(k)
       : "memory");
 }
 
 template <unsigned F, unsigned KM, int V>
 __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, StepParams P, int step) {
-  static_assert(sizeof(Phase) + sizeof(StepParams) + sizeof(int) <= 0x300, "kernel arguments past the touched lines");
+  static_assert(sizeof(Phase) + sizeof(StepParams) + sizeof(int) <= 0x340, "kernel arguments past the touched lines");
   touch_kernel_args();
   const Phase* d_ph = &ph;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -189,9 +190,11 @@ __global__ __launch_bounds__(kStepThreads) void phase_kernel(const Phase ph, Ste
 // with the fields its first loads depend on as leading scalar arguments, which the hardware
 // preloads into SGPRs (-amdgpu-kernarg-preload-count): the input row and the weight requests go
 // out at wave start instead of after a scalar load of the argument segment.  `hx` input rows,
-// `hw` / `hsc` weights and Q8_0 / Q4_0 block scales, `hnw` norm weights, `hepn` = epilogue | norm
-// kind << 8 | blocks per weight thread << 16 | (bf16 dense weights, or Q4_0 codes) << 24, `hxs`
-// input row stride.
+// `hw` / `hsc` weights and Q8_0 / Q4_0 block scales, `hnw` norm weights, `hparts` = units per batch
+// row | batch rows << 16, `hepn` = epilogue | norm kind << 8 | blocks per weight thread << 16 |
+// (bf16 dense weights, or Q4_0 codes) << 24, `hxs` input row stride.  Workgroup w runs unit
+// (w % B) * parts + w / B: the batch rows of one slice of weight rows run side by side, so that
+// their weights come from L2 after the first read (lockstep batches, prefill blocks).
 template <unsigned F, int V>
 __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* hx, const void* hw, const void* hsc,
                                                                   const float* hnw, int hin, int hipw, int hparts,
@@ -201,24 +204,27 @@ __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* h
   __shared__ WgSync ws;
   init_wg_sync(&ws);
   const int epi = hepn & 0xff, maxb = (hepn >> 16) & 0xff;
+  const int nparts = hparts & 0xffff, nbatch = hparts >> 16;
+  const int unit = nbatch > 1 ? (int)(blockIdx.x % nbatch) * nparts + (int)(blockIdx.x / nbatch) : (int)blockIdx.x;
+  hparts = nparts;
   if (threadIdx.x >= kRowThreads) {
     if (!lds_wait<true>(&ws.r_issued, kRowWaves, &ws.stop)) return;
     if constexpr (F == FAM_Q8) {
       WItem it;
-      w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, maxb, epi, blockIdx.x, it,
+      w_issue_at((const int8_t*)hw, (const uint16_t*)hsc, hin, hitems, hipw, hparts, maxb, epi, unit, it,
                  (hepn >> 24) & 1);
       if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
       w_terms(it, smem);
     } else if constexpr (F == FAM_Q4K) {
       WItemQ4 it;
-      w_issue_q4k_at((const unsigned char*)hw, hin, hitems, hipw, hparts, maxb, epi, blockIdx.x, it);
+      w_issue_q4k_at((const unsigned char*)hw, hin, hitems, hipw, hparts, maxb, epi, unit, it);
       if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
       w_terms_q4k(it, smem);
     } else {
       const bool ok = (hepn >> 24) ? w_dense_at<true>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi,
-                                                      blockIdx.x, &ws, smem, 0)
+                                                      unit, &ws, smem, 0)
                                    : w_dense_at<false>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi,
-                                                       blockIdx.x, &ws, smem, 0);
+                                                       unit, &ws, smem, 0);
       if (!ok) return;
     }
     lds_signal(&ws.t_parts);
@@ -236,9 +242,9 @@ __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* h
   a.nw = hnw;
   if (epi == EPI_SILU_GATE) a.ff_hidden = hitems;
   else a.L.out = hitems;
-  if constexpr (F == FAM_Q8) gemv_q8_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
-  else if constexpr (F == FAM_Q4K) gemv_q4k_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
-  else gemv_dense_rows<V>(a, blockIdx.x, P.pos, smem, rs, 0u);
+  if constexpr (F == FAM_Q8) gemv_q8_rows<V>(a, unit, P.pos, smem, rs, 0u);
+  else if constexpr (F == FAM_Q4K) gemv_q4k_rows<V>(a, unit, P.pos, smem, rs, 0u);
+  else gemv_dense_rows<V>(a, unit, P.pos, smem, rs, 0u);
 }
 
 // An attention phase launched like gemv_phase_kernel: the query, K / V ring, position and order
@@ -390,7 +396,7 @@ hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t s
     const int items = g.epi == EPI_SILU_GATE ? g.ff_hidden : g.L.out;
     const int epn = g.epi | (g.norm << 8) | (g.maxb << 16) | ((g.L.fmt == FMT_BF16C || g.L.fmt == FMT_Q4_0 ? 1 : 0) << 24);
     hipLaunchKernelGGL(kq, dim3(ph.units), dim3(kStepThreads), smem, s, g.x, (const void*)g.L.w, (const void*)g.L.scale,
-                       g.nw, g.L.in, g.ipw, g.parts, items, epn, g.x_stride, ph, p, step);
+                       g.nw, g.L.in, g.ipw, g.parts | (g.B << 16), items, epn, g.x_stride, ph, p, step);
     return hipGetLastError();
   }
   if (ph.kind == PH_QUANT || ph.kind == PH_QGEMM) {
@@ -478,9 +484,11 @@ void plan_gemv(GemvArgs& g, int grid, int* units) {
     g.maxb = (per_row * ipw * nb + kWeightThreads - 1) / kWeightThreads;
     if (g.maxb > kQ4Blocks) g.maxb = kQ4Blocks;
   } else if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C) {
-    // About one unit per workgroup and batch row, at most 64 rows (two weight-wave passes).
+    // About one unit per workgroup over all batch rows, at most 64 rows (two weight-wave passes):
+    // a single row spreads over the workgroups; many rows (lockstep batches, prefill blocks) take
+    // up to 64 rows per unit, each unit's weights read once per batch row.
     const int per_row = silu ? 2 : 1;
-    int ipw = (items + grid - 1) / grid;
+    int ipw = (int)(((int64_t)items * g.B + grid - 1) / grid);
     if (g.epi == EPI_QKV_ROPE && (ipw & 1)) ++ipw;
     if (ipw > 64 / per_row) ipw = 64 / per_row;
     g.ipw = ipw;

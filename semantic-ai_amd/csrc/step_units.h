@@ -509,7 +509,8 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row,
       if (region == 0) {
         st_co(a.q_out + (size_t)b * qdim + rr, out);
       } else {
-        const size_t idx = (((size_t)b * a.KVH + head) * a.cap + (size_t)(p % a.cap)) * a.hd + dim;
+        const size_t kb = a.kv_group > 1 ? (size_t)(b / a.kv_group) : (size_t)b;  // the ring's stream
+        const size_t idx = ((kb * a.KVH + head) * a.cap + (size_t)(p % a.cap)) * a.hd + dim;
         void* base = region == 1 ? a.kc : a.vc;
         if (a.kv_bf16) st_co((uint16_t*)base + idx, f32_to_bf16(out));
         else st_co((float*)base + idx, out);
@@ -1696,8 +1697,9 @@ __device__ __forceinline__ void attn_unit(const AttnArgs& a, int unit, const int
   // h0 + row % HPU.
   const int off0 = wave * 1024 + lane * 16, off1 = off0 + 8192;
   const int row0 = off0 / RB, col0 = off0 % RB, row1 = off1 / RB, col1 = off1 % RB;
-  const size_t base0 = ((size_t)b * KVH + (h0 + row0 % HPU) / (H / KVH)) * (size_t)cap;
-  const size_t base1 = ((size_t)b * KVH + (h0 + row1 % HPU) / (H / KVH)) * (size_t)cap;
+  const size_t kb = a.kv_group > 1 ? (size_t)(b / a.kv_group) : (size_t)b;  // the ring's stream
+  const size_t base0 = (kb * KVH + (h0 + row0 % HPU) / (H / KVH)) * (size_t)cap;
+  const size_t base1 = (kb * KVH + (h0 + row1 % HPU) / (H / KVH)) * (size_t)cap;
   auto issue = [&](const void* kv, int c) {
     unsigned char* st = smem + (c % kAttnStages) * kAttnChunkBytes;
     const int j0 = min(c * RH + row0 / HPU, L - 1), j1 = min(c * RH + row1 / HPU, L - 1);

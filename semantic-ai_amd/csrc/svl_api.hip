@@ -75,6 +75,7 @@ const svl_tensor* find_tensor(const svl_tensor* ts, size_t n, const std::string&
 }
 
 size_t numel(const svl_tensor* t) {
+  if (t->ndim < 0 || t->ndim > 5) return 0;  // svl_tensor::shape holds 5 dimensions
   size_t n = 1;
   for (int i = 0; i < t->ndim; ++i) n *= (size_t)t->shape[i];
   return n;
@@ -193,15 +194,23 @@ struct svl_state {
   int grid = 0;
   bool persistent = true;
   size_t lds_budget = 0;  // dynamic LDS a step launch may request on this device
+  // Prefill (Transformer::forward with T > 1 positions, unlimited context): the positions of a
+  // block run as the batch rows of a shadow state whose ring is this state's (kv_group rows per
+  // stream), so that one pass of the step's phases processes the whole block.
+  int kv_group = 1;
+  bool owns_stream = true;
+  svl_state* shadow = nullptr;
+  std::vector<int> pos_stage;  // host staging of positions uploaded by a call (waited for in it)
 
   ~svl_state() {
     hipSetDevice(m->device);
     if (stream) hipStreamSynchronize(stream);
+    delete shadow;
     for (void* p : allocs) hipFree(p);
     if (rope_ovf) hipFree(rope_ovf);
     if (ovf_host) hipHostFree(ovf_host);
     if (ovf_copied) hipEventDestroy(ovf_copied);
-    if (stream) hipStreamDestroy(stream);
+    if (stream && owns_stream) hipStreamDestroy(stream);
   }
   int alloc(void** p, size_t bytes) {
     HIP_TRY(hipMalloc(p, bytes ? bytes : 16));
@@ -805,6 +814,7 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     g.g.vc = s->vc[i];
     g.g.cap = s->slots;
     g.g.kv_bf16 = kv_bf16;
+    g.g.kv_group = s->kv_group;
     add_gemv(s, out, g);
     // attention over the ring
     Phase a{};
@@ -822,6 +832,7 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
     a.at.scale = std::pow((float)hd, -0.5f);  // (d as f32).powf(-0.5), attention.rs:100
     a.at.out = s->att;
     a.at.order = s->attn_order;
+    a.at.kv_group = s->kv_group;
     // two heads per unit once the batch has at least two units per workgroup without pairing
     // (SVL_ATTN_PAIRS=1 forces pairs, for tests)
     const char* pairs = getenv("SVL_ATTN_PAIRS");
@@ -1168,11 +1179,14 @@ int check_abort(svl_state* s) {
   return 0;
 }
 
-int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** out) {
+// A state for `batch` streams; with `kv_parent`, a prefill shadow: `batch` = kv_group rows per
+// stream of kv_parent, sharing its rings and stream (kv_parent outlives it).
+int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** out, svl_state* kv_parent = nullptr,
+               int kv_group = 1) {
   const svl_config& c = m->cfg;
   if (batch <= 0) return set_error(SVL_ERR_INVALID_INPUT, "batch must be positive");
   if (batch > kMaxBatch) return set_error(SVL_UNSUPPORTED, "batch must be <= %d", kMaxBatch);
-  int slots = c.context > 0 ? c.context : capacity;
+  int slots = kv_parent ? kv_parent->slots : (c.context > 0 ? c.context : capacity);
   if (slots <= 0) return set_error(SVL_ERR_INVALID_INPUT, "an unlimited-context model needs a positive capacity");
   if (slots > kMaxRingSlots) return set_error(SVL_UNSUPPORTED, "capacity must be <= %d", kMaxRingSlots);
   HIP_TRY(hipSetDevice(m->device));
@@ -1181,6 +1195,7 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   s->m = m;
   s->B = batch;
   s->slots = slots;
+  s->kv_group = kv_parent ? kv_group : 1;
   s->grid = step_program_grid(m->device);
   const char* mode = getenv("SVL_STEP_LAUNCH");
   // one launch per phase by default (kernel boundaries order the phases); SVL_STEP_LAUNCH=persistent
@@ -1192,13 +1207,21 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device) != hipSuccess || max_lds <= 0)
     return fail(set_error(SVL_ERR_DEVICE, "cannot query the LDS size"));
   s->lds_budget = (size_t)max_lds - kStaticLdsReserve;
-  if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
+  if (kv_parent) {
+    s->stream = kv_parent->stream;
+    s->owns_stream = false;
+  } else if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) {
     return fail(set_error(SVL_ERR_DEVICE, "hipStreamCreate failed"));
+  }
   const size_t kvb = (size_t)batch * c.num_kv_heads * slots * c.head_dim * (c.kv_dtype == SVL_BF16 ? 2 : 4);
   s->kc.resize(c.num_layers);
   s->vc.resize(c.num_layers);
   int rc = 0;
-  for (int i = 0; i < c.num_layers && !rc; ++i) {
+  if (kv_parent) {
+    s->kc = kv_parent->kc;
+    s->vc = kv_parent->vc;
+  }
+  for (int i = 0; i < c.num_layers && !rc && !kv_parent; ++i) {
     rc = s->alloc(&s->kc[i], kvb);
     if (!rc) rc = s->alloc(&s->vc[i], kvb);
     if (!rc && hipMemsetAsync(s->kc[i], 0, kvb, s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
@@ -1644,6 +1667,93 @@ static int state_load_stream_impl(svl_state* s, int32_t stream, int64_t len, con
   return 0;
 }
 
+// Voice::load (SVL/tts/voice.rs:103-143): the state after a voice prompt as upstream Pocket TTS
+// saves it -- per layer i, "transformer.layers.{i}.self_attn/cache" [2, batch, time, heads,
+// head_dim] (keys, then values), "/offset" (the cached length; older exports: the length of
+// "/current_end", else `time`) and "/pad" (must be zero) -- loaded into stream `stream` as
+// TransformerState::from_layer_caches does.
+static int state_load_voice_impl(svl_state* s, int32_t stream, const svl_tensor* ts, size_t n) {
+  if (!s || (n && !ts)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  const svl_config& c = s->m->cfg;
+  const std::string pre = "transformer.layers.", suf = ".self_attn/cache";
+  std::vector<const svl_tensor*> caches(c.num_layers, nullptr);
+  std::vector<int64_t> lens(c.num_layers, -1);
+  size_t found = 0;
+  auto to_i64 = [](const svl_tensor* t, int64_t* v) -> bool {
+    if (!t || !t->data || numel(t) < 1) return false;
+    if (t->dtype == SVL_I64) *v = ((const int64_t*)t->data)[0];
+    else if (t->dtype == SVL_F32) *v = (int64_t)((const float*)t->data)[0];
+    else return false;
+    return true;
+  };
+  for (size_t i = 0; i < n; ++i) {
+    if (!ts[i].name) continue;
+    const std::string name = ts[i].name;
+    if (name.size() <= pre.size() + suf.size() || name.compare(0, pre.size(), pre) ||
+        name.compare(name.size() - suf.size(), suf.size(), suf))
+      continue;
+    const std::string idx = name.substr(pre.size(), name.size() - pre.size() - suf.size());
+    char* end = nullptr;
+    const long layer = strtol(idx.c_str(), &end, 10);
+    if (idx.empty() || *end || layer < 0) return set_error(SVL_ERR_INVALID_INPUT, "bad tensor name %s", name.c_str());
+    if (layer >= c.num_layers) return set_error(SVL_ERR_INVALID_INPUT, "%s: the model has %d layers", name.c_str(), c.num_layers);
+    const svl_tensor* t = &ts[i];
+    if (t->ndim != 5 || t->shape[0] != 2 || t->shape[3] != c.num_kv_heads || t->shape[4] != c.head_dim)
+      return set_error(SVL_ERR_INVALID_INPUT, "%s: expected [2, batch, time, %d, %d]", name.c_str(), c.num_kv_heads,
+                       c.head_dim);
+    if (t->dtype != SVL_F32 && t->dtype != SVL_BF16)
+      return set_error(SVL_ERR_INVALID_INPUT, "%s: f32 or bf16 cache expected", name.c_str());
+    if (t->shape[1] != 1) return set_error(SVL_UNSUPPORTED, "%s: voice states of batch %lld", name.c_str(), (long long)t->shape[1]);
+    const std::string module = name.substr(0, name.size() - std::string("/cache").size());
+    int64_t len = t->shape[2], v = 0;
+    if (to_i64(find_tensor(ts, n, module + "/offset"), &v)) len = v;
+    else if (const svl_tensor* ce = find_tensor(ts, n, module + "/current_end")) len = ce->ndim > 0 ? ce->shape[0] : 0;
+    const svl_tensor* pad = find_tensor(ts, n, module + "/pad");
+    if (pad && pad->data) {
+      for (size_t k = 0; k < numel(pad); ++k) {
+        const int64_t pv = pad->dtype == SVL_I64 ? ((const int64_t*)pad->data)[k] : (int64_t)((const float*)pad->data)[k];
+        if (pv != 0) return set_error(SVL_ERR_INVALID_INPUT, "padded (batched) voice states are not supported");
+      }
+    }
+    if (len < 0 || len > t->shape[2]) return set_error(SVL_ERR_INVALID_INPUT, "%s: offset %lld past the cache", name.c_str(), (long long)len);
+    if (!caches[layer]) ++found;
+    caches[layer] = t;
+    lens[layer] = len;
+  }
+  if (found == 0) return set_error(SVL_ERR_INVALID_INPUT, "not a voice state");
+  if (found != (size_t)c.num_layers) return set_error(SVL_ERR_INVALID_INPUT, "voice state has %zu of %d layers", found, c.num_layers);
+  const int64_t len = lens[0];
+  for (int64_t l : lens)
+    if (l != len) return set_error(SVL_ERR_INVALID_INPUT, "voice state layers of different lengths");
+  // [2][1][time][heads][hd] -> keys / values [heads][len][hd] f32
+  const size_t kvh = c.num_kv_heads, hd = c.head_dim;
+  std::vector<std::vector<float>> kh(c.num_layers), vh(c.num_layers);
+  std::vector<const float*> kp(c.num_layers), vp(c.num_layers);
+  for (int l = 0; l < c.num_layers; ++l) {
+    const svl_tensor* t = caches[l];
+    const size_t T = t->shape[2];
+    kh[l].resize(kvh * len * hd);
+    vh[l].resize(kvh * len * hd);
+    for (int kv = 0; kv < 2; ++kv)
+      for (int64_t j = 0; j < len; ++j)
+        for (size_t h = 0; h < kvh; ++h)
+          for (size_t e = 0; e < hd; ++e) {
+            const size_t src = (((size_t)kv * T + j) * kvh + h) * hd + e;
+            const float v = t->dtype == SVL_F32 ? ((const float*)t->data)[src]
+                                                : [&] {
+                                                    uint32_t u = (uint32_t)((const uint16_t*)t->data)[src] << 16;
+                                                    float f;
+                                                    memcpy(&f, &u, 4);
+                                                    return f;
+                                                  }();
+            (kv ? vh : kh)[l][(h * len + j) * hd + e] = v;
+          }
+    kp[l] = kh[l].data();
+    vp[l] = vh[l].data();
+  }
+  return state_load_stream_impl(s, stream, len, kp.data(), vp.data());
+}
+
 static int state_layer_cache_impl(const svl_state* s, int32_t stream, int32_t layer, float* keys, float* values, int64_t* len,
                           int64_t* first) {
   if (!s) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
@@ -1721,6 +1831,61 @@ static int state_synchronize_impl(svl_state* s) {
 
 void* svl_state_stream(const svl_state* s) { return s ? (void*)s->stream : nullptr; }
 
+// Positions of one Transformer::forward block run together at most (rows of the prefill shadow).
+constexpr int kPrefillBlock = 256;
+
+// One block of Transformer::forward (SVL/nn/transformer.rs:139-154) for positions t0 .. t0 + tb - 1
+// of every stream of an unlimited-context state: the shadow state's batch rows b * tb + i are
+// position pos[b] + t0 + i of stream b; they write their keys and values into stream b's ring
+// slots and attend to the keys up to their own position (the causal mask of the block), so that
+// one pass of the step's phases is the block's forward, each row with the arithmetic of a single
+// step.  din / dout: [B][t][d] on the device.
+static int prefill_block(svl_state* s, const float* din, float* dout, int64_t t, int64_t t0, int tb, int* pos_stage) {
+  const svl_model* m = s->m;
+  const int d = m->cfg.d_model, B = s->B;
+  if (!s->shadow || s->shadow->B != B * tb) {
+    delete s->shadow;
+    s->shadow = nullptr;
+    svl_state* sh = nullptr;
+    TRY(make_state(m, B * tb, s->slots, &sh, s, tb));
+    s->shadow = sh;
+    for (Phase& ph : sh->fwd_prog.phases)
+      if (ph.kind == PH_COPY_IN || ph.kind == PH_COPY_OUT) {
+        ph.cp.x_stride = d;
+        ph.cp.y_stride = d;
+      }
+    HIP_TRY(hipMemcpyAsync(sh->fwd_prog.dev, sh->fwd_prog.phases.data(), sh->fwd_prog.phases.size() * sizeof(Phase),
+                           hipMemcpyHostToDevice, sh->stream));
+  }
+  svl_state* sh = s->shadow;
+  const size_t rows = (size_t)B * tb;
+  if (sh->fwd_cap < 2 * rows * d * 4) {
+    void* p;
+    TRY(sh->alloc(&p, 2 * rows * d * 4));
+    sh->fwd = (float*)p;
+    sh->fwd_cap = 2 * rows * d * 4;
+  }
+  for (int b = 0; b < B; ++b)
+    for (int i = 0; i < tb; ++i) {
+      sh->pos_host[(size_t)b * tb + i] = s->pos_host[b] + t0 + i;
+      pos_stage[(size_t)b * tb + i] = (int)(s->pos_host[b] + t0 + i);
+    }
+  HIP_TRY(hipMemcpyAsync(sh->pos, pos_stage, rows * sizeof(int), hipMemcpyHostToDevice, sh->stream));
+  TRY(check_room(sh, 1));
+  float* sin = sh->fwd;
+  float* sout = sh->fwd + rows * d;
+  HIP_TRY(hipMemcpy2DAsync(sin, (size_t)tb * d * 4, din + (size_t)t0 * d, (size_t)t * d * 4, (size_t)tb * d * 4, B,
+                           hipMemcpyDeviceToDevice, sh->stream));
+  StepParams P{};
+  P.fwd_in = sin;
+  P.fwd_out = sout;
+  P.fwd_T = 1;
+  TRY(run_program(sh, sh->fwd_prog, P, 1));
+  HIP_TRY(hipMemcpy2DAsync(dout + (size_t)t0 * d, (size_t)t * d * 4, sout, (size_t)tb * d * 4, (size_t)tb * d * 4, B,
+                           hipMemcpyDeviceToDevice, sh->stream));
+  return 0;
+}
+
 static int transformer_forward_impl(const svl_model* m, svl_state* s, const float* xs, int64_t t, float* ys) {
   if (!m || !s || (t > 0 && (!xs || !ys))) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   if (s->m != m) return set_error(SVL_ERR_INVALID_INPUT, "state belongs to another model");
@@ -1738,20 +1903,38 @@ static int transformer_forward_impl(const svl_model* m, svl_state* s, const floa
   }
   float* din = s->fwd;
   float* dout = s->fwd + (size_t)s->B * t * d;
-  // the copy phases read column `step` of [B][T][d]
-  for (Phase& ph : s->fwd_prog.phases)
-    if (ph.kind == PH_COPY_IN || ph.kind == PH_COPY_OUT) {
-      ph.cp.x_stride = (int)(t * d);
-      ph.cp.y_stride = ph.kind == PH_COPY_IN ? d : (int)(t * d);
-    }
-  HIP_TRY(hipMemcpyAsync(s->fwd_prog.dev, s->fwd_prog.phases.data(), s->fwd_prog.phases.size() * sizeof(Phase),
-                         hipMemcpyHostToDevice, s->stream));
   HIP_TRY(hipMemcpyAsync(din, xs, bytes, hipMemcpyHostToDevice, s->stream));
-  StepParams P{};
-  P.fwd_in = din;
-  P.fwd_out = dout;
-  P.fwd_T = (int)t;
-  TRY(run_program(s, s->fwd_prog, P, t));
+  // Blocks of positions when nothing is evicted from the ring meanwhile (unlimited context: the
+  // ring holds every position); a windowed ring has no room for a block's later keys.
+  const int tmax = std::min<int64_t>(kPrefillBlock, kMaxBatch / s->B);
+  if (m->cfg.context == 0 && t > 1 && tmax > 1) {
+    const int64_t nblk = (t + tmax - 1) / tmax;
+    const int tb = (int)((t + nblk - 1) / nblk);  // equal blocks but the last
+    s->pos_stage.resize((size_t)(nblk + 1) * s->B * tb + s->B);
+    int64_t t0 = 0;
+    for (int64_t k = 0; k < nblk; ++k, t0 += tb)
+      TRY(prefill_block(s, din, dout, t, t0, (int)std::min<int64_t>(tb, t - t0), s->pos_stage.data() + (size_t)k * s->B * tb));
+    int* np = s->pos_stage.data() + (size_t)nblk * s->B * tb;
+    for (int b = 0; b < s->B; ++b) {
+      s->pos_host[b] += t;
+      np[b] = (int)s->pos_host[b];
+    }
+    HIP_TRY(hipMemcpyAsync(s->pos, np, (size_t)s->B * sizeof(int), hipMemcpyHostToDevice, s->stream));
+  } else {
+    // one position at a time: the copy phases read column `step` of [B][T][d]
+    for (Phase& ph : s->fwd_prog.phases)
+      if (ph.kind == PH_COPY_IN || ph.kind == PH_COPY_OUT) {
+        ph.cp.x_stride = (int)(t * d);
+        ph.cp.y_stride = ph.kind == PH_COPY_IN ? d : (int)(t * d);
+      }
+    HIP_TRY(hipMemcpyAsync(s->fwd_prog.dev, s->fwd_prog.phases.data(), s->fwd_prog.phases.size() * sizeof(Phase),
+                           hipMemcpyHostToDevice, s->stream));
+    StepParams P{};
+    P.fwd_in = din;
+    P.fwd_out = dout;
+    P.fwd_T = (int)t;
+    TRY(run_program(s, s->fwd_prog, P, t));
+  }
   HIP_TRY(hipMemcpyAsync(ys, dout, bytes, hipMemcpyDeviceToHost, s->stream));
   HIP_TRY(hipStreamSynchronize(s->stream));
   return check_abort(s);
@@ -2157,6 +2340,10 @@ int svl_stt_recognize_turns_async(const svl_model* m, svl_state* s, int64_t n_st
     return stt_recognize_heads_async_impl(m, s, n_steps, d_audio_tokens, d_out_tokens, d_out_probs, turn,
                                           d_out_turn_ends);
   });
+}
+
+int svl_state_load_voice(svl_state* s, int32_t stream, const svl_tensor* tensors, size_t count) {
+  return guarded([&] { return state_load_voice_impl(s, stream, tensors, count); });
 }
 
 int svl_tts_step(const svl_model* m, svl_state* s, const float* latent, const float* noise, int32_t decode_steps,

@@ -28,7 +28,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB_PATH = os.environ.get("SVL_LIBRARY") or os.path.join(PKG, "lib", "libsvl.so")
 
-F32, BF16, F16, Q8_0, Q4K, Q4_0 = 0, 1, 2, 3, 4, 5
+F32, BF16, F16, Q8_0, Q4K, Q4_0, I64 = 0, 1, 2, 3, 4, 5, 6
 NORM_LAYER, NORM_RMS = 0, 1
 FF_PLAIN_GELU, FF_GATED_SILU = 0, 1
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
@@ -46,6 +46,7 @@ EXPORTS = [
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
     "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase",
     "svl_tts_step", "svl_tts_step_async", "svl_stt_recognize_turns", "svl_stt_recognize_turns_async",
+    "svl_state_load_voice",
 ]
 
 
@@ -86,7 +87,7 @@ class TurnConfig(C.Structure):
 class Tensor(C.Structure):
     _fields_ = [
         ("name", C.c_char_p), ("dtype", C.c_int32), ("ndim", C.c_int32),
-        ("shape", C.c_int64 * 4), ("data", C.c_void_p),
+        ("shape", C.c_int64 * 5), ("data", C.c_void_p),
     ]
 
 
@@ -112,6 +113,7 @@ def load_library(path: str = LIB_PATH):
     L.svl_state_duplicate.argtypes = [vp, C.POINTER(vp)]
     L.svl_state_load_stream.argtypes = [vp, i32, i64, C.POINTER(vp), C.POINTER(vp)]
     L.svl_state_layer_cache.argtypes = [vp, i32, i32, vp, vp, C.POINTER(i64), C.POINTER(i64)]
+    L.svl_state_load_voice.argtypes = [vp, i32, C.POINTER(Tensor), sz]
     L.svl_state_positions.argtypes = [vp, vp]
     L.svl_state_reset.argtypes = [vp]
     L.svl_state_destroy.argtypes = [vp]
@@ -369,6 +371,22 @@ class State:
         kp = (C.c_void_p * len(ks))(*[k.ctypes.data for k in ks])
         vp = (C.c_void_p * len(vs))(*[v.ctypes.data for v in vs])
         _check(load_library().svl_state_load_stream(self.h, stream, n, kp, vp))
+
+    def load_voice(self, tensors: dict, stream: int = 0) -> None:
+        """Voice::load (SVL/tts/voice.rs:103-143) from name -> (dtype code, shape, ndarray)."""
+        keep = []
+        arr = (Tensor * len(tensors))()
+        for i, (name, (dtype, shape, data)) in enumerate(tensors.items()):
+            data = np.ascontiguousarray(data)
+            nm = name.encode()
+            keep += [data, nm]
+            arr[i].name = nm
+            arr[i].dtype = dtype
+            arr[i].ndim = len(shape)
+            for j, d in enumerate(shape):
+                arr[i].shape[j] = d
+            arr[i].data = data.ctypes.data
+        _check(load_library().svl_state_load_voice(self.h, stream, arr, len(tensors)))
 
     def layer_caches(self, stream: int = 0):
         """Per layer (keys, values, first) with keys/values [kvh, len, hd]."""

@@ -279,3 +279,24 @@ def linear_bytes(s: Shape, dtype: str) -> int:
         else:
             total += n * 4
     return total
+
+
+def voice_tensors(keys, values, pad_to: int = 0) -> dict:
+    """Per-layer caches [1, kvh, len, hd] in the layout Voice::save writes (SVL/tts/voice.rs:76-99):
+    "transformer.layers.{i}.self_attn/cache" [2, 1, time, kvh, hd] f32, "/offset" [len] i64 and
+    "/pad" [0] i64; `pad_to` > len leaves seeded junk in the time rows past the offset."""
+    out = {}
+    for i, (k, v) in enumerate(zip(keys, values)):
+        k = np.asarray(k, np.float32).reshape(k.shape[-3:])  # [kvh, len, hd]
+        v = np.asarray(v, np.float32).reshape(v.shape[-3:])
+        n = k.shape[1]
+        t = max(pad_to, n)
+        cache = _rng(7, f"voice.junk.{i}").standard_normal((2, 1, t, k.shape[0], k.shape[2]), dtype=np.float32)
+        cache[0, 0, :n] = k.transpose(1, 0, 2)
+        cache[1, 0, :n] = v.transpose(1, 0, 2)
+        m = f"transformer.layers.{i}.self_attn"
+        out[m + "/cache"] = (F32, cache.shape, cache)
+        out[m + "/offset"] = (6, (1,), np.array([n], np.int64))
+        out[m + "/pad"] = (6, (1,), np.array([0], np.int64))
+    return out
+
