@@ -84,6 +84,10 @@ struct AttnArgs {
   int hpu;             // heads per unit (1 or 2); units = B * H / hpu
   const int* order;    // [B] the stream of units k H / hpu .. (k + 1) H / hpu - 1
   int kv_group;        // as GemvArgs::kv_group
+  // split launches (launch_attn_split): per-head meeting counters (32 words apart) and the value
+  // every counter reaches once the launch's units of that head have published their scores
+  unsigned* split_ctr;
+  unsigned split_target;
 };
 
 struct EmbedArgs {
@@ -214,6 +218,22 @@ constexpr int kVmWait1 = vm_wait_imm(1 * (kGemmStages - 2 * kSyncChunks));
 constexpr int kVmWait0 = vm_wait_imm(0);
 constexpr int kAttnChunkBytes = 16384;  // K or V rows per LDS stage of an attention unit
 constexpr int kAttnStages = 6;
+constexpr int kMaxSplit = 16;  // units per head of a split attention launch
+constexpr int kSplitKeys = 32;  // visible keys per split unit (the split starts at 2 kSplitKeys keys)
+// A split attention unit's LDS: the V columns of its dims for every key ([key][hd / S], by direct
+// loads of `split_piece_bytes` per lane, whole rounds of kRowThreads pieces, kSplitSlack keys of
+// slack for the chains' read-ahead), then the weights [cap + kSplitSlack] and 16 words of slots.
+constexpr int kSplitSlack = 48;
+__host__ __device__ constexpr int split_piece_bytes(int hd, int kv_bf16, int S) {
+  return (hd / S) * (kv_bf16 ? 2 : 4) % 16 == 0 ? 16 : 4;
+}
+__host__ __device__ constexpr size_t split_v_bytes(int cap, int hd, int kv_bf16, int S) {
+  return (size_t)(((size_t)(cap + kSplitSlack) * ((hd / S) * (kv_bf16 ? 2 : 4) / split_piece_bytes(hd, kv_bf16, S)) +
+                   kRowThreads - 1) / kRowThreads) * kRowThreads * split_piece_bytes(hd, kv_bf16, S);
+}
+__host__ __device__ constexpr size_t split_smem(int cap, int hd, int kv_bf16, int S) {
+  return split_v_bytes(cap, hd, kv_bf16, S) + (size_t)(cap + kSplitSlack + 16) * 4 + 64;
+}
 constexpr int kAttnVmWait = vm_wait_imm(2 * (kAttnStages - 2 * kSyncChunks));  // two direct loads per wave and chunk
 
 // Unit families of a step program.  The persistent kernel is compiled for a few family sets, so
@@ -228,6 +248,10 @@ enum UnitFamily : unsigned {
 unsigned program_families(const Phase* phases, int n);
 hipError_t launch_step_program(const StepParams& p, unsigned families, int grid, size_t smem, hipStream_t s);
 hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s);
+// An attention phase with each (stream, head) split over S units (S = 2, 4, 8 or 16; S divides
+// the head dim): `scores` [B * H][cap] f32 and ph.at.split_ctr / split_target as in AttnArgs.
+// Per-phase launches only (the units of a head meet within the launch).
+hipError_t launch_attn_split(const Phase& ph, const StepParams& p, int step, int S, float* scores, hipStream_t s);
 int step_program_grid(int device);
 size_t phase_smem(const Phase& ph);
 // Fills the unit layout of a GEMV phase (ipw, parts, maxb, units) for `grid` workgroups.

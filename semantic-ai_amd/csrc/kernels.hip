@@ -76,19 +76,6 @@ __device__ __forceinline__ const Phase& phase_at(const Phase* prog, int p) {
   return *(const Phase*)(const SVL_CONST Phase*)(prog + p);
 }
 
-__device__ __forceinline__ void init_wg_sync(WgSync* ws) {
-  if (threadIdx.x == 0) {
-    ws->r_arrive = 0;
-    ws->xq_parts = 0;
-    ws->t_parts = 0;
-    ws->r_issued = 0;
-    ws->g_arrive = 0;
-    ws->g_release = 0;
-    ws->stop = 0;
-  }
-  __syncthreads();  // the only full-workgroup barrier: nothing is in flight yet
-}
-
 template <unsigned F>
 __global__ __launch_bounds__(kStepThreads) void step_program_kernel(StepParams P) {
   extern __shared__ __align__(16) unsigned char smem[];

@@ -180,6 +180,20 @@ struct RowSync {
   }
 };
 
+// Clears the workgroup's LDS counters; the one full-workgroup barrier of a launch.
+__device__ __forceinline__ void init_wg_sync(WgSync* ws) {
+  if (threadIdx.x == 0) {
+    ws->r_arrive = 0;
+    ws->xq_parts = 0;
+    ws->t_parts = 0;
+    ws->r_issued = 0;
+    ws->g_arrive = 0;
+    ws->g_release = 0;
+    ws->stop = 0;
+  }
+  __syncthreads();  // the only full-workgroup barrier: nothing is in flight yet
+}
+
 // ---- rows, norms, activation quantization ---------------------------------------------------------
 // A row of K <= 8192 activations is held in registers by the row waves, thread t owning
 // elements t + 512 u for u < KP, KP = row_slots(K) (a compile-time count, so that no branch

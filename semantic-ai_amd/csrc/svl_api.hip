@@ -193,6 +193,15 @@ struct svl_state {
   unsigned gen = 0;
   int grid = 0;
   bool persistent = true;
+  // split attention (per-phase launches of few streams): up to split_max units per head, one per
+  // split_keys visible keys; per-head score rows [B * H][slots], meeting counters [B * H][32] and
+  // the total every counter has reached (split_gen); split_used: a split launch ran since the last
+  // check of the abort flag
+  int split_max = 1, split_min = 2, split_keys = 0;  // split_min: the fewest units whose LDS fits
+  float* split_scores = nullptr;
+  unsigned* split_ctr = nullptr;
+  unsigned split_gen = 0;
+  bool split_used = false;
   size_t lds_budget = 0;  // dynamic LDS a step launch may request on this device
   // Prefill (Transformer::forward with T > 1 positions, unlimited context): the positions of a
   // block run as the batch rows of a shadow state whose ring is this state's (kv_group rows per
@@ -1131,6 +1140,35 @@ int refresh_attn_order(svl_state* s) {
   return 0;
 }
 
+// Units per head of the attention launches of step `step` of a call (1: the unsplit unit): the
+// largest power of two up to split_max with split_keys visible keys per unit for the longest
+// stream, and at least split_min once the head is split at all.
+int attn_split(const svl_state* s, int64_t step) {
+  if (s->split_max < 2) return 1;
+  const int64_t window = s->m->cfg.context;
+  int64_t L = 0;
+  for (int64_t q : s->pos_host) L = std::max(L, window > 0 ? std::min(q + step + 1, window) : q + step + 1);
+  int S = 1;
+  while (S < s->split_max && (int64_t)2 * S * s->split_keys <= L) S *= 2;
+  return S > 1 ? std::max(S, s->split_min) : 1;
+}
+
+// One split attention launch: every head's counter grows by S.
+int launch_split(svl_state* s, const Phase& ph, const StepParams& P, int step, int S) {
+  const int nh = s->B * s->m->cfg.num_heads;
+  if (s->split_gen >= (1u << 30)) {  // long before the counters wrap
+    HIP_TRY(launch_fill_u32(s->split_ctr, 0u, (size_t)nh * 32, s->stream));
+    s->split_gen = 0;
+  }
+  Phase a = ph;
+  a.at.split_ctr = s->split_ctr;
+  a.at.split_target = s->split_gen + (unsigned)S;
+  s->split_gen += (unsigned)S;
+  s->split_used = true;
+  HIP_TRY(launch_attn_split(a, P, step, S, s->split_scores, s->stream));
+  return 0;
+}
+
 // Runs `n_steps` steps of program `p` on the state's stream: one persistent launch, or one
 // launch per phase.
 int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
@@ -1158,9 +1196,13 @@ int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
     s->gen += need;
   } else {
     P.n_steps = (int)n_steps;  // the units see the launch's step count (next-step gathers)
-    for (int64_t step = 0; step < n_steps; ++step)
-      for (int i = 0; i < P.nphase; ++i)
-        HIP_TRY(launch_phase(p.phases[i], P, (int)step, p.smem, s->stream));
+    for (int64_t step = 0; step < n_steps; ++step) {
+      const int S = attn_split(s, step);
+      for (int i = 0; i < P.nphase; ++i) {
+        if (S > 1 && p.phases[i].kind == PH_ATTN) TRY(launch_split(s, p.phases[i], P, (int)step, S));
+        else HIP_TRY(launch_phase(p.phases[i], P, (int)step, p.smem, s->stream));
+      }
+    }
   }
   for (auto& q : s->pos_host) q += n_steps;
   return 0;
@@ -1168,13 +1210,16 @@ int run_program(svl_state* s, Program& p, StepParams P, int64_t n_steps) {
 
 // After a synchronization: reports (and clears) a grid barrier that gave up waiting.
 int check_abort(svl_state* s) {
-  if (!s->persistent) return 0;
+  if (!s->persistent && !s->split_used) return 0;
   unsigned flag = 0;
   HIP_TRY(hipMemcpy(&flag, &s->sync->abort_flag[0], sizeof(flag), hipMemcpyDeviceToHost));
+  s->split_used = false;
   if (flag) {
     HIP_TRY(hipMemset(s->sync, 0, sizeof(SyncState)));
     s->gen = 0;
-    return set_error(SVL_ERR_DEVICE, "a grid barrier of the step kernel timed out; the state is undefined");
+    if (s->split_ctr) HIP_TRY(hipMemset(s->split_ctr, 0, (size_t)s->B * s->m->cfg.num_heads * 32 * 4));
+    s->split_gen = 0;
+    return set_error(SVL_ERR_DEVICE, "a grid barrier or attention meeting of the step timed out; the state is undefined");
   }
   return 0;
 }
@@ -1268,6 +1313,28 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   if (!rc) rc = s->alloc(&p, (size_t)batch * sizeof(int)), s->rope_delta = (int*)p;
   if (!rc) rc = s->alloc(&p, sizeof(SyncState)), s->sync = (SyncState*)p;
   if (!rc && hipMemsetAsync(s->sync, 0, sizeof(SyncState), s->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "memset");
+  if (!rc) {
+    // split attention while B * H units leave most CUs idle (SVL_ATTN_SPLIT: keys per split unit,
+    // 0 = never split)
+    const char* sp = getenv("SVL_ATTN_SPLIT");
+    s->split_keys = sp ? std::max(atoi(sp), 0) : kSplitKeys;
+    const int nh = batch * c.num_heads, kv_bf16 = c.kv_dtype == SVL_BF16 ? 1 : 0;
+    int S = kMaxSplit;
+    while (S > 1 && nh * S > s->grid) S /= 2;
+    if (s->persistent || kv_parent || s->split_keys == 0 || (c.head_dim != 64 && c.head_dim != 128) ||
+        split_smem(slots, c.head_dim, kv_bf16, S) > s->lds_budget)
+      S = 1;
+    s->split_max = S;
+    // fewer units hold more value columns each
+    s->split_min = 2;
+    while (s->split_min < S && split_smem(slots, c.head_dim, kv_bf16, s->split_min) > s->lds_budget) s->split_min *= 2;
+    if (S > 1) {
+      rc = s->alloc(&p, (size_t)nh * slots * 4), s->split_scores = (float*)p;
+      if (!rc) rc = s->alloc(&p, (size_t)nh * 32 * 4), s->split_ctr = (unsigned*)p;
+      if (!rc && hipMemsetAsync(s->split_ctr, 0, (size_t)nh * 32 * 4, s->stream) != hipSuccess)
+        rc = set_error(SVL_ERR_DEVICE, "memset");
+    }
+  }
   if (!rc) rc = build_programs(m, s);
   if (rc) return fail(rc);
   for (const Program* p : {&s->stt, &s->tts, &s->fwd_prog})

@@ -472,6 +472,35 @@ def test_s1_q8_0_64_stream_lockstep_matches_gemv_and_oracle(s1_q8):
                 assert to == t1[0]
 
 
+def test_s1_q8_0_split_attention_through_the_window_wrap(s1_q8, monkeypatch):
+    """Batch 1 at the full window: rings pre-filled to 740 positions, 24 steps through the wrap of
+    the 750-slot window.  The split attention launches (16 units per head) give the bits of one
+    unit per head, and the first 3 steps equal the oracle's."""
+    g, o = s1_q8
+    s = W.S1
+    ks, vs = W.prefill_caches(s, 740, seed=72)
+    audio = W.audio_tokens(s, 24, seed=73)[0]
+    runs = []
+    for split in ("0", "32"):
+        monkeypatch.setenv("SVL_ATTN_SPLIT", split)
+        st = g.init_state()
+        st.load_stream(0, ks, vs)
+        text, logits = s.text_card, []
+        for i in range(24):
+            tok, lg = g.step([text], audio[i][None], st, want_logits=True)
+            logits.append(lg[0])
+            text = int(tok[0])
+        runs.append(np.stack(logits))
+        del st
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+    ob = o.state_from_layer_caches(ks, vs)
+    text = s.text_card
+    for i in range(3):
+        to, lo = ob.stt_step(text, audio[i], want_logits=True)
+        assert np.array_equal(runs[1][i].view(np.uint32), lo.view(np.uint32)), i
+        text = int(to)
+
+
 @pytest.fixture(scope="module")
 def s1_bf16():
     oracle.set_threads(min(16, os.cpu_count() or 4))
