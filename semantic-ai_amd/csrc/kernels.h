@@ -84,10 +84,9 @@ struct AttnArgs {
   int hpu;             // heads per unit (1 or 2); units = B * H / hpu
   const int* order;    // [B] the stream of units k H / hpu .. (k + 1) H / hpu - 1
   int kv_group;        // as GemvArgs::kv_group
-  // split launches (launch_attn_split): per-head meeting counters (32 words apart) and the value
-  // every counter reaches once the launch's units of that head have published their scores
-  unsigned* split_ctr;
-  unsigned split_target;
+  // split launches (launch_attn_split): the tag that marks this launch's entries in the score
+  // rows (distinct from the tags of the state's earlier launches)
+  unsigned split_tag;
 };
 
 struct EmbedArgs {
@@ -220,19 +219,27 @@ constexpr int kAttnChunkBytes = 16384;  // K or V rows per LDS stage of an atten
 constexpr int kAttnStages = 6;
 constexpr int kMaxSplit = 16;  // units per head of a split attention launch
 constexpr int kSplitKeys = 32;  // visible keys per split unit (the split starts at 2 kSplitKeys keys)
-// A split attention unit's LDS: the V columns of its dims for every key ([key][hd / S], by direct
-// loads of `split_piece_bytes` per lane, whole rounds of kRowThreads pieces, kSplitSlack keys of
-// slack for the chains' read-ahead), then the weights [cap + kSplitSlack] and 16 words of slots.
+// A split attention unit's LDS:
+//   * the V columns of its hd / S dims as rows of keys (f32 words, bf16 widened; split_row_words
+//     words a row: 16 keys of slack for the chains' read-ahead, and a row stride of 16 bytes past
+//     a multiple of 256, so that the lanes' 16-byte reads of their rows fall in different banks);
+//   * the staging of those columns as they arrive ([key][hd / S] in pieces of split_piece_bytes,
+//     rounds of 256 pieces by four waves);
+//   * the weights [cap + kSplitSlack] and 32 words of slots.
 constexpr int kSplitSlack = 48;
+__host__ __device__ constexpr int split_row_words(int cap) { return (cap + 16 + 63) / 64 * 64 + 4; }
 __host__ __device__ constexpr int split_piece_bytes(int hd, int kv_bf16, int S) {
   return (hd / S) * (kv_bf16 ? 2 : 4) % 16 == 0 ? 16 : 4;
 }
-__host__ __device__ constexpr size_t split_v_bytes(int cap, int hd, int kv_bf16, int S) {
-  return (size_t)(((size_t)(cap + kSplitSlack) * ((hd / S) * (kv_bf16 ? 2 : 4) / split_piece_bytes(hd, kv_bf16, S)) +
-                   kRowThreads - 1) / kRowThreads) * kRowThreads * split_piece_bytes(hd, kv_bf16, S);
+__host__ __device__ constexpr size_t split_rows_bytes(int cap, int hd, int S) {
+  return (size_t)(hd / S) * split_row_words(cap) * 4;
+}
+__host__ __device__ constexpr size_t split_stage_bytes(int cap, int hd, int kv_bf16, int S) {
+  return ((size_t)cap * ((hd / S) * (kv_bf16 ? 2 : 4) / split_piece_bytes(hd, kv_bf16, S)) + 255) / 256 * 256 *
+         split_piece_bytes(hd, kv_bf16, S);
 }
 __host__ __device__ constexpr size_t split_smem(int cap, int hd, int kv_bf16, int S) {
-  return split_v_bytes(cap, hd, kv_bf16, S) + (size_t)(cap + kSplitSlack + 16) * 4 + 64;
+  return split_rows_bytes(cap, hd, S) + split_stage_bytes(cap, hd, kv_bf16, S) + (size_t)(cap + kSplitSlack + 32) * 4 + 64;
 }
 constexpr int kAttnVmWait = vm_wait_imm(2 * (kAttnStages - 2 * kSyncChunks));  // two direct loads per wave and chunk
 
@@ -249,9 +256,9 @@ unsigned program_families(const Phase* phases, int n);
 hipError_t launch_step_program(const StepParams& p, unsigned families, int grid, size_t smem, hipStream_t s);
 hipError_t launch_phase(const Phase& ph, const StepParams& p, int step, size_t smem, hipStream_t s);
 // An attention phase with each (stream, head) split over S units (S = 2, 4, 8 or 16; S divides
-// the head dim): `scores` [B * H][cap] f32 and ph.at.split_ctr / split_target as in AttnArgs.
-// Per-phase launches only (the units of a head meet within the launch).
-hipError_t launch_attn_split(const Phase& ph, const StepParams& p, int step, int S, float* scores, hipStream_t s);
+// the head dim): `scores` [B * H][cap] tagged entries (tag << 32 | f32 bits), ph.at.split_tag as
+// in AttnArgs.  Per-phase launches only (the units of a head exchange scores within the launch).
+hipError_t launch_attn_split(const Phase& ph, const StepParams& p, int step, int S, uint64_t* scores, hipStream_t s);
 int step_program_grid(int device);
 size_t phase_smem(const Phase& ph);
 // Fills the unit layout of a GEMV phase (ipw, parts, maxb, units) for `grid` workgroups.

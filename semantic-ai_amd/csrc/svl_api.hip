@@ -194,12 +194,10 @@ struct svl_state {
   int grid = 0;
   bool persistent = true;
   // split attention (per-phase launches of few streams): up to split_max units per head, one per
-  // split_keys visible keys; per-head score rows [B * H][slots], meeting counters [B * H][32] and
-  // the total every counter has reached (split_gen); split_used: a split launch ran since the last
-  // check of the abort flag
+  // split_keys visible keys; per-head rows of tagged scores [B * H][slots] and the tag of the last
+  // split launch (split_gen); split_used: a split launch ran since the last check of the abort flag
   int split_max = 1, split_min = 2, split_keys = 0;  // split_min: the fewest units whose LDS fits
-  float* split_scores = nullptr;
-  unsigned* split_ctr = nullptr;
+  uint64_t* split_scores = nullptr;
   unsigned split_gen = 0;
   bool split_used = false;
   size_t lds_budget = 0;  // dynamic LDS a step launch may request on this device
@@ -1140,6 +1138,9 @@ int refresh_attn_order(svl_state* s) {
   return 0;
 }
 
+// 32-bit words of a state's split score rows.
+size_t split_score_words(const svl_state* s) { return (size_t)s->B * s->m->cfg.num_heads * s->slots * 2; }
+
 // Units per head of the attention launches of step `step` of a call (1: the unsplit unit): the
 // largest power of two up to split_max with split_keys visible keys per unit for the longest
 // stream, and at least split_min once the head is split at all.
@@ -1153,17 +1154,15 @@ int attn_split(const svl_state* s, int64_t step) {
   return S > 1 ? std::max(S, s->split_min) : 1;
 }
 
-// One split attention launch: every head's counter grows by S.
+// One split attention launch, tagged split_gen + 1 (the rows are cleared to tag 0 before the tags
+// would wrap).
 int launch_split(svl_state* s, const Phase& ph, const StepParams& P, int step, int S) {
-  const int nh = s->B * s->m->cfg.num_heads;
-  if (s->split_gen >= (1u << 30)) {  // long before the counters wrap
-    HIP_TRY(launch_fill_u32(s->split_ctr, 0u, (size_t)nh * 32, s->stream));
+  if (s->split_gen >= (1u << 31)) {
+    HIP_TRY(launch_fill_u32((uint32_t*)s->split_scores, 0u, split_score_words(s), s->stream));
     s->split_gen = 0;
   }
   Phase a = ph;
-  a.at.split_ctr = s->split_ctr;
-  a.at.split_target = s->split_gen + (unsigned)S;
-  s->split_gen += (unsigned)S;
+  a.at.split_tag = ++s->split_gen;
   s->split_used = true;
   HIP_TRY(launch_attn_split(a, P, step, S, s->split_scores, s->stream));
   return 0;
@@ -1217,7 +1216,7 @@ int check_abort(svl_state* s) {
   if (flag) {
     HIP_TRY(hipMemset(s->sync, 0, sizeof(SyncState)));
     s->gen = 0;
-    if (s->split_ctr) HIP_TRY(hipMemset(s->split_ctr, 0, (size_t)s->B * s->m->cfg.num_heads * 32 * 4));
+    if (s->split_scores) HIP_TRY(hipMemset(s->split_scores, 0, split_score_words(s) * 4));
     s->split_gen = 0;
     return set_error(SVL_ERR_DEVICE, "a grid barrier or attention meeting of the step timed out; the state is undefined");
   }
@@ -1329,9 +1328,8 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
     s->split_min = 2;
     while (s->split_min < S && split_smem(slots, c.head_dim, kv_bf16, s->split_min) > s->lds_budget) s->split_min *= 2;
     if (S > 1) {
-      rc = s->alloc(&p, (size_t)nh * slots * 4), s->split_scores = (float*)p;
-      if (!rc) rc = s->alloc(&p, (size_t)nh * 32 * 4), s->split_ctr = (unsigned*)p;
-      if (!rc && hipMemsetAsync(s->split_ctr, 0, (size_t)nh * 32 * 4, s->stream) != hipSuccess)
+      rc = s->alloc(&p, (size_t)nh * slots * 8), s->split_scores = (uint64_t*)p;
+      if (!rc && hipMemsetAsync(s->split_scores, 0, (size_t)nh * slots * 8, s->stream) != hipSuccess)
         rc = set_error(SVL_ERR_DEVICE, "memset");
     }
   }
