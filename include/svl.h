@@ -253,6 +253,27 @@ int svl_tts_step(const svl_model* model, svl_state* state, const float* latent, 
 int svl_tts_step_async(const svl_model* model, svl_state* state, const float* d_latent, const float* d_noise,
                        int32_t decode_steps, float* d_out_latent, float* d_out_eos_logit);
 
+/* ---- the STT audio-token producer's quantizer ----------------------------------------------- */
+
+/* Mimi's split residual vector quantizer, encoding only (SVL/stt/model.rs:84-174;
+ * Quantizer::new, :93-98, binds `n_q` codebooks of `bins` entries).  Tensors (f32, bf16 or f16):
+ *   rvq_first.input_proj.weight, rvq_rest.input_proj.weight        [256, 512, 1] or [256, 512]
+ *   rvq_first.vq.layers.0._codebook.embedding_sum                   [bins, 256]
+ *   rvq_first.vq.layers.0._codebook.cluster_usage                   [bins]
+ *   rvq_rest.vq.layers.<i>._codebook.{embedding_sum, cluster_usage} for i < n_q - 1
+ * (the names under the checkpoint's `quantizer.` prefix, SVL/stt/mod.rs:196). */
+typedef struct svl_rvq svl_rvq;
+int svl_rvq_create(const svl_tensor* tensors, size_t count, int32_t n_q, int32_t bins, int device,
+                   svl_rvq** out);
+void svl_rvq_destroy(svl_rvq* rvq);
+/* Quantizer::encode (:101-104): latents [batch][512][frames] f32 -> codes [batch][frames][n_q].
+ * Host pointers. */
+int svl_rvq_encode(svl_rvq* rvq, int32_t batch, int32_t frames, const float* latents, uint32_t* codes);
+/* The same on device buffers, enqueued on the quantizer's stream; svl_rvq_synchronize waits. */
+int svl_rvq_encode_async(svl_rvq* rvq, int32_t batch, int32_t frames, const float* d_latents,
+                         uint32_t* d_codes);
+int svl_rvq_synchronize(svl_rvq* rvq);
+
 #ifdef __cplusplus
 }
 #endif

@@ -135,6 +135,11 @@ def lib():
             L.svlo_stt_step.restype = C.c_int
             L.svlo_stt_greedy.argtypes = [vp, vp, C.c_int64, vp, vp, vp, vp]
             L.svlo_tts_step.argtypes = [vp, vp, vp, vp, C.c_int, vp, vp]
+            L.svlo_rvq_create.argtypes = [C.c_int, C.c_int, vp, vp, vp, vp]
+            L.svlo_rvq_create.restype = vp
+            L.svlo_rvq_destroy.argtypes = [vp]
+            L.svlo_rvq_codebook.argtypes = [vp, C.c_int, vp, vp]
+            L.svlo_rvq_encode.argtypes = [vp, sz, sz, vp, vp]
             L.svlo_turn_init.argtypes = [vp, C.c_float, C.c_int, C.c_int]
             L.svlo_turn_init.restype = None
             L.svlo_turn_word.argtypes = [vp]
@@ -420,6 +425,47 @@ class TurnDetector:
     def step(self, token: int, probs) -> bool:
         p = np.ascontiguousarray(probs, dtype=np.float32)
         return bool(lib().svlo_turn_step(C.byref(self.t), token, _p(p) if p.size else None, p.size))
+
+
+# ---- Mimi's split residual vector quantizer (rvq.c) ---------------------------------------------
+
+RVQ_IN, RVQ_DIM = 512, 256
+
+
+class Rvq:
+    """Quantizer::encode (SVL/stt/model.rs:84-174).  w_first / w_rest: input_proj weights
+    [256, 512] (or [256, 512, 1]); sums [n_q, bins, 256], usage [n_q, bins]: embedding_sum and
+    cluster_usage of the first quantizer's codebook, then the rest's."""
+
+    def __init__(self, w_first, w_rest, sums, usage):
+        self._w = [np.ascontiguousarray(np.reshape(w, (RVQ_DIM, RVQ_IN)), dtype=np.float32) for w in (w_first, w_rest)]
+        s = np.ascontiguousarray(sums, dtype=np.float32)
+        u = np.ascontiguousarray(usage, dtype=np.float32)
+        self.n_q, self.bins = s.shape[0], s.shape[1]
+        assert s.shape == (self.n_q, self.bins, RVQ_DIM) and u.shape == (self.n_q, self.bins)
+        self.h = lib().svlo_rvq_create(self.n_q, self.bins, _p(self._w[0]), _p(self._w[1]), _p(s), _p(u))
+        if not self.h:
+            raise RuntimeError("svlo_rvq_create failed")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().svlo_rvq_destroy(self.h)
+            self.h = None
+
+    def codebook(self, stage: int):
+        emb = np.empty((self.bins, RVQ_DIM), np.float32)
+        hn = np.empty(self.bins, np.float32)
+        lib().svlo_rvq_codebook(self.h, stage, _p(emb), _p(hn))
+        return emb, hn
+
+    def encode(self, latents) -> np.ndarray:
+        """latents [batch, 512, frames] -> codes [batch, frames, n_q] (uint32)."""
+        x = np.ascontiguousarray(latents, dtype=np.float32)
+        b, c, t = x.shape
+        assert c == RVQ_IN
+        codes = np.empty((b, t, self.n_q), np.uint32)
+        lib().svlo_rvq_encode(self.h, b, t, _p(x), _p(codes))
+        return codes
 
 
 # ---- model -------------------------------------------------------------------------------------

@@ -93,6 +93,22 @@ uint32_t svlo_argmax(const float* x, size_t n);
 /* softmax over x[0..n) (candle-nn softmax_last_dim), returning its first element */
 float svlo_softmax_first(const float* x, size_t n);
 
+/* ---- Mimi's split residual vector quantizer, encoding (rvq.c) ------------------------- */
+
+#define SVLO_RVQ_IN 512   /* latent channels */
+#define SVLO_RVQ_DIM 256  /* codebook dims (ResidualQuantizer::DIM) */
+typedef struct svlo_rvq svlo_rvq;
+/* w_first / w_rest: input_proj weights [256][512]; sums [n_q][bins][256] and usage [n_q][bins]:
+ * the codebooks' embedding_sum and cluster_usage, the first quantizer's codebook first, then the
+ * rest's in order. */
+svlo_rvq* svlo_rvq_create(int n_q, int bins, const float* w_first, const float* w_rest, const float* sums,
+                          const float* usage);
+void svlo_rvq_destroy(svlo_rvq* q);
+/* the prepared embedding [bins][256] and half norms [bins] of codebook `stage` */
+void svlo_rvq_codebook(const svlo_rvq* q, int stage, float* emb, float* half_norms);
+/* latents [batch][512][frames] -> codes [batch][frames][n_q] */
+void svlo_rvq_encode(const svlo_rvq* q, size_t batch, size_t frames, const float* latents, uint32_t* codes);
+
 /* ---- model ------------------------------------------------------------------------------ */
 
 enum { SVLO_F32 = 0, SVLO_BF16 = 1, SVLO_F16 = 2, SVLO_Q8_0 = 3, SVLO_Q4K = 4, SVLO_Q4_0 = 5 };

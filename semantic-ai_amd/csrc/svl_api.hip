@@ -31,6 +31,7 @@
 #include "../../include/svl_bench.h"
 #include "flow_head.h"
 #include "kernels.h"
+#include "rvq.h"
 
 using namespace svl;
 
@@ -226,11 +227,43 @@ struct svl_state {
   }
 };
 
+// Mimi's split residual vector quantizer (encoding): input projections, prepared codebooks and the
+// work buffers of a call, on its own stream.
+struct svl_rvq {
+  int device = 0, n_q = 0, bins = 0;
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocs;
+  float* w = nullptr;               // input_proj of the first and the rest quantizer [2][256][512]
+  float *emb = nullptr, *hn = nullptr;  // codebooks [n_q][bins][256] and half norms [n_q][bins]
+  // per-call work for up to rows_cap rows: projections [2][rows][256], residuals [2][rows][256],
+  // keys [n_q][rows], and the staging of the host-pointer call
+  int64_t rows_cap = 0;
+  float *proj = nullptr, *res = nullptr, *lat = nullptr;
+  unsigned long long* keys = nullptr;
+  uint32_t* codes = nullptr;
+
+  ~svl_rvq() {
+    hipSetDevice(device);
+    if (stream) hipStreamSynchronize(stream);
+    free_work();
+    for (void* p : allocs) hipFree(p);
+    if (stream) hipStreamDestroy(stream);
+  }
+  void free_work() {
+    for (void* p : {(void*)proj, (void*)res, (void*)lat, (void*)keys, (void*)codes})
+      if (p) hipFree(p);
+    proj = res = lat = nullptr;
+    keys = nullptr;
+    codes = nullptr;
+    rows_cap = 0;
+  }
+};
+
 namespace {
 
 // Copies a dense tensor of n elements to device memory dst as f32 (converted on the GPU from
 // bf16/f16).
-int copy_f32(svl_model* m, const svl_tensor* t, size_t n, void* dst) {
+int copy_f32_on(hipStream_t stream, const svl_tensor* t, size_t n, void* dst) {
   if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor");
   if (numel(t) != n)
     return set_error(SVL_ERR_INVALID_INPUT, "tensor %s: %zu elements, expected %zu", t->name, numel(t), n);
@@ -240,9 +273,9 @@ int copy_f32(svl_model* m, const svl_tensor* t, size_t n, void* dst) {
     void* tmp;
     HIP_TRY(hipMalloc(&tmp, n * 2));
     HIP_TRY(hipMemcpy(tmp, t->data, n * 2, hipMemcpyHostToDevice));
-    hipError_t e = t->dtype == SVL_BF16 ? launch_bf16_to_f32((const uint16_t*)tmp, (float*)dst, n, m->stream)
-                                         : launch_f16_to_f32((const uint16_t*)tmp, (float*)dst, n, m->stream);
-    hipError_t e2 = hipStreamSynchronize(m->stream);
+    hipError_t e = t->dtype == SVL_BF16 ? launch_bf16_to_f32((const uint16_t*)tmp, (float*)dst, n, stream)
+                                         : launch_f16_to_f32((const uint16_t*)tmp, (float*)dst, n, stream);
+    hipError_t e2 = hipStreamSynchronize(stream);
     hipFree(tmp);
     HIP_TRY(e);
     HIP_TRY(e2);
@@ -251,6 +284,8 @@ int copy_f32(svl_model* m, const svl_tensor* t, size_t n, void* dst) {
   }
   return 0;
 }
+
+int copy_f32(svl_model* m, const svl_tensor* t, size_t n, void* dst) { return copy_f32_on(m->stream, t, n, dst); }
 
 // Uploads a dense tensor as f32 into a new model allocation.
 int upload_f32(svl_model* m, const svl_tensor* t, size_t n, float** out) {
@@ -1568,6 +1603,112 @@ extern "C" {
 
 const char* svl_last_error(void) { return g_error.c_str(); }
 
+static int rvq_create_impl(const svl_tensor* ts, size_t n, int32_t n_q, int32_t bins, int device, svl_rvq** out) {
+  if (!out) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  *out = nullptr;
+  if (n_q < 1 || bins < 1 || bins > (1 << 24)) return set_error(SVL_ERR_CONFIG, "n_q and bins must be positive");
+  if (!ts && n) return set_error(SVL_ERR_INVALID_INPUT, "null tensors");
+  HIP_TRY(hipSetDevice(device));
+  std::unique_ptr<svl_rvq> q(new svl_rvq());
+  q->device = device;
+  q->n_q = n_q;
+  q->bins = bins;
+  HIP_TRY(hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking));
+  auto alloc = [&](void** p, size_t bytes) -> int {
+    HIP_TRY(hipMalloc(p, bytes));
+    q->allocs.push_back(*p);
+    return 0;
+  };
+  const size_t wn = (size_t)kRvqDim * kRvqIn, entries = (size_t)n_q * bins;
+  void* p;
+  TRY(alloc(&p, 2 * wn * 4));
+  q->w = (float*)p;
+  TRY(alloc(&p, entries * kRvqDim * 4));
+  q->emb = (float*)p;
+  TRY(alloc(&p, entries * 4));
+  q->hn = (float*)p;
+  const char* parts[2] = {"rvq_first", "rvq_rest"};
+  for (int part = 0; part < 2; ++part) {
+    const std::string name = std::string(parts[part]) + ".input_proj.weight";
+    const svl_tensor* t = find_tensor(ts, n, name);
+    if (!t) return set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s", name.c_str());
+    TRY(copy_f32_on(q->stream, t, wn, q->w + part * wn));
+  }
+  // the codebooks' sums and usages, staged and prepared on the GPU
+  float *sums = nullptr, *usage = nullptr;
+  HIP_TRY(hipMalloc((void**)&sums, entries * kRvqDim * 4));
+  int rc = 0;
+  if (hipMalloc((void**)&usage, entries * 4) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "hipMalloc failed");
+  for (int stage = 0; stage < n_q && !rc; ++stage) {
+    const std::string pre = stage == 0 ? "rvq_first.vq.layers.0._codebook."
+                                       : "rvq_rest.vq.layers." + std::to_string(stage - 1) + "._codebook.";
+    const svl_tensor* es = find_tensor(ts, n, pre + "embedding_sum");
+    const svl_tensor* us = find_tensor(ts, n, pre + "cluster_usage");
+    if (!es || !us) {
+      rc = set_error(SVL_ERR_INVALID_INPUT, "missing tensor %s%s", pre.c_str(), es ? "cluster_usage" : "embedding_sum");
+      break;
+    }
+    rc = copy_f32_on(q->stream, es, (size_t)bins * kRvqDim, sums + (size_t)stage * bins * kRvqDim);
+    if (!rc) rc = copy_f32_on(q->stream, us, (size_t)bins, usage + (size_t)stage * bins);
+  }
+  if (!rc && launch_rvq_prepare(sums, usage, entries, q->emb, q->hn, q->stream) != hipSuccess)
+    rc = set_error(SVL_ERR_DEVICE, "codebook preparation failed");
+  if (!rc && hipStreamSynchronize(q->stream) != hipSuccess) rc = set_error(SVL_ERR_DEVICE, "codebook preparation failed");
+  hipFree(sums);
+  if (usage) hipFree(usage);
+  TRY(rc);
+  *out = q.release();
+  return 0;
+}
+
+// Work buffers for `rows` rows (waits for the stream before replacing smaller ones).
+static int rvq_reserve(svl_rvq* q, int64_t rows) {
+  if (rows <= q->rows_cap) return 0;
+  HIP_TRY(hipStreamSynchronize(q->stream));
+  q->free_work();
+  const int64_t cap = std::max<int64_t>(rows, 64);
+  HIP_TRY(hipMalloc((void**)&q->proj, (size_t)cap * 2 * kRvqDim * 4));
+  HIP_TRY(hipMalloc((void**)&q->res, (size_t)cap * 2 * kRvqDim * 4));
+  HIP_TRY(hipMalloc((void**)&q->lat, (size_t)cap * kRvqIn * 4));
+  HIP_TRY(hipMalloc((void**)&q->keys, (size_t)cap * q->n_q * 8));
+  HIP_TRY(hipMalloc((void**)&q->codes, (size_t)cap * q->n_q * 4));
+  q->rows_cap = cap;
+  return 0;
+}
+
+static int rvq_encode_async_impl(svl_rvq* q, int32_t batch, int32_t frames, const float* d_lat, uint32_t* d_codes) {
+  if (!q || (!d_lat && batch * (int64_t)frames > 0) || (!d_codes && batch * (int64_t)frames > 0))
+    return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (batch < 0 || frames < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative batch or frames");
+  const int64_t rows = (int64_t)batch * frames;
+  if (rows == 0) return 0;
+  if (rows > (1 << 20)) return set_error(SVL_ERR_INVALID_INPUT, "at most 2^20 frames a call");
+  HIP_TRY(hipSetDevice(q->device));
+  TRY(rvq_reserve(q, rows));
+  const int r = (int)rows;
+  HIP_TRY(launch_fill_u32((uint32_t*)q->keys, 0xffffffffu, (size_t)rows * q->n_q * 2, q->stream));
+  HIP_TRY(launch_rvq_project(d_lat, batch, frames, q->w, q->w + (size_t)kRvqDim * kRvqIn, q->proj, q->stream));
+  for (int k = 0; k < std::max(q->n_q - 1, 1); ++k)
+    HIP_TRY(launch_rvq_stage(k, q->n_q, r, q->bins, q->emb, q->hn, q->proj, q->res, q->keys, q->stream));
+  HIP_TRY(launch_rvq_codes(q->keys, r, q->n_q, d_codes, q->stream));
+  return 0;
+}
+
+static int rvq_encode_impl(svl_rvq* q, int32_t batch, int32_t frames, const float* lat, uint32_t* codes) {
+  if (!q || ((!lat || !codes) && batch * (int64_t)frames > 0)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (batch < 0 || frames < 0) return set_error(SVL_ERR_INVALID_INPUT, "negative batch or frames");
+  const int64_t rows = (int64_t)batch * frames;
+  if (rows == 0) return 0;
+  if (rows > (1 << 20)) return set_error(SVL_ERR_INVALID_INPUT, "at most 2^20 frames a call");
+  HIP_TRY(hipSetDevice(q->device));
+  TRY(rvq_reserve(q, rows));
+  HIP_TRY(hipMemcpyAsync(q->lat, lat, (size_t)rows * kRvqIn * 4, hipMemcpyHostToDevice, q->stream));
+  TRY(rvq_encode_async_impl(q, batch, frames, q->lat, q->codes));
+  HIP_TRY(hipMemcpyAsync(codes, q->codes, (size_t)rows * q->n_q * 4, hipMemcpyDeviceToHost, q->stream));
+  HIP_TRY(hipStreamSynchronize(q->stream));
+  return 0;
+}
+
 static int device_count_impl(int* count) {
   HIP_TRY(hipGetDeviceCount(count));
   return 0;
@@ -2301,6 +2442,29 @@ int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* s
 
 int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {
   return guarded([&] { return bench_row_stats_impl(device, x, rows, k, norm, out, stream); });
+}
+
+int svl_rvq_create(const svl_tensor* tensors, size_t count, int32_t n_q, int32_t bins, int device, svl_rvq** out) {
+  return guarded([&] { return rvq_create_impl(tensors, count, n_q, bins, device, out); });
+}
+
+void svl_rvq_destroy(svl_rvq* rvq) { delete rvq; }
+
+int svl_rvq_encode(svl_rvq* rvq, int32_t batch, int32_t frames, const float* latents, uint32_t* codes) {
+  return guarded([&] { return rvq_encode_impl(rvq, batch, frames, latents, codes); });
+}
+
+int svl_rvq_encode_async(svl_rvq* rvq, int32_t batch, int32_t frames, const float* d_latents, uint32_t* d_codes) {
+  return guarded([&] { return rvq_encode_async_impl(rvq, batch, frames, d_latents, d_codes); });
+}
+
+int svl_rvq_synchronize(svl_rvq* rvq) {
+  return guarded([&] {
+    if (!rvq) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+    HIP_TRY(hipSetDevice(rvq->device));
+    HIP_TRY(hipStreamSynchronize(rvq->stream));
+    return 0;
+  });
 }
 
 int svl_model_create(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {

@@ -46,7 +46,8 @@ EXPORTS = [
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
     "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase",
     "svl_tts_step", "svl_tts_step_async", "svl_stt_recognize_turns", "svl_stt_recognize_turns_async",
-    "svl_state_load_voice",
+    "svl_state_load_voice", "svl_rvq_create", "svl_rvq_destroy", "svl_rvq_encode", "svl_rvq_encode_async",
+    "svl_rvq_synchronize",
 ]
 
 
@@ -134,11 +135,18 @@ def load_library(path: str = LIB_PATH):
     L.svl_stt_recognize_turns.argtypes = [vp, vp, i64, vp, C.POINTER(TurnConfig), vp, vp, vp]
     L.svl_stt_recognize_turns_async.argtypes = [vp, vp, i64, vp, C.POINTER(TurnConfig), vp, vp, vp]
     L.svl_tts_step_async.argtypes = [vp, vp, vp, vp, i32, vp, vp]
+    L.svl_rvq_create.argtypes = [C.POINTER(Tensor), sz, i32, i32, C.c_int, C.POINTER(vp)]
+    L.svl_rvq_destroy.argtypes = [vp]
+    L.svl_rvq_destroy.restype = None
+    L.svl_rvq_encode.argtypes = [vp, i32, i32, vp, vp]
+    L.svl_rvq_encode_async.argtypes = [vp, i32, i32, vp, vp]
+    L.svl_rvq_synchronize.argtypes = [vp]
     L.svl_bench_phase.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int)]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
     L.svl_bench_row_stats.argtypes = [C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp]
     for name in EXPORTS:
-        if name not in ("svl_last_error", "svl_model_destroy", "svl_state_destroy", "svl_state_stream"):
+        if name not in ("svl_last_error", "svl_model_destroy", "svl_state_destroy", "svl_state_stream",
+                        "svl_rvq_destroy"):
             getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -182,6 +190,59 @@ def make_config(cfg: dict) -> Config:
     for k, v in cfg.items():
         setattr(c, k, v)
     return c
+
+
+def _tensor_array(tensors: dict):
+    keep = []
+    arr = (Tensor * len(tensors))()
+    for i, (name, (dtype, shape, data)) in enumerate(tensors.items()):
+        data = np.ascontiguousarray(data)
+        nm = name.encode()
+        keep += [data, nm]
+        arr[i].name = nm
+        arr[i].dtype = dtype
+        arr[i].ndim = len(shape)
+        for j, s in enumerate(shape):
+            arr[i].shape[j] = s
+        arr[i].data = data.ctypes.data
+    return arr, keep
+
+
+class Rvq:
+    """Mimi's split residual vector quantizer on one GPU (svl_rvq_*, SVL/stt/model.rs:84-174).
+    ``tensors``: name -> (dtype code, shape, ndarray), the names of svl.h."""
+
+    def __init__(self, tensors: dict, n_q: int, bins: int, device: int = 0):
+        L = load_library()
+        arr, keep = _tensor_array(tensors)
+        h = C.c_void_p()
+        _check(L.svl_rvq_create(arr, len(tensors), n_q, bins, device, C.byref(h)))
+        self.h, self.n_q, self.bins = h, n_q, bins
+
+    def close(self):
+        if getattr(self, "h", None):
+            load_library().svl_rvq_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def encode(self, latents) -> np.ndarray:
+        """latents [batch, 512, frames] -> codes [batch, frames, n_q] (uint32)."""
+        x = np.ascontiguousarray(latents, dtype=np.float32)
+        b, c, t = x.shape
+        if c != 512:
+            raise ValueError("512 latent channels expected")
+        codes = np.empty((b, t, self.n_q), np.uint32)
+        _check(load_library().svl_rvq_encode(self.h, b, t, _p(x), _p(codes)))
+        return codes
+
+    def encode_async(self, batch: int, frames: int, d_latents: int, d_codes: int) -> None:
+        """Device-pointer variant: enqueues on the quantizer's stream and returns."""
+        _check(load_library().svl_rvq_encode_async(self.h, batch, frames, C.c_void_p(d_latents), C.c_void_p(d_codes)))
+
+    def synchronize(self) -> None:
+        _check(load_library().svl_rvq_synchronize(self.h))
 
 
 class Model:

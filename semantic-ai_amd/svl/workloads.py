@@ -300,3 +300,38 @@ def voice_tensors(keys, values, pad_to: int = 0) -> dict:
         out[m + "/pad"] = (6, (1,), np.array([0], np.int64))
     return out
 
+
+
+# ---- the STT quantizer (SVL/stt/model.rs:84-174; Kyutai STT: 32 codebooks of 2048 entries) -------
+
+RVQ_NQ, RVQ_BINS = 32, 2048
+
+
+def rvq_weights(n_q: int = RVQ_NQ, bins: int = RVQ_BINS, seed: int = 0):
+    """Seeded quantizer weights: input projections [256, 512] for the first and the rest quantizer,
+    embedding sums [n_q, bins, 256] ~ N(0, 1) and cluster usages [n_q, bins] in [0.5, 4) (a few
+    below the 1e-5 floor), stage order (the first quantizer's codebook, then the rest's)."""
+    w_first = normal(seed, "rvq.w_first", (256, 512), 0.05)
+    w_rest = normal(seed, "rvq.w_rest", (256, 512), 0.05)
+    sums = normal(seed, "rvq.sums", (n_q, bins, 256), 1.0)
+    usage = _rng(seed, "rvq.usage").uniform(0.5, 4.0, (n_q, bins)).astype(np.float32)
+    usage[:, ::97] = np.float32(1e-7)
+    return w_first, w_rest, sums, usage
+
+
+def rvq_tensors(w_first, w_rest, sums, usage) -> dict:
+    """The quantizer's tensors under the names svl_rvq_create reads (the checkpoint's, after its
+    `quantizer.` prefix), input projections as [256, 512, 1] convolution weights."""
+    out = {"rvq_first.input_proj.weight": (F32, (256, 512, 1), np.asarray(w_first, np.float32).reshape(256, 512, 1)),
+           "rvq_rest.input_proj.weight": (F32, (256, 512, 1), np.asarray(w_rest, np.float32).reshape(256, 512, 1))}
+    n_q, bins = sums.shape[0], sums.shape[1]
+    for s in range(n_q):
+        pre = "rvq_first.vq.layers.0._codebook." if s == 0 else f"rvq_rest.vq.layers.{s - 1}._codebook."
+        out[pre + "embedding_sum"] = (F32, (bins, 256), np.ascontiguousarray(sums[s]))
+        out[pre + "cluster_usage"] = (F32, (bins,), np.ascontiguousarray(usage[s]))
+    return out
+
+
+def rvq_latents(batch: int, frames: int, seed: int = 0) -> np.ndarray:
+    """Seeded encoder latents [batch, 512, frames] ~ N(0, 1)."""
+    return normal(seed, f"rvq.latents.{batch}.{frames}", (batch, 512, frames), 1.0)
