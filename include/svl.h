@@ -52,7 +52,9 @@ typedef enum {
 typedef enum { SVL_F32 = 0, SVL_BF16 = 1, SVL_F16 = 2, SVL_Q8_0 = 3, SVL_Q4K = 4, SVL_Q4_0 = 5, SVL_I64 = 6 } svl_dtype;
 
 typedef enum { SVL_NORM_LAYER = 0, SVL_NORM_RMS = 1 } svl_norm;          /* transformer.rs:12-16 */
-typedef enum { SVL_FF_PLAIN_GELU = 0, SVL_FF_GATED_SILU = 1 } svl_ff;    /* transformer.rs:18-24 */
+/* transformer.rs:18-24: linear2(gelu(linear1(x))) with the tanh GELU, the gated SiLU, or the plain
+ * feed-forward with erf GELU (`exact_gelu`, the Kyutai STT Mimi's transformers, mimi.rs:47-48) */
+typedef enum { SVL_FF_PLAIN_GELU = 0, SVL_FF_GATED_SILU = 1, SVL_FF_PLAIN_GELU_ERF = 2 } svl_ff;
 typedef enum { SVL_MODEL_TRANSFORMER = 0, SVL_MODEL_STT = 1, SVL_MODEL_TTS = 2 } svl_model_kind;
 /* FlowKind (SVL/tts/config.rs:170-195): LSD (two flow times), flow matching (one), drifting and
  * pointwise (none). */

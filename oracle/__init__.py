@@ -22,7 +22,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, BF16, F16, Q8_0, Q4K, Q4_0 = 0, 1, 2, 3, 4, 5
 NORM_LAYER, NORM_RMS = 0, 1
-FF_PLAIN, FF_GATED = 0, 1
+FF_PLAIN, FF_GATED, FF_PLAIN_ERF = 0, 1, 2
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
 FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 
@@ -98,7 +98,7 @@ def lib():
             L.svlo_get_fma.restype = C.c_int
             L.svlo_dot.argtypes = [vp, vp, sz]
             L.svlo_dot.restype = C.c_float
-            for name in ["svlo_exp", "svlo_silu", "svlo_gelu_tanh"]:
+            for name in ["svlo_exp", "svlo_silu", "svlo_gelu_tanh", "svlo_gelu_erf"]:
                 getattr(L, name).argtypes = [C.c_float]
                 getattr(L, name).restype = C.c_float
             L.svlo_silu_n.argtypes = [vp, sz]
@@ -319,6 +319,10 @@ def silu_n(x) -> np.ndarray:
     y = np.array(x, dtype=np.float32, copy=True).ravel()
     lib().svlo_silu_n(_p(y), y.size)
     return y.reshape(np.shape(x))
+
+
+def gelu_erf(x: float) -> float:
+    return lib().svlo_gelu_erf(float(x))
 
 
 def gelu_tanh_n(x) -> np.ndarray:

@@ -95,6 +95,13 @@ float svlo_gelu_tanh(float x) {
     return x / (1.0f + svlo_exp(-2.0f * y));
 }
 
+/* [candle hypothesis] Tensor::gelu_erf (SVL/nn/transformer.rs:446-447) for f32: evaluated in f64
+ * as (erf(v / sqrt 2) + 1) * 0.5 * v with the C library's erf, rounded to f32. */
+float svlo_gelu_erf(float x) {
+    const double v = (double)x;
+    return (float)((erf(v / 1.4142135623730951) + 1.0) * 0.5 * v);
+}
+
 void svlo_silu_n(float* x, size_t n) {
     for (size_t i = 0; i < n; ++i) x[i] = svlo_silu(x[i]);
 }

@@ -574,7 +574,11 @@ static int layer_forward(const svlo_model* m, const layer_t* L, kvcache_t* cache
     } else {
         float* hid = (float*)malloc(sizeof(float) * rows * F);
         linear_forward(&L->ff1, h, rows, hid);
-        svlo_gelu_tanh_n(hid, rows * F);
+        if (c->ff_kind == SVLO_FF_PLAIN_ERF) {
+            for (size_t j = 0; j < rows * F; ++j) hid[j] = svlo_gelu_erf(hid[j]);
+        } else {
+            svlo_gelu_tanh_n(hid, rows * F);
+        }
         linear_forward(&L->ff2, hid, rows, upd);
         free(hid);
     }

@@ -67,6 +67,7 @@ float svlo_dot(const float* a, const float* b, size_t n);
 float svlo_exp(float x);
 float svlo_silu(float x);
 float svlo_gelu_tanh(float x);
+float svlo_gelu_erf(float x);
 void svlo_silu_n(float* x, size_t n);
 void svlo_gelu_tanh_n(float* x, size_t n);
 void svlo_matvec(const float* x, const float* w, const float* bias, float* y, size_t n, size_t k);
@@ -113,7 +114,7 @@ void svlo_rvq_encode(const svlo_rvq* q, size_t batch, size_t frames, const float
 
 enum { SVLO_F32 = 0, SVLO_BF16 = 1, SVLO_F16 = 2, SVLO_Q8_0 = 3, SVLO_Q4K = 4, SVLO_Q4_0 = 5 };
 enum { SVLO_NORM_LAYER = 0, SVLO_NORM_RMS = 1 };
-enum { SVLO_FF_PLAIN = 0, SVLO_FF_GATED = 1 };
+enum { SVLO_FF_PLAIN = 0, SVLO_FF_GATED = 1, SVLO_FF_PLAIN_ERF = 2 };
 enum { SVLO_MODEL_TRANSFORMER = 0, SVLO_MODEL_STT = 1, SVLO_MODEL_TTS = 2 };
 /* FlowKind (SVL/tts/config.rs:170-185) */
 enum { SVLO_FLOW_LSD = 0, SVLO_FLOW_MATCHING = 1, SVLO_FLOW_DRIFTING = 2, SVLO_FLOW_POINTWISE = 3 };

@@ -75,6 +75,13 @@ __device__ __forceinline__ float ref_gelu_tanh(float x) {
   float y = 0.7978846f * fmaf(a, x2, x);
   return x / (1.0f + ref_exp(-2.0f * y));
 }
+// Tensor::gelu_erf (SVL/nn/transformer.rs:446-447) as candle evaluates it for f32 [candle
+// hypothesis]: in f64, (erf(v / sqrt 2) + 1) * 0.5 * v, rounded to f32; erf is the device
+// library's f64 erf.
+__device__ __forceinline__ float ref_gelu_erf(float x) {
+  const double v = (double)x;
+  return (float)((erf(v / 1.4142135623730951) + 1.0) * 0.5 * v);
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -8,7 +8,7 @@ namespace svl {
 
 enum WeightFmt { FMT_F32 = 0, FMT_BF16 = 1, FMT_Q8_0 = 3, FMT_Q4K = 4, FMT_F32C = 5, FMT_BF16C = 6, FMT_Q4_0 = 7 };
 enum NormKind { NORM_NONE = 0, NORM_LAYER = 1, NORM_RMS = 2 };
-enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 3, EPI_GELU = 4 };
+enum Epilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU_GATE = 2, EPI_QKV_ROPE = 3, EPI_GELU = 4, EPI_GELU_ERF = 5 };
 
 // One linear layer as held on the device.
 //   FMT_F32 / FMT_BF16: w = [out][in] row-major.

@@ -490,6 +490,9 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int b, int row,
     case EPI_GELU:
       st_co(a.y + (size_t)b * a.y_stride + row, ref_gelu_tanh(y));
       break;
+    case EPI_GELU_ERF:
+      st_co(a.y + (size_t)b * a.y_stride + row, ref_gelu_erf(y));
+      break;
     case EPI_SILU_GATE: {
       // FeedForwardLayer::forward, gated (SVL/nn/transformer.rs:453-461): silu(gate) * value
       float g = ref_silu(y);

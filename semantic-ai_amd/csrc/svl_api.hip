@@ -678,7 +678,8 @@ int check_config(const svl_config* c) {
   if (c->num_heads % c->num_kv_heads) return set_error(SVL_ERR_CONFIG, "num_heads must be a multiple of num_kv_heads");
   if (c->ff_hidden <= 0) return set_error(SVL_ERR_CONFIG, "ff_hidden must be positive");
   if (c->norm_kind != SVL_NORM_LAYER && c->norm_kind != SVL_NORM_RMS) return set_error(SVL_ERR_CONFIG, "unknown norm");
-  if (c->ff_kind != SVL_FF_PLAIN_GELU && c->ff_kind != SVL_FF_GATED_SILU) return set_error(SVL_ERR_CONFIG, "unknown feed-forward");
+  if (c->ff_kind != SVL_FF_PLAIN_GELU && c->ff_kind != SVL_FF_GATED_SILU && c->ff_kind != SVL_FF_PLAIN_GELU_ERF)
+    return set_error(SVL_ERR_CONFIG, "unknown feed-forward");
   if (c->context < 0) return set_error(SVL_ERR_CONFIG, "context must be >= 0");
   if (c->kv_dtype != SVL_F32 && c->kv_dtype != SVL_BF16) return set_error(SVL_ERR_CONFIG, "kv_dtype must be F32 or BF16");
   if (c->quantize != 0 && c->quantize != SVL_Q8_0 && c->quantize != SVL_Q4_0 && c->quantize != SVL_Q4K)
@@ -907,7 +908,7 @@ void build_layers(const svl_model* m, const svl_state* s, std::vector<Phase>& ou
       f.g.epi = EPI_SILU_GATE;
       f.g.ff_hidden = c.ff_hidden;
     } else {
-      f.g.epi = EPI_GELU;
+      f.g.epi = c.ff_kind == SVL_FF_PLAIN_GELU_ERF ? EPI_GELU_ERF : EPI_GELU;
     }
     add_gemv(s, out, f);
     // feed-forward out + residual

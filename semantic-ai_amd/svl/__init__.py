@@ -30,7 +30,7 @@ LIB_PATH = os.environ.get("SVL_LIBRARY") or os.path.join(PKG, "lib", "libsvl.so"
 
 F32, BF16, F16, Q8_0, Q4K, Q4_0, I64 = 0, 1, 2, 3, 4, 5, 6
 NORM_LAYER, NORM_RMS = 0, 1
-FF_PLAIN_GELU, FF_GATED_SILU = 0, 1
+FF_PLAIN_GELU, FF_GATED_SILU, FF_PLAIN_GELU_ERF = 0, 1, 2
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
 FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 

@@ -24,7 +24,7 @@ import numpy as np
 
 F32, BF16, F16, Q8_0, Q4K, Q4_0 = 0, 1, 2, 3, 4, 5
 NORM_LAYER, NORM_RMS = 0, 1
-FF_PLAIN, FF_GATED = 0, 1
+FF_PLAIN, FF_GATED, FF_PLAIN_ERF = 0, 1, 2
 MODEL_TRANSFORMER, MODEL_STT, MODEL_TTS = 0, 1, 2
 FLOW_LSD, FLOW_MATCHING, FLOW_DRIFTING, FLOW_POINTWISE = 0, 1, 2, 3
 
@@ -95,6 +95,12 @@ S2_SMALL = stt_shape("stt-small-q4k", 512, 2, 4, 4.5, 40, card=64, n_q=4, text_c
 T1_SMALL = tts_shape("tts-small", 256, 2, 4, 1024, flow_dim=64, flow_depth=2)
 
 assert S1.ff_hidden == 5632 and S2.ff_hidden == 6912
+
+# The Kyutai STT Mimi's encoder transformer (SVL/stt/model.rs:60-70, SVL/nn/mimi.rs:87-103): d 512,
+# 8 layers of 8 heads, erf-GELU feed-forward 2048, LayerNorm 1e-5, layer scale, context 250; it
+# runs at the SEANet frame rate (25 Hz), between the SEANet encoder and the downsampling.
+MIMI_ENC = Shape("mimi-encoder-transformer", MODEL_TRANSFORMER, 512, 8, 8, 8, 64, FF_PLAIN_ERF, 2048, NORM_LAYER,
+                 1e-5, 250, layer_scale=1)
 
 
 def _rng(seed: int, name: str) -> np.random.Generator:

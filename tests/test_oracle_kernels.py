@@ -61,6 +61,22 @@ def test_activations_match_candle_points():
     assert np.max(np.abs(oracle.gelu_tanh_n(x) - gelu)) < 1e-6
 
 
+def test_gelu_erf_is_the_rounded_float64_definition():
+    """Tensor::gelu_erf (transformer.rs:446-447, the Mimi transformers' exact GELU): the float64
+    definition x (1 + erf(x / sqrt 2)) / 2 (scipy's erf) rounded to float32, on 400k points and at
+    the limits (0, -0, large magnitudes: x and -0)."""
+    from scipy.special import erf
+    x = np.concatenate([np.linspace(-12, 12, 400001, dtype=np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 1e-8, 40.0, -40.0, 3e38, -3e38], np.float32)])
+    got = np.array([oracle.gelu_erf(v) for v in x], np.float32)
+    xd = x.astype(np.float64)
+    want = ((erf(xd / np.sqrt(2.0)) + 1.0) * 0.5 * xd).astype(np.float32)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1 and np.mean(ulp == 0) > 0.9999
+    assert got[-4] == 40.0 and got[-2] == np.float32(3e38)  # x for large x
+    assert all(np.signbit(got[i]) and got[i] == 0.0 for i in (-8, -3, -1))  # -0, -40, -3e38: -0
+
+
 def test_exp_few_ulp_and_limits(fma_mode):
     x = np.linspace(-87, 88, 200_001, dtype=np.float32)
     got = np.array([oracle.exp(v) for v in x[::97]], dtype=np.float32)
