@@ -28,7 +28,9 @@ int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, f
 /* Launches phase `phase` (program order) of the state's decode-step program -- program 0 the
  * STT step, 1 the TTS backbone step -- `reps` times back to back on the state's stream, after one
  * untimed launch, and returns the mean time per launch from HIP events around the batch (which
- * includes the gap between back-to-back launches).  info[6] receives the phase's kind, weight
+ * includes the gap between back-to-back launches).  An attention phase launches as the state's
+ * next step would (split over several units per head when its streams' visible keys call for
+ * it).  info[6] receives the phase's kind, weight
  * format, linear rows and input width (GEMV phases), work units and attention heads per unit.
  * The phases recompute their outputs from the state's current contents; use a state whose
  * contents do not matter afterwards (a duplicate). */

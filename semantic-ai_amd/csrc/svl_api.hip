@@ -2288,7 +2288,7 @@ static int bench_phase_impl(const svl_model* m, svl_state* s, int program, int p
   info[2] = (ph.kind == PH_GEMV || ph.kind == PH_QUANT || ph.kind == PH_QGEMM) ? ph.g.L.out : 0;
   info[3] = (ph.kind == PH_GEMV || ph.kind == PH_QUANT || ph.kind == PH_QGEMM) ? ph.g.L.in : 0;
   info[4] = ph.units;
-  info[5] = ph.kind == PH_ATTN ? ph.at.hpu : 0;
+  info[5] = ph.kind == PH_ATTN ? ph.at.hpu : 0;  // heads per unit (a split launch: 1 head, split over units)
   if (ph.kind == PH_GEMV && ph.g.epi == EPI_QKV_ROPE) TRY(check_room(s, 1));
   HIP_TRY(hipSetDevice(m->device));
   TRY(refresh_attn_order(s));
@@ -2307,7 +2307,14 @@ static int bench_phase_impl(const svl_model* m, svl_state* s, int program, int p
   P.pos = s->pos;
   P.B = s->B;
   P.n_steps = 1;
-  HIP_TRY(launch_phase(ph, P, 0, p->smem, s->stream));  // warm-up
+  // an attention phase launches as the step would at the state's positions (split or not)
+  const int split = ph.kind == PH_ATTN ? attn_split(s, 0) : 1;
+  auto one = [&]() -> int {
+    if (split > 1) return launch_split(s, ph, P, 0, split);
+    HIP_TRY(launch_phase(ph, P, 0, p->smem, s->stream));
+    return 0;
+  };
+  TRY(one());  // warm-up
   hipEvent_t e0, e1;
   HIP_TRY(hipEventCreate(&e0));
   hipError_t e = hipEventCreate(&e1);
@@ -2316,7 +2323,13 @@ static int bench_phase_impl(const svl_model* m, svl_state* s, int program, int p
     HIP_TRY(e);
   }
   e = hipEventRecord(e0, s->stream);
-  for (int r = 0; r < reps && e == hipSuccess; ++r) e = launch_phase(ph, P, 0, p->smem, s->stream);
+  int rc = 0;
+  for (int r = 0; r < reps && e == hipSuccess && !rc; ++r) rc = one();
+  if (rc) {
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return rc;
+  }
   if (e == hipSuccess) e = hipEventRecord(e1, s->stream);
   if (e == hipSuccess) e = hipEventSynchronize(e1);
   float ms = 0.0f;
