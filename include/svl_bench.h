@@ -25,6 +25,12 @@ int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* s
  * for numerics tests on chosen rows. */
 int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream);
 
+/* The step kernels' element functions on n f32 values (x, y: device memory, enqueued on `stream`):
+ * kind 0 exp (the reference's Cody-Waite + Taylor exp), 1 SiLU, 2 GELU-tanh, 3 erf GELU -- the
+ * functions the FF epilogues, the attention softmax and the flow head evaluate.  Exposes them for
+ * the known-answer sweeps of the numerics tests. */
+int svl_bench_activation(int device, int kind, const float* x, size_t n, float* y, void* stream);
+
 /* Launches phase `phase` (program order) of the state's decode-step program -- program 0 the
  * STT step, 1 the TTS backbone step -- `reps` times back to back on the state's stream, after one
  * untimed launch, and returns the mean time per launch from HIP events around the batch (which

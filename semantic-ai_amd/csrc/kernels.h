@@ -284,6 +284,8 @@ hipError_t launch_bf16_to_f32(const uint16_t* x, float* y, size_t n, hipStream_t
 hipError_t launch_kv_to_f32(const void* src, int kv_bf16, float* dst, size_t n, hipStream_t s);
 hipError_t launch_f32_to_kv(const float* src, void* dst, int kv_bf16, size_t n, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
+// y = exp / SiLU / GELU-tanh / erf GELU (kind 0 .. 3) of x, as the step kernels evaluate them.
+hipError_t launch_activation(int kind, const float* x, size_t n, float* y, hipStream_t s);
 hipError_t launch_fill_i32(int* p, int v, size_t n, hipStream_t s);
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
 hipError_t launch_row_stats(const float* x, int rows, int K, int norm, float* out, hipStream_t s);

@@ -990,6 +990,19 @@ hipError_t launch_row_stats(const float* x, int rows, int K, int norm, float* ou
   return hipGetLastError();
 }
 
+__global__ void activation_kernel(int kind, const float* x, size_t n, float* y) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  y[i] = kind == 0 ? ref_exp(v) : kind == 1 ? ref_silu(v) : kind == 2 ? ref_gelu_tanh(v) : ref_gelu_erf(v);
+}
+
+hipError_t launch_activation(int kind, const float* x, size_t n, float* y, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(activation_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kind, x, n, y);
+  return hipGetLastError();
+}
+
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s) {
   const size_t n = bytes / 16;
   const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 8192);

@@ -1733,6 +1733,15 @@ static int bench_row_stats_impl(int device, const float* x, int rows, int k, int
   return 0;
 }
 
+static int bench_activation_impl(int device, int kind, const float* x, size_t n, float* y, void* stream) {
+  if ((!x || !y) && n) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  if (kind < 0 || kind > 3) return set_error(SVL_ERR_INVALID_INPUT, "unknown function %d", kind);
+  if (n > ((size_t)1 << 31)) return set_error(SVL_ERR_INVALID_INPUT, "at most 2^31 values");
+  HIP_TRY(hipSetDevice(device));
+  HIP_TRY(launch_activation(kind, x, n, y, (hipStream_t)stream));
+  return 0;
+}
+
 static int model_create_impl(const svl_config* cfg, const svl_tensor* tensors, size_t count, int device, svl_model** out) {
   if (!cfg || !out || (!tensors && count)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
   *out = nullptr;
@@ -2452,6 +2461,10 @@ int svl_device_count(int* count) {
 
 int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* stream) {
   return guarded([&] { return bench_copy_impl(device, src, dst, bytes, stream); });
+}
+
+int svl_bench_activation(int device, int kind, const float* x, size_t n, float* y, void* stream) {
+  return guarded([&] { return bench_activation_impl(device, kind, x, n, y, stream); });
 }
 
 int svl_bench_row_stats(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {

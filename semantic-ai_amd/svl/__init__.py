@@ -44,7 +44,7 @@ EXPORTS = [
     "svl_state_synchronize", "svl_state_stream", "svl_transformer_forward", "svl_stt_step",
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
-    "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase",
+    "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase", "svl_bench_activation",
     "svl_tts_step", "svl_tts_step_async", "svl_stt_recognize_turns", "svl_stt_recognize_turns_async",
     "svl_state_load_voice", "svl_rvq_create", "svl_rvq_destroy", "svl_rvq_encode", "svl_rvq_encode_async",
     "svl_rvq_synchronize",
@@ -144,6 +144,7 @@ def load_library(path: str = LIB_PATH):
     L.svl_bench_phase.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int)]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
     L.svl_bench_row_stats.argtypes = [C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp]
+    L.svl_bench_activation.argtypes = [C.c_int, C.c_int, vp, sz, vp, vp]
     for name in EXPORTS:
         if name not in ("svl_last_error", "svl_model_destroy", "svl_state_destroy", "svl_state_stream",
                         "svl_rvq_destroy"):
@@ -162,6 +163,19 @@ def _check(rc: int) -> None:
 def _p(a: np.ndarray):
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(C.c_void_p)
+
+
+def activation(kind: int, x, device: int = 0) -> np.ndarray:
+    """The step kernels' exp (0), SiLU (1), GELU-tanh (2) or erf GELU (3) of x on the GPU
+    (svl_bench_activation)."""
+    from . import hip
+    v = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    dx = hip.DeviceBuffer.from_array(v)
+    dy = hip.DeviceBuffer(v.nbytes)
+    _check(load_library().svl_bench_activation(device, kind, C.c_void_p(dx.address), v.size, C.c_void_p(dy.address),
+                                                None))
+    hip.synchronize()
+    return dy.to_array(np.float32, v.size).reshape(np.shape(x))
 
 
 def row_stats(x: np.ndarray, norm: int, device: int = 0) -> np.ndarray:
