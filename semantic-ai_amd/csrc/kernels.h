@@ -68,7 +68,7 @@ struct GemvArgs {
                        // stream processed together, prefill); 0 or 1: one ring per batch row
   int advance_pos;
   // batched Q8_0 path (PH_QUANT / PH_QGEMM): the quantized input rows of the whole batch
-  int8_t* xq;          // [B][L.in]
+  int8_t* xq;          // [ceil(L.in / 128)][B][128]: chunk-major, so that a chunk of all rows is contiguous
   float* xdq;          // [B][L.in / 32] (f16-rounded block scales)
 };
 
@@ -202,10 +202,12 @@ constexpr int kMaxRingSlots = 12000;
 constexpr size_t kStaticLdsReserve = 8192;  // static LDS of the step kernels (barrier state, positions)  // KV ring slots per stream and layer (attention keeps a head's scores in LDS)
 constexpr int kGemmChunk = 4;    // Q8_0 blocks (128 bytes of K) per LDS stage of a GEMM unit
 constexpr int kGemmStages = 6;   // LDS stages of a GEMM unit (kGemmStages - 1 chunks in flight)
-// weights [kTileRows][128] | activations [kTileBatch][128] | weight scales [kTileRows][4] (f16 in
-// the low half of a dword: a 2-byte direct load fills a 4-byte LDS slot per lane) | activation
-// scales [kTileBatch][4] f32
-constexpr int kGemmStageBytes = kTileRows * 128 + kTileBatch * 128 + kTileRows * kGemmChunk * 4 + kTileBatch * kGemmChunk * 4;
+// A GEMM stage: weights [kTileRows][128] | activations [kTileBatch][128] | weight scales
+// [kTileRows][4] f16 (two 4-byte direct loads per row) | activation scales [kTileBatch][4] f32.  The
+// operand rows come in groups of 8 (one wave's 1 KB direct load), each group kGemmGroupBytes
+// apart: the 128 bytes between groups put rows j and j + 8 of an MFMA operand in different banks.
+constexpr int kGemmGroupBytes = 1152;
+constexpr int kGemmStageBytes = kTileRows / 8 * kGemmGroupBytes + kTileBatch / 8 * kGemmGroupBytes + kTileRows * kGemmChunk * 4 + kTileBatch * kGemmChunk * 4;
 constexpr int kSyncChunks = 2;   // stages consumed between two row-wave barriers
 // s_waitcnt immediates (vmcnt only): the direct loads of the kGemmStages - 2 kSyncChunks chunks
 // after the ones about to be consumed may still be in flight (2 or 3 loads per wave and chunk), or

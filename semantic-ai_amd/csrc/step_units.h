@@ -1108,8 +1108,12 @@ __device__ __forceinline__ void quant_unit(const GemvArgs& a, int b, unsigned ch
   }
   quantize_row4(v, K, xq, xdq);
   rs.sync();
-  uint32_t* dq = (uint32_t*)(a.xq + (size_t)b * K);
-  for (int i = threadIdx.x; i < K / 4; i += kRowThreads) st_co(dq + i, ((const uint32_t*)xq)[i]);
+  // chunk-major: the 128-byte chunk c of every batch row is one contiguous run of B x 128 bytes, so
+  // that the GEMM units' concurrent reads of a chunk spread over the L2 channels
+  for (int i = threadIdx.x; i < K / 4; i += kRowThreads) {
+    const int c = i / 32, w = i % 32;
+    st_co((uint32_t*)(a.xq + ((size_t)c * a.B + b) * 128) + w, ((const uint32_t*)xq)[i]);
+  }
   for (int i = threadIdx.x; i < nb; i += kRowThreads) st_co(a.xdq + (size_t)b * nb + i, xdq[i]);
 }
 
@@ -1146,7 +1150,7 @@ __device__ __forceinline__ void lds_dma(const void* src, unsigned char* dst_wave
 struct GemmStage {
   unsigned char* w;   // [kTileRows][128] int8, swizzled
   unsigned char* x;   // [kTileBatch][128] int8, swizzled
-  uint32_t* dw;       // [kTileRows][kGemmChunk] f16 in the low half
+  uint32_t* dw;       // [kTileRows][kGemmChunk / 2] f16 pairs
   float* dx;          // [kTileBatch][kGemmChunk]
 };
 
@@ -1154,21 +1158,20 @@ __device__ __forceinline__ GemmStage gemm_stage(unsigned char* smem, int s) {
   unsigned char* base = smem + kTileRows * kTileBatch * 4 + s * kGemmStageBytes;
   GemmStage g;
   g.w = base;
-  g.x = base + kTileRows * 128;
-  g.dw = (uint32_t*)(g.x + kTileBatch * 128);
+  g.x = base + kTileRows / 8 * kGemmGroupBytes;
+  g.dw = (uint32_t*)(g.x + kTileBatch / 8 * kGemmGroupBytes);
   g.dx = (float*)(g.dw + kTileRows * kGemmChunk);
   return g;
 }
 
 // Byte offset of 16-byte segment `seg` of row j in a swizzled 128-byte row.
-__device__ __forceinline__ int swz(int j, int seg) { return j * 128 + ((seg ^ (j & 7)) << 4); }
+__device__ __forceinline__ int swz(int j, int seg) {
+  return j * 128 + (j >> 3) * 128 + ((seg ^ (j & 7)) << 4);
+}
+__device__ __forceinline__ uint32_t u4c(const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(size_t)(const SVL_LDS void*)p; }
 
-// One lane's operands of a chunk: the A and B fragments of its four blocks, the weight scales of
-// its four D rows and the activation scales of its D column.  The reads and their wait are one
-// statement: the compiler would otherwise wait for every direct load still landing in the other
-// stages before the first read.
 // RowSync::sync for the GEMM loop, its LDS accesses written out so that the compiler does not
 // wait for the direct loads in flight before them (it cannot tell the counters from the stages).
 // Prior LDS reads of the wave have completed (gemm_read waits for them).
@@ -1205,41 +1208,110 @@ __device__ __forceinline__ void gemm_sync(RowSync& rs) {
 }
 
 struct GemmOps {
-  v_i8x8 a[4], b[4];
-  uint4 dw[4];
-  float4 dx;
+  v_i8x8 a[4], b[4];  // A (weight) and B (activation) fragments of blocks 0-3
+  uint4 dw[2];        // weight scales as f16 pairs: rows 4g, 4g + 1, then rows 4g + 2, 4g + 3
+  float4 dx;          // activation scales of the lane's column, blocks 0-3
 };
 
-__device__ __forceinline__ void gemm_read(const GemmStage& st, int ja, int jb, int g, int r0, GemmOps& o) {
-  uint32_t aa[4], ba[4], da[4];
+struct GemmAddr {
+  uint32_t a[4], b[4], w, x;
+};
+
+__device__ __forceinline__ GemmAddr gemm_addr(const GemmStage& st, int ja, int jb, int g, int r0) {
+  GemmAddr p;
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     const int seg = 2 * kk + g / 2, inner = 8 * (g & 1);
-    aa[kk] = lds_addr(st.w) + swz(ja, seg) + inner;
-    ba[kk] = lds_addr(st.x) + swz(jb, seg) + inner;
-    da[kk] = lds_addr(st.dw) + (r0 + 4 * g + kk) * (kGemmChunk * 4);
+    p.a[kk] = lds_addr(st.w) + swz(ja, seg) + inner;
+    p.b[kk] = lds_addr(st.x) + swz(jb, seg) + inner;
   }
-  const uint32_t xa = lds_addr(st.dx) + jb * (kGemmChunk * 4);
+  p.w = lds_addr(st.dw) + (r0 + 4 * g) * 8;
+  p.x = lds_addr(st.dx) + jb * (kGemmChunk * 4);
+  return p;
+}
+
+// One lane's operands of a chunk.  The reads and their wait are one statement: the compiler would
+// otherwise wait for every direct load still landing in the other stages before the first read.
+__device__ __forceinline__ void gemm_read(const GemmAddr& p, GemmOps& o) {
   asm volatile(
-      "ds_read_b64 %0, %13\n\t"
-      "ds_read_b64 %1, %14\n\t"
-      "ds_read_b64 %2, %15\n\t"
-      "ds_read_b64 %3, %16\n\t"
-      "ds_read_b64 %4, %17\n\t"
-      "ds_read_b64 %5, %18\n\t"
-      "ds_read_b64 %6, %19\n\t"
-      "ds_read_b64 %7, %20\n\t"
-      "ds_read_b128 %8, %21\n\t"
-      "ds_read_b128 %9, %22\n\t"
-      "ds_read_b128 %10, %23\n\t"
-      "ds_read_b128 %11, %24\n\t"
-      "ds_read_b128 %12, %25\n\t"
+      "ds_read_b64 %0, %11\n\t"
+      "ds_read_b64 %1, %12\n\t"
+      "ds_read_b64 %2, %13\n\t"
+      "ds_read_b64 %3, %14\n\t"
+      "ds_read_b64 %4, %15\n\t"
+      "ds_read_b64 %5, %16\n\t"
+      "ds_read_b64 %6, %17\n\t"
+      "ds_read_b64 %7, %18\n\t"
+      "ds_read_b128 %8, %19\n\t"
+      "ds_read_b128 %9, %19 offset:16\n\t"
+      "ds_read_b128 %10, %20\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(o.a[0]), "=&v"(o.a[1]), "=&v"(o.a[2]), "=&v"(o.a[3]), "=&v"(o.b[0]), "=&v"(o.b[1]), "=&v"(o.b[2]),
-        "=&v"(o.b[3]), "=&v"(o.dw[0]), "=&v"(o.dw[1]), "=&v"(o.dw[2]), "=&v"(o.dw[3]), "=&v"(o.dx)
-      : "v"(aa[0]), "v"(aa[1]), "v"(aa[2]), "v"(aa[3]), "v"(ba[0]), "v"(ba[1]), "v"(ba[2]), "v"(ba[3]), "v"(da[0]),
-        "v"(da[1]), "v"(da[2]), "v"(da[3]), "v"(xa)
+        "=&v"(o.b[3]), "=&v"(o.dw[0]), "=&v"(o.dw[1]), "=&v"(o.dx)
+      : "v"(p.a[0]), "v"(p.a[1]), "v"(p.a[2]), "v"(p.a[3]), "v"(p.b[0]), "v"(p.b[1]), "v"(p.b[2]), "v"(p.b[3]),
+        "v"(p.w), "v"(p.x)
       : "memory");
+}
+
+// The operands of two chunks in adjacent stages (the second at kGemmStageBytes further), one wait
+// for both.
+static_assert(kGemmStageBytes == 15360, "the offsets below");
+__device__ __forceinline__ void gemm_read2(const GemmAddr& p, GemmOps& o, GemmOps& q) {
+  asm volatile(
+      "ds_read_b64 %0, %22\n\t"
+      "ds_read_b64 %1, %23\n\t"
+      "ds_read_b64 %2, %24\n\t"
+      "ds_read_b64 %3, %25\n\t"
+      "ds_read_b64 %4, %26\n\t"
+      "ds_read_b64 %5, %27\n\t"
+      "ds_read_b64 %6, %28\n\t"
+      "ds_read_b64 %7, %29\n\t"
+      "ds_read_b128 %8, %30\n\t"
+      "ds_read_b128 %9, %30 offset:16\n\t"
+      "ds_read_b128 %10, %31\n\t"
+      "ds_read_b64 %11, %22 offset:15360\n\t"
+      "ds_read_b64 %12, %23 offset:15360\n\t"
+      "ds_read_b64 %13, %24 offset:15360\n\t"
+      "ds_read_b64 %14, %25 offset:15360\n\t"
+      "ds_read_b64 %15, %26 offset:15360\n\t"
+      "ds_read_b64 %16, %27 offset:15360\n\t"
+      "ds_read_b64 %17, %28 offset:15360\n\t"
+      "ds_read_b64 %18, %29 offset:15360\n\t"
+      "ds_read_b128 %19, %30 offset:15360\n\t"
+      "ds_read_b128 %20, %30 offset:15376\n\t"
+      "ds_read_b128 %21, %31 offset:15360\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o.a[0]), "=&v"(o.a[1]), "=&v"(o.a[2]), "=&v"(o.a[3]), "=&v"(o.b[0]), "=&v"(o.b[1]), "=&v"(o.b[2]),
+        "=&v"(o.b[3]), "=&v"(o.dw[0]), "=&v"(o.dw[1]), "=&v"(o.dx), "=&v"(q.a[0]), "=&v"(q.a[1]), "=&v"(q.a[2]),
+        "=&v"(q.a[3]), "=&v"(q.b[0]), "=&v"(q.b[1]), "=&v"(q.b[2]), "=&v"(q.b[3]), "=&v"(q.dw[0]), "=&v"(q.dw[1]),
+        "=&v"(q.dx)
+      : "v"(p.a[0]), "v"(p.a[1]), "v"(p.a[2]), "v"(p.a[3]), "v"(p.b[0]), "v"(p.b[1]), "v"(p.b[2]), "v"(p.b[3]),
+        "v"(p.w), "v"(p.x)
+      : "memory");
+}
+
+// The block products of a chunk (independent MFMAs).
+__device__ __forceinline__ void gemm_mfma(const GemmOps& o, v4i (&cc)[kGemmChunk]) {
+#pragma unroll
+  for (int kk = 0; kk < kGemmChunk; ++kk)
+    cc[kk] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+
+// The chunk's terms ((f32)dot * d_w) * d_x added to the lane's four outputs in block order; nk
+// (uniform) blocks of the chunk are in K.
+__device__ __forceinline__ void gemm_terms(const GemmOps& o, const v4i (&cc)[kGemmChunk], int nk, float (&acc)[4]) {
+  const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
+#pragma unroll
+  for (int kk = 0; kk < kGemmChunk; ++kk) {
+    if (kk >= nk) break;  // uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t dwp = u4c(o.dw[i >> 1], (i & 1) * 2 + (kk >> 1));
+      const float dw = f16_to_f32((uint16_t)(kk & 1 ? dwp >> 16 : dwp & 0xFFFF));
+      const float t = (float)cc[kk][i] * dw;
+      acc[i] = acc[i] + t * dxs[kk];
+    }
+  }
 }
 
 template <int TR>  // tile rows: 32 (waves 0-7 compute) or 16 (waves 0-3 compute)
@@ -1256,15 +1328,16 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
   float* Y = (float*)smem;            // [kTileRows][kTileBatch]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   // ---- loads of one chunk: wave w brings X rows 8w..8w+7.  TR = 32: waves 0-3 W rows 8w..8w+7,
-  // waves 4-5 the weight scales of rows 16 (w - 4) .., waves 6-7 the activation scales of batch
-  // rows 32 (w - 6) .. (two loads).  TR = 16: waves 0-1 W rows 8w..8w+7, wave 2 the weight
-  // scales, waves 4-7 the activation scales of batch rows 16 (w - 4) ...  Rows past the tile load
-  // the last row in use; blocks past K load the last block (their results are never used).
+  // wave 4 the weight scales (lane l: the f16 pair of blocks 2 (l % 2), + 1 of row l / 2), waves
+  // 6-7 the activation scales of batch rows 32 (w - 6) .. (two loads).  TR = 16: waves 0-1 W rows
+  // 8w..8w+7, wave 2 the weight scales, waves 4-7 the activation scales of batch rows 16 (w - 4) ..
+  // Rows past the tile load the last row in use; blocks past K load the last block (pair) in K
+  // (their results are never used).  The pairs are 4-byte aligned: K / 32 is even on this path.
   const int lrow = 8 * wave + lane / 8, lslot = lane % 8;
-  const int8_t* xsrc = a.xq + (size_t)(b0 + min(lrow, nbat - 1)) * K;
+  const int8_t* xsrc = a.xq + (size_t)(b0 + min(lrow, nbat - 1)) * 128;  // + chunk * B * 128
   const int8_t* wsrc = (const int8_t*)a.L.w +
                        (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(wave < TR / 8 ? lrow : 0, NR - 1)) * K;
-  const int srow = (TR == 32 ? 16 * (wave & 1) : 0) + lane / 4, sblk = lane % 4;
+  const int srow = lane / 2, sblk = 2 * (lane % 2);  // f16 pairs: blocks sblk, sblk + 1 of row srow
   const uint16_t* dwsrc = a.L.scale + (size_t)gemv_phys_row(a.epi, a.ff_hidden, i0, ni, min(srow, NR - 1)) * nb;
   const int xrow0 = (TR == 32 ? 32 * (wave & 1) : 16 * (wave & 3)) + lane / 4;
   const float* dxsrc0 = a.xdq + (size_t)(b0 + min(xrow0, nbat - 1)) * nb;
@@ -1273,25 +1346,27 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
     const GemmStage st = gemm_stage(smem, c % kGemmStages);
     const int seg = lslot ^ (lrow & 7);
     const int off = min(128 * c + 16 * seg, K - 16);
-    lds_dma<16, true>(xsrc + off, st.x + wave * 1024);
-    const int k = min(kGemmChunk * c + sblk, nb - 1);
+    lds_dma<16, true>(xsrc + (size_t)(off / 128) * a.B * 128 + off % 128, st.x + wave * kGemmGroupBytes);
+    const int k = min(kGemmChunk * c + sblk, nb - 2);  // weight scales
+    const int kx = min(kGemmChunk * c + lane % 4, nb - 1);                  // activation scales
     if constexpr (TR == 32) {
       if (wave < 4) {
-        lds_dma<16, false>(wsrc + off, st.w + wave * 1024);
+        lds_dma<16, false>(wsrc + off, st.w + wave * kGemmGroupBytes);
       } else if (wave < 6) {
-        lds_dma<2, false>(dwsrc + k, (unsigned char*)st.dw + (wave - 4) * 256);
+        if (wave == 4) lds_dma<4, false>(dwsrc + k, (unsigned char*)st.dw);
       } else {
-        lds_dma<4, true>(dxsrc0 + k, (unsigned char*)st.dx + (wave - 6) * 512);
-        lds_dma<4, true>(dxsrc1 + k, (unsigned char*)st.dx + (wave - 6) * 512 + 256);
+        lds_dma<4, true>(dxsrc0 + kx, (unsigned char*)st.dx + (wave - 6) * 512);
+        lds_dma<4, true>(dxsrc1 + kx, (unsigned char*)st.dx + (wave - 6) * 512 + 256);
       }
     } else {
-      if (wave < 2) lds_dma<16, false>(wsrc + off, st.w + wave * 1024);
-      else if (wave == 2) lds_dma<2, false>(dwsrc + k, (unsigned char*)st.dw);
-      else if (wave >= 4) lds_dma<4, true>(dxsrc0 + k, (unsigned char*)st.dx + (wave - 4) * 256);
+      if (wave < 2) lds_dma<16, false>(wsrc + off, st.w + wave * kGemmGroupBytes);
+      else if (wave == 2) lds_dma<4, false>(dwsrc + k, (unsigned char*)st.dw);
+      else if (wave >= 4) lds_dma<4, true>(dxsrc0 + kx, (unsigned char*)st.dx + (wave - 4) * 256);
     }
   };
   const int nch = (nb + kGemmChunk - 1) / kGemmChunk;
   constexpr int S = kSyncChunks, AHEAD = kGemmStages - kSyncChunks;  // chunks per sync, chunks issued ahead
+  static_assert(S == 2 && kGemmStages % 2 == 0, "an interval's two chunks sit in adjacent stages");
   __builtin_amdgcn_s_waitcnt(kVmWait0);  // no older stores interleave with the counted loads
   for (int c = 0; c < min(AHEAD, nch); ++c) issue(c);
   const int r0 = 16 * (wave / 4), c0 = 16 * (wave % 4);
@@ -1302,6 +1377,7 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
     if (c + AHEAD <= nch) {
       if (TR == 32 && wave >= 6) __builtin_amdgcn_s_waitcnt(kVmWait3);
       else if (TR == 16 && wave == 3) __builtin_amdgcn_s_waitcnt(kVmWait1);
+      else if (TR == 32 && wave == 5) __builtin_amdgcn_s_waitcnt(kVmWait1);
       else __builtin_amdgcn_s_waitcnt(kVmWait2);
     } else {
       __builtin_amdgcn_s_waitcnt(kVmWait0);
@@ -1310,28 +1386,23 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
 #pragma unroll
     for (int u = 0; u < S; ++u)
       if (c + AHEAD + u < nch) issue(c + AHEAD + u);
-#pragma unroll 1
-    for (int u = 0; u < S; ++u) {
-      if (c + u >= nch || wave >= TR / 4) break;  // uniform
-      GemmOps o;
-      gemm_read(gemm_stage(smem, (c + u) % kGemmStages), ja, jb, g, r0, o);
-      const float dxs[4] = {o.dx.x, o.dx.y, o.dx.z, o.dx.w};
-      // the chunk's block products first (independent), then their terms added in block order
-      const int nk = min(kGemmChunk, nb - kGemmChunk * (c + u));  // uniform: 4 except in a last partial chunk
-      v4i cc[kGemmChunk];
-#pragma unroll
-      for (int kk = 0; kk < kGemmChunk; ++kk)
-        cc[kk] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[kk], o.b[kk], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-      for (int kk = 0; kk < kGemmChunk; ++kk) {
-        if (kk >= nk) break;  // uniform
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t dwp = kk == 0 ? o.dw[i].x : (kk == 1 ? o.dw[i].y : (kk == 2 ? o.dw[i].z : o.dw[i].w));
-          const float dw = f16_to_f32((uint16_t)(dwp & 0xFFFF));
-          const float t = (float)cc[kk][i] * dw;
-          acc[i] = acc[i] + t * dxs[kk];
-        }
+    if (wave < TR / 4) {  // uniform
+      const GemmAddr pa = gemm_addr(gemm_stage(smem, c % kGemmStages), ja, jb, g, r0);
+      const int nk0 = min(kGemmChunk, nb - kGemmChunk * c);  // uniform: 4 except in a last partial chunk
+      if (c + 1 < nch) {  // both chunks of the interval, in adjacent stages (c is even)
+        GemmOps o, q;
+        gemm_read2(pa, o, q);
+        v4i cc[kGemmChunk], cq[kGemmChunk];
+        gemm_mfma(o, cc);
+        gemm_mfma(q, cq);
+        gemm_terms(o, cc, nk0, acc);
+        gemm_terms(q, cq, min(kGemmChunk, nb - kGemmChunk * (c + 1)), acc);
+      } else {
+        GemmOps o;
+        gemm_read(pa, o);
+        v4i cc[kGemmChunk];
+        gemm_mfma(o, cc);
+        gemm_terms(o, cc, nk0, acc);
       }
     }
   }

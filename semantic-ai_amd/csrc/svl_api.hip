@@ -178,7 +178,7 @@ struct svl_state {
   size_t fwd_cap = 0;
   uint32_t* tok_in = nullptr; // explicit tokens staging [B] + [B][n_q]
   void* stage = nullptr;      // STT: next step's audio embedding rows [B][n_q][d]
-  int8_t* xqb = nullptr;      // batched Q8_0 path: quantized input rows [B][width]
+  int8_t* xqb = nullptr;      // batched Q8_0 path: quantized input rows [width / 128][B][128]
   float* xdqb = nullptr;      //                    and their block scales [B][width / 32]
   uint32_t* tok_out = nullptr;  // [B] tokens, then the bad-token flag (EmbedArgs::bad_token)
   // RoPE rows of positions at or past the model table's cap, computed for each call
@@ -808,9 +808,10 @@ Phase gemv_phase(const svl_state* s, const LinearDev& L) {
 
 // A Q8_0 linear of a lockstep batch of at least kBatchMfma streams runs as two phases: the
 // input rows are normalized and quantized once (PH_QUANT, one unit per stream), then an MFMA
-// GEMM reads every weight block once per 64 streams (PH_QGEMM).  Otherwise one GEMV phase.
+// GEMM reads every weight block once per 64 streams (PH_QGEMM; its weight scales travel as f16
+// pairs, so the input width must be a multiple of 64).  Otherwise one GEMV phase.
 void add_gemv(const svl_state* s, std::vector<Phase>& out, Phase ph) {
-  if (ph.g.L.fmt == FMT_Q8_0 && s->B >= kBatchMfma) {
+  if (ph.g.L.fmt == FMT_Q8_0 && s->B >= kBatchMfma && ph.g.L.in % 64 == 0) {
     ph.g.xq = s->xqb;
     ph.g.xdq = s->xdqb;
     Phase q = ph;
@@ -1330,7 +1331,7 @@ int make_state(const svl_model* m, int32_t batch, int32_t capacity, svl_state** 
   }
   if (!rc && batch >= kBatchMfma) {
     const int wmax = std::max(std::max(c.d_model, c.num_heads * c.head_dim), c.ff_hidden);
-    rc = s->alloc(&p, (size_t)batch * wmax), s->xqb = (int8_t*)p;
+    rc = s->alloc(&p, (size_t)batch * ((wmax + 127) / 128 * 128)), s->xqb = (int8_t*)p;
     if (!rc) rc = s->alloc(&p, (size_t)batch * (wmax / 32) * 4), s->xdqb = (float*)p;
   }
   if (!rc && c.kind == SVL_MODEL_TTS && c.flow_dim > 0) {
