@@ -201,7 +201,7 @@ constexpr int kMaxBatch = 1024;
 constexpr int kMaxRingSlots = 12000;
 constexpr size_t kStaticLdsReserve = 8192;  // static LDS of the step kernels (barrier state, positions)  // KV ring slots per stream and layer (attention keeps a head's scores in LDS)
 constexpr int kGemmChunk = 4;    // Q8_0 blocks (128 bytes of K) per LDS stage of a GEMM unit
-constexpr int kGemmStages = 6;   // LDS stages of a GEMM unit (kGemmStages - 1 chunks in flight)
+constexpr int kGemmStages = 8;   // LDS stages of a GEMM unit
 // A GEMM stage: weights [kTileRows][128] | activations [kTileBatch][128] | weight scales
 // [kTileRows][4] f16 (two 4-byte direct loads per row) | activation scales [kTileBatch][4] f32.  The
 // operand rows come in groups of 8 (one wave's 1 KB direct load), each group kGemmGroupBytes
@@ -209,13 +209,13 @@ constexpr int kGemmStages = 6;   // LDS stages of a GEMM unit (kGemmStages - 1 c
 constexpr int kGemmGroupBytes = 1152;
 constexpr int kGemmStageBytes = kTileRows / 8 * kGemmGroupBytes + kTileBatch / 8 * kGemmGroupBytes + kTileRows * kGemmChunk * 4 + kTileBatch * kGemmChunk * 4;
 constexpr int kSyncChunks = 2;   // stages consumed between two row-wave barriers
-// s_waitcnt immediates (vmcnt only): the direct loads of the kGemmStages - 2 kSyncChunks chunks
-// after the ones about to be consumed may still be in flight (2 or 3 loads per wave and chunk), or
-// none
+// s_waitcnt immediates (vmcnt only) of the GEMM: at a barrier the chunks of the interval being
+// consumed and of the next one (read ahead) have landed, the kGemmStages - 3 kSyncChunks chunks after
+// them may still be in flight (1, 2 or 3 loads per wave and chunk), or none
 constexpr int vm_wait_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 2 * kSyncChunks));
-constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 2 * kSyncChunks));
-constexpr int kVmWait1 = vm_wait_imm(1 * (kGemmStages - 2 * kSyncChunks));
+constexpr int kVmWait2 = vm_wait_imm(2 * (kGemmStages - 3 * kSyncChunks));
+constexpr int kVmWait3 = vm_wait_imm(3 * (kGemmStages - 3 * kSyncChunks));
+constexpr int kVmWait1 = vm_wait_imm(1 * (kGemmStages - 3 * kSyncChunks));
 constexpr int kVmWait0 = vm_wait_imm(0);
 constexpr int kAttnChunkBytes = 16384;  // K or V rows per LDS stage of an attention unit
 constexpr int kAttnStages = 6;

@@ -1168,13 +1168,14 @@ __device__ __forceinline__ GemmStage gemm_stage(unsigned char* smem, int s) {
 __device__ __forceinline__ int swz(int j, int seg) {
   return j * 128 + (j >> 3) * 128 + ((seg ^ (j & 7)) << 4);
 }
-__device__ __forceinline__ uint32_t u4c(const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t u4c(const u32x4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(size_t)(const SVL_LDS void*)p; }
 
 // RowSync::sync for the GEMM loop, its LDS accesses written out so that the compiler does not
 // wait for the direct loads in flight before them (it cannot tell the counters from the stages).
-// Prior LDS reads of the wave have completed (gemm_read waits for them).
+// Prior LDS reads of the wave have completed (gemm_wait waits for them).
 __device__ __forceinline__ void gemm_sync(RowSync& rs) {
   if (rs.hw) {
     asm volatile("s_barrier" : : : "memory");
@@ -1209,8 +1210,8 @@ __device__ __forceinline__ void gemm_sync(RowSync& rs) {
 
 struct GemmOps {
   v_i8x8 a[4], b[4];  // A (weight) and B (activation) fragments of blocks 0-3
-  uint4 dw[2];        // weight scales as f16 pairs: rows 4g, 4g + 1, then rows 4g + 2, 4g + 3
-  float4 dx;          // activation scales of the lane's column, blocks 0-3
+  u32x4 dw[2];        // weight scales as f16 pairs: rows 4g, 4g + 1, then rows 4g + 2, 4g + 3
+  v4f dx;             // activation scales of the lane's column, blocks 0-3
 };
 
 struct GemmAddr {
@@ -1230,9 +1231,11 @@ __device__ __forceinline__ GemmAddr gemm_addr(const GemmStage& st, int ja, int j
   return p;
 }
 
-// One lane's operands of a chunk.  The reads and their wait are one statement: the compiler would
-// otherwise wait for every direct load still landing in the other stages before the first read.
-__device__ __forceinline__ void gemm_read(const GemmAddr& p, GemmOps& o) {
+// One lane's operands of a chunk, issued by gemm_issue and completed by gemm_wait, whose operands
+// are the same registers: in between the wave computes the chunk before.  Direct loads land in the
+// LDS stages meanwhile, which is why the reads are written out: the compiler would wait for every
+// direct load in flight before a read it issued itself.
+__device__ __forceinline__ void gemm_issue(const GemmAddr& p, GemmOps& o) {
   asm volatile(
       "ds_read_b64 %0, %11\n\t"
       "ds_read_b64 %1, %12\n\t"
@@ -1244,8 +1247,7 @@ __device__ __forceinline__ void gemm_read(const GemmAddr& p, GemmOps& o) {
       "ds_read_b64 %7, %18\n\t"
       "ds_read_b128 %8, %19\n\t"
       "ds_read_b128 %9, %19 offset:16\n\t"
-      "ds_read_b128 %10, %20\n\t"
-      "s_waitcnt lgkmcnt(0)"
+      "ds_read_b128 %10, %20"
       : "=&v"(o.a[0]), "=&v"(o.a[1]), "=&v"(o.a[2]), "=&v"(o.a[3]), "=&v"(o.b[0]), "=&v"(o.b[1]), "=&v"(o.b[2]),
         "=&v"(o.b[3]), "=&v"(o.dw[0]), "=&v"(o.dw[1]), "=&v"(o.dx)
       : "v"(p.a[0]), "v"(p.a[1]), "v"(p.a[2]), "v"(p.a[3]), "v"(p.b[0]), "v"(p.b[1]), "v"(p.b[2]), "v"(p.b[3]),
@@ -1253,41 +1255,13 @@ __device__ __forceinline__ void gemm_read(const GemmAddr& p, GemmOps& o) {
       : "memory");
 }
 
-// The operands of two chunks in adjacent stages (the second at kGemmStageBytes further), one wait
-// for both.
-static_assert(kGemmStageBytes == 15360, "the offsets below");
-__device__ __forceinline__ void gemm_read2(const GemmAddr& p, GemmOps& o, GemmOps& q) {
-  asm volatile(
-      "ds_read_b64 %0, %22\n\t"
-      "ds_read_b64 %1, %23\n\t"
-      "ds_read_b64 %2, %24\n\t"
-      "ds_read_b64 %3, %25\n\t"
-      "ds_read_b64 %4, %26\n\t"
-      "ds_read_b64 %5, %27\n\t"
-      "ds_read_b64 %6, %28\n\t"
-      "ds_read_b64 %7, %29\n\t"
-      "ds_read_b128 %8, %30\n\t"
-      "ds_read_b128 %9, %30 offset:16\n\t"
-      "ds_read_b128 %10, %31\n\t"
-      "ds_read_b64 %11, %22 offset:15360\n\t"
-      "ds_read_b64 %12, %23 offset:15360\n\t"
-      "ds_read_b64 %13, %24 offset:15360\n\t"
-      "ds_read_b64 %14, %25 offset:15360\n\t"
-      "ds_read_b64 %15, %26 offset:15360\n\t"
-      "ds_read_b64 %16, %27 offset:15360\n\t"
-      "ds_read_b64 %17, %28 offset:15360\n\t"
-      "ds_read_b64 %18, %29 offset:15360\n\t"
-      "ds_read_b128 %19, %30 offset:15360\n\t"
-      "ds_read_b128 %20, %30 offset:15376\n\t"
-      "ds_read_b128 %21, %31 offset:15360\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(o.a[0]), "=&v"(o.a[1]), "=&v"(o.a[2]), "=&v"(o.a[3]), "=&v"(o.b[0]), "=&v"(o.b[1]), "=&v"(o.b[2]),
-        "=&v"(o.b[3]), "=&v"(o.dw[0]), "=&v"(o.dw[1]), "=&v"(o.dx), "=&v"(q.a[0]), "=&v"(q.a[1]), "=&v"(q.a[2]),
-        "=&v"(q.a[3]), "=&v"(q.b[0]), "=&v"(q.b[1]), "=&v"(q.b[2]), "=&v"(q.b[3]), "=&v"(q.dw[0]), "=&v"(q.dw[1]),
-        "=&v"(q.dx)
-      : "v"(p.a[0]), "v"(p.a[1]), "v"(p.a[2]), "v"(p.a[3]), "v"(p.b[0]), "v"(p.b[1]), "v"(p.b[2]), "v"(p.b[3]),
-        "v"(p.w), "v"(p.x)
-      : "memory");
+// The registers are operands so that they stay where the reads land until the wait.
+__device__ __forceinline__ void gemm_wait(const GemmOps& o) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               :
+               : "v"(o.a[0]), "v"(o.a[1]), "v"(o.a[2]), "v"(o.a[3]), "v"(o.b[0]), "v"(o.b[1]), "v"(o.b[2]),
+                 "v"(o.b[3]), "v"(o.dw[0]), "v"(o.dw[1]), "v"(o.dx)
+               : "memory");
 }
 
 // The block products of a chunk (independent MFMAs).
@@ -1366,14 +1340,26 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
   };
   const int nch = (nb + kGemmChunk - 1) / kGemmChunk;
   constexpr int S = kSyncChunks, AHEAD = kGemmStages - kSyncChunks;  // chunks per sync, chunks issued ahead
-  static_assert(S == 2 && kGemmStages % 2 == 0, "an interval's two chunks sit in adjacent stages");
+  static_assert(S == 2 && kGemmStages >= 3 * S, "a barrier certifies the interval and the next one");
   __builtin_amdgcn_s_waitcnt(kVmWait0);  // no older stores interleave with the counted loads
   for (int c = 0; c < min(AHEAD, nch); ++c) issue(c);
   const int r0 = 16 * (wave / 4), c0 = 16 * (wave % 4);
   const int g = lane / 16, ja = r0 + lane % 16, jb = c0 + lane % 16;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Chunk k is computed from the registers its reads landed in while the reads of chunk k + 1 are in
+  // flight (even chunks in `ra`, odd ones in `rb`).  The barrier of interval c certifies the chunks
+  // up to c + 3, so the read-ahead of c + 2 may be issued before the next barrier.
+  GemmOps ra, rb;
+  auto chunk = [&](int k, GemmOps& cur, GemmOps& nxt) {
+    if (k >= nch) return;  // uniform
+    if (k + 1 < nch) gemm_issue(gemm_addr(gemm_stage(smem, (k + 1) % kGemmStages), ja, jb, g, r0), nxt);
+    v4i cc[kGemmChunk];
+    gemm_mfma(cur, cc);
+    gemm_terms(cur, cc, min(kGemmChunk, nb - kGemmChunk * k), acc);  // uniform block count
+    if (k + 1 < nch) gemm_wait(nxt);
+  };
   for (int c = 0; c < nch; c += S) {
-    // this wave's loads of chunks c .. c + S - 1 have landed (later chunks may still be in flight)
+    // this wave's loads of chunks .. c + 3 have landed (later chunks may still be in flight)
     if (c + AHEAD <= nch) {
       if (TR == 32 && wave >= 6) __builtin_amdgcn_s_waitcnt(kVmWait3);
       else if (TR == 16 && wave == 3) __builtin_amdgcn_s_waitcnt(kVmWait1);
@@ -1382,28 +1368,17 @@ __device__ __forceinline__ void qgemm_unit(const GemvArgs& a, int unit, const in
     } else {
       __builtin_amdgcn_s_waitcnt(kVmWait0);
     }
-    gemm_sync(rs);  // chunks c .. are in LDS everywhere; every wave is done with the chunks before
+    gemm_sync(rs);  // chunks .. c + 3 are in LDS everywhere; every wave is done reading the chunks before c
 #pragma unroll
     for (int u = 0; u < S; ++u)
       if (c + AHEAD + u < nch) issue(c + AHEAD + u);
     if (wave < TR / 4) {  // uniform
-      const GemmAddr pa = gemm_addr(gemm_stage(smem, c % kGemmStages), ja, jb, g, r0);
-      const int nk0 = min(kGemmChunk, nb - kGemmChunk * c);  // uniform: 4 except in a last partial chunk
-      if (c + 1 < nch) {  // both chunks of the interval, in adjacent stages (c is even)
-        GemmOps o, q;
-        gemm_read2(pa, o, q);
-        v4i cc[kGemmChunk], cq[kGemmChunk];
-        gemm_mfma(o, cc);
-        gemm_mfma(q, cq);
-        gemm_terms(o, cc, nk0, acc);
-        gemm_terms(q, cq, min(kGemmChunk, nb - kGemmChunk * (c + 1)), acc);
-      } else {
-        GemmOps o;
-        gemm_read(pa, o);
-        v4i cc[kGemmChunk];
-        gemm_mfma(o, cc);
-        gemm_terms(o, cc, nk0, acc);
+      if (c == 0) {
+        gemm_issue(gemm_addr(gemm_stage(smem, 0), ja, jb, g, r0), ra);
+        gemm_wait(ra);
       }
+      chunk(c, ra, rb);
+      chunk(c + 1, rb, ra);
     }
   }
   if (wave < TR / 4) {
@@ -1641,7 +1616,7 @@ __device__ __forceinline__ bool is_chained_dense(int fmt) { return fmt == FMT_F3
 // max, e_j = exp(w_j - max), the sum of e_j in key order, then out = sum over keys in order of
 // mul_add(e_j / sum, v_j, out), thread d owning dim d.  K and then V rows stream through
 // kAttnStages LDS stages of kAttnChunkBytes by direct loads issued kAttnStages - 1 chunks ahead;
-// the LDS reads of the stages are written out (see gemm_read).
+// the LDS reads of the stages are written out (see gemm_issue).
 
 __device__ __forceinline__ int visible_keys(const AttnArgs& a, int p) {
   return a.window > 0 ? min(p + 1, a.window) : p + 1;
