@@ -58,7 +58,8 @@ def traffic_file(name):
 
 def read_traffic(name):
     """The committed counter summary of a workload (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the
-    copy-kernel calibration): {"hbm_bytes_per_step", "dominant_hbm_bytes_per_launch", "steps"}, or {}."""
+    copy-kernel calibration): {"hbm_bytes_per_step", "steps", "per_kernel": {kernel group: HBM bytes
+    per launch}} (lines `hbm_bytes_per_launch[<kernel group>]: N`), or {}."""
     path = traffic_file(name)
     if not os.path.exists(path):
         return {}
@@ -67,12 +68,18 @@ def read_traffic(name):
         if ":" in line and not line.lstrip().startswith("#"):
             k, v = line.split(":", 1)
             kv[k.strip()] = v.strip()
-    out = {}
-    for k in ("hbm_bytes_per_step", "dominant_hbm_bytes_per_launch", "steps"):
+    out = {"per_kernel": {}}
+    for k in ("hbm_bytes_per_step", "steps"):
         try:
             out[k] = int(float(kv[k]))
         except (KeyError, ValueError):
             pass
+    for k, v in kv.items():
+        if k.startswith("hbm_bytes_per_launch[") and k.endswith("]"):
+            try:
+                out["per_kernel"][k[len("hbm_bytes_per_launch["):-1]] = int(float(v))
+            except ValueError:
+                pass
     return out
 
 
@@ -354,7 +361,7 @@ def bench_b64(args, shape, dtype, tensors, model, steps, warmup):
            "kernel_shares": {k: {"share": v["share_of_replayed_step"], "avg_launch_us": v["avg_launch_us"],
                                  "GBps": round(v["achieved_gbs"], 1)} for k, v in shares.items()}}
     tr = read_traffic("stt1b_q8_b64")
-    out["roofline"]["traffic"] = tr.get("dominant_hbm_bytes_per_launch")
+    out["roofline"]["traffic"] = tr.get("per_kernel", {}).get(dom["kernel"])
     out["step_roofline"]["traffic"] = tr.get("hbm_bytes_per_step")
     out["step_roofline"]["traffic_counter_steps"] = tr.get("steps")
     if not args.no_cpu_baseline:
@@ -447,7 +454,7 @@ def b1_line(args, shape, dtype, tensors, model, steps, warmup, name, traffic_nam
     dom, shares = dominant_roofline(res["table"], 1)
     tr = read_traffic(traffic_name)
     traffic, tsteps = tr.get("hbm_bytes_per_step"), tr.get("steps")
-    line["roofline"] = roofline_obj(dom["achieved_gbs"], traffic=tr.get("dominant_hbm_bytes_per_launch"),
+    line["roofline"] = roofline_obj(dom["achieved_gbs"], traffic=tr.get("per_kernel", {}).get(dom["kernel"]),
                                     traffic_counter_steps=tsteps, kernel=dom["kernel"],
                                     launches_per_step=dom["launches_per_step"],
                                     algorithmic_bytes_per_launch=dom["algorithmic_bytes_per_launch"],
