@@ -215,24 +215,28 @@ def kernel_roofline(table, pick, name):
             "share_of_replayed_step": None}
 
 
+# The kernel groups a step's replayed phases are sorted into (svl_bench_phase's info: kind, weight
+# format, rows, input width); the names key the committed traffic files' per-kernel entries.
+KERNEL_GROUPS = {
+    "gemv_phase_kernel<1u,4> (Q8_0 GEMV, input rows <= 2048)": lambda i: i[0] == PH_GEMV and i[1] == 3 and i[3] <= 2048,
+    "gemv_phase_kernel<1u,16> (Q8_0 GEMV, input rows > 4096)": lambda i: i[0] == PH_GEMV and i[1] == 3 and i[3] > 4096,
+    "gemv_phase_kernel<2u,*> (Q4K GEMV)": lambda i: i[0] == PH_GEMV and i[1] == 4,
+    "gemv_phase_kernel<4u,*> (dense GEMV)": lambda i: i[0] == PH_GEMV and i[1] in (0, 1, 5, 6),
+    "attn_phase_kernel (attention)": lambda i: i[0] == PH_ATTN,
+    "batch_phase_kernel (MFMA int8 GEMM)": lambda i: i[0] == PH_QGEMM,
+    "batch_phase_kernel (activation quantization)": lambda i: i[0] == PH_QUANT,
+    "phase_kernel (embedding, argmax, other)": lambda i: i[0] not in (PH_GEMV, PH_ATTN, PH_QGEMM, PH_QUANT),
+}
+
+
 def dominant_roofline(table, B):
-    """Roofline of the kernel instance with the largest share of the step: the Q8_0 GEMV over
-    rows of 2048 (gemv_phase_kernel<1u,4>) at B = 1, the MFMA GEMM (batch_phase_kernel) at B = 64.
-    Also the shares of every kind."""
+    """Roofline of the kernel group with the largest share of the replayed step (the Q8_0 GEMV
+    over rows of 2048, gemv_phase_kernel<1u,4>, at B = 1; the attention or the MFMA GEMM at
+    B = 64, within a percent of each other).  Also the shares of every group."""
     total = sum(us for _, _, us, _ in table)
-    groups = {
-        "gemv_phase_kernel<1u,4> (Q8_0 GEMV, input rows <= 2048)": lambda i: i[0] == PH_GEMV and i[1] == 3 and i[3] <= 2048,
-        "gemv_phase_kernel<1u,16> (Q8_0 GEMV, input rows > 4096)": lambda i: i[0] == PH_GEMV and i[1] == 3 and i[3] > 4096,
-        "gemv_phase_kernel<2u,*> (Q4K GEMV)": lambda i: i[0] == PH_GEMV and i[1] == 4,
-        "gemv_phase_kernel<4u,*> (dense GEMV)": lambda i: i[0] == PH_GEMV and i[1] in (0, 1, 5, 6),
-        "attn_phase_kernel (attention)": lambda i: i[0] == PH_ATTN,
-        "batch_phase_kernel (MFMA int8 GEMM)": lambda i: i[0] == PH_QGEMM,
-        "batch_phase_kernel (activation quantization)": lambda i: i[0] == PH_QUANT,
-        "phase_kernel (embedding, argmax, other)": lambda i: i[0] not in (PH_GEMV, PH_ATTN, PH_QGEMM, PH_QUANT),
-    }
     shares = {}
     best = None
-    for name, pick in groups.items():
+    for name, pick in KERNEL_GROUPS.items():
         r = kernel_roofline(table, pick, name)
         if r is None:
             continue
