@@ -22,7 +22,9 @@ Default run (--workload stt1b-q8): ONE JSON line whose `value` is the B = 1 rate
     included) the same way;
   * `cpu_baseline`: the oracle (this repository's C restatement of the reference's CPU path) on
     4 host threads (the reference's default) over a bounded sample, with its tokens compared
-    to the GPU's, the CPU model and an all-cores figure.
+    to the GPU's, the CPU model and an all-cores figure;
+  * `copy_ceiling`: libsvl's copy kernel over 1 GiB (read and written), the achievable HBM rate
+    beside the vendor peak; each roofline also gives `frac_of_copy_ceiling`.
 Other workloads (--workload): stt1b-bf16-b1, stt2.6b-q4k-b1, tts-f32-b1 (one line each).
 
 `--calibrate-copy BYTES` runs libsvl's plain copy kernel over BYTES three times (the known-size
@@ -147,6 +149,30 @@ def calibrate_copy(nbytes):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "dispatches": 3,
                       "ms": [round(t, 4) for t in times],
                       "GBps_read_plus_write": round(2 * nbytes / (min(times) / 1e3) / 1e9, 1)}), flush=True)
+
+
+def copy_ceiling(nbytes=1 << 30):
+    """The achievable HBM rate of a plain kernel: libsvl's copy kernel over `nbytes` (read and
+    written), best of three after one warm-up, HIP events."""
+    import svl
+    from svl import hip
+
+    L = svl.load_library()
+    src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    e0, e1 = hip.Event(), hip.Event()
+    best = None
+    for i in range(4):
+        e0.record(None)
+        svl._check(L.svl_bench_copy(0, src.address, dst.address, nbytes, None))
+        e1.record(None)
+        hip.synchronize()
+        if i:
+            t = e0.elapsed_ms(e1)
+            best = t if best is None else min(best, t)
+    del src, dst
+    gbs = 2 * nbytes / (best / 1e3) / 1e9
+    return {"GBps": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_read": nbytes,
+            "bytes_written": nbytes, "kernel": "libsvl copy kernel (16-byte loads and stores)"}
 
 
 def timed_launch(model, st, n, d_audio, d_out, warmup):
@@ -581,6 +607,11 @@ def main():
         tensors, model = stt_model(shape, dtype)
         name = f"{shape.name} {dtype} greedy decode, batch 1"
         line = b1_line(args, shape, dtype, tensors, model, steps, warmup, name, wl.replace("-", "_"))
+    # the achievable ceiling beside the vendor peak: the dominant kernel's rate as a fraction of it
+    line["copy_ceiling"] = copy_ceiling()
+    for r in [line.get("roofline")] + ([line["b64"].get("roofline")] if "b64" in line else []):
+        if r:
+            r["frac_of_copy_ceiling"] = round(r["achieved"] / line["copy_ceiling"]["GBps"], 4)
     print(json.dumps(line), flush=True)
 
 
