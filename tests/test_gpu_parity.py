@@ -275,9 +275,13 @@ def test_lockstep_batch_equals_independent_streams():
 
 # text vocabulary 8000: text_linear runs in 32-row GEMM tiles, the other linears in 16-row tiles
 S1_SMALL_VOCAB = W.stt_shape("stt-small-vocab", 256, 2, 4, 4.125, 24, card=64, n_q=4, text_card=8000)
+# d_model 320: 10 blocks, three 128-byte chunks, the last one half full (an odd chunk count, fewer
+# chunks than the loads issued ahead); FF hidden 672: 21 blocks, so the FF-out linear of the batch
+# runs on the GEMV path (the GEMM's weight scales travel in pairs)
+S1_ODD_CHUNKS = W.stt_shape("stt-odd-chunks", 320, 2, 5, 3.15, 24, card=64, n_q=4, text_card=100)
 
 
-@pytest.mark.parametrize("shape", [W.S1_SMALL, S1_SMALL_VOCAB], ids=["small", "vocab8000"])
+@pytest.mark.parametrize("shape", [W.S1_SMALL, S1_SMALL_VOCAB, S1_ODD_CHUNKS], ids=["small", "vocab8000", "odd-chunks"])
 def test_mfma_batch_equals_independent_streams(shape):
     """A lockstep batch large enough for the MFMA GEMM path (20 streams at different positions):
     logits and tokens bit-identical to each stream stepped alone through the GEMV path."""
