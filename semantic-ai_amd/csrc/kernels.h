@@ -198,8 +198,8 @@ constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8
 constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit (or 16)
 constexpr int kTileBatch = 64;   // batch rows of a GEMM unit
 constexpr int kMaxBatch = 1024;
-constexpr int kMaxRingSlots = 12000;
-constexpr size_t kStaticLdsReserve = 8192;  // static LDS of the step kernels (barrier state, positions)  // KV ring slots per stream and layer (attention keeps a head's scores in LDS)
+constexpr int kMaxRingSlots = 12000;  // KV ring slots per stream and layer (attention keeps a head's scores in LDS)
+constexpr size_t kStaticLdsReserve = 8192;  // static LDS of the step kernels (barrier state, positions)
 constexpr int kGemmChunk = 4;    // Q8_0 blocks (128 bytes of K) per LDS stage of a GEMM unit
 constexpr int kGemmStages = 8;   // LDS stages of a GEMM unit
 // A GEMM stage: weights [kTileRows][128] | activations [kTileBatch][128] | weight scales
@@ -207,7 +207,10 @@ constexpr int kGemmStages = 8;   // LDS stages of a GEMM unit
 // operand rows come in groups of 8 (one wave's 1 KB direct load), each group kGemmGroupBytes
 // apart: the 128 bytes between groups put rows j and j + 8 of an MFMA operand in different banks.
 constexpr int kGemmGroupBytes = 1152;
-constexpr int kGemmStageBytes = kTileRows / 8 * kGemmGroupBytes + kTileBatch / 8 * kGemmGroupBytes + kTileRows * kGemmChunk * 4 + kTileBatch * kGemmChunk * 4;
+constexpr int kGemmStageBytes = kTileRows / 8 * kGemmGroupBytes + kTileBatch / 8 * kGemmGroupBytes + kTileRows * kGemmChunk * 2 +
+                                kTileBatch * kGemmChunk * 4;
+static_assert(kGemmStageBytes % 16 == 0 && (kTileRows / 8 * kGemmGroupBytes + kTileBatch / 8 * kGemmGroupBytes + kTileRows * kGemmChunk * 2) % 16 == 0,
+              "16-byte aligned stages and activation scales");
 constexpr int kSyncChunks = 2;   // stages consumed between two row-wave barriers
 // s_waitcnt immediates (vmcnt only) of the GEMM: at a barrier the chunks of the interval being
 // consumed and of the next one (read ahead) have landed, the kGemmStages - 3 kSyncChunks chunks after

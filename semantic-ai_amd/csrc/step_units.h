@@ -1160,7 +1160,7 @@ __device__ __forceinline__ GemmStage gemm_stage(unsigned char* smem, int s) {
   g.w = base;
   g.x = base + kTileRows / 8 * kGemmGroupBytes;
   g.dw = (uint32_t*)(g.x + kTileBatch / 8 * kGemmGroupBytes);
-  g.dx = (float*)(g.dw + kTileRows * kGemmChunk);
+  g.dx = (float*)(g.dw + kTileRows * kGemmChunk / 2);
   return g;
 }
 
