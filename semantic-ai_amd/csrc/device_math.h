@@ -123,6 +123,16 @@ __device__ __forceinline__ uint32_t half_max_bits(uint32_t v) {
   return v;
 }
 
+// The sum of an int over each row of 16 lanes, in the row's last lane (DPP row shifts, in-row
+// prefix sums; integer adds, so the order is immaterial).  Every lane of the wave must be active.
+__device__ __forceinline__ int row16_isum_last(int s) {
+  s += __builtin_amdgcn_update_dpp(0, s, 0x111, 0xf, 0xf, false);  // row_shr:1
+  s += __builtin_amdgcn_update_dpp(0, s, 0x112, 0xf, 0xf, false);  // row_shr:2
+  s += __builtin_amdgcn_update_dpp(0, s, 0x114, 0xf, 0xf, false);  // row_shr:4
+  s += __builtin_amdgcn_update_dpp(0, s, 0x118, 0xf, 0xf, false);  // row_shr:8
+  return s;
+}
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its
 // outstanding global loads (which __syncthreads would wait for).
 __device__ __forceinline__ void lds_barrier() {

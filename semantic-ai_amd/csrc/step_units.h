@@ -849,10 +849,11 @@ __host__ __device__ constexpr int q4k_lane_pos(int e) { return ((e & 7) << 2) | 
 // maximum (in `red`, by item parity) and synchronizes the row waves; the second part writes the
 // quants once the weight waves are done with the previous item's.
 template <int KP>
-__device__ __forceinline__ void q8k_wave_maxima(const float (&v)[KP], float* red, RowSync& rs) {
+__device__ __forceinline__ void q8k_wave_maxima(const float (&v)[KP], int K, float* red, RowSync& rs) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
 #pragma unroll
   for (int u = 0; u < KP; ++u) {
+    if (u * kRowThreads >= K) break;  // uniform: slots past the row
     const uint32_t a = __float_as_uint(fabsf(v[u]));
     const uint32_t hm = half_max_bits(a);
     const uint32_t m = max((uint32_t)__builtin_amdgcn_readlane((int)hm, 0), (uint32_t)__builtin_amdgcn_readlane((int)hm, 32));
@@ -872,6 +873,7 @@ __device__ __forceinline__ void q8k_write(const float (&v)[KP], int K, const flo
   const int half = threadIdx.x / 256;
 #pragma unroll
   for (int u = 0; u < KP; ++u) {
+    if (u * kRowThreads >= K) break;  // uniform: slots past the row
     uint32_t best = 0;
     float mx = 0.0f;
 #pragma unroll
@@ -885,14 +887,10 @@ __device__ __forceinline__ void q8k_write(const float (&v)[KP], int K, const flo
     const float iscale = best != 0 ? -128.0f / mx : 0.0f;
     const int i = threadIdx.x + u * kRowThreads;
     const int q = best != 0 ? sat_i8(fminf(roundf(iscale * v[u]), 127.0f)) : 0;
-    int s = q;
-    s += __shfl_xor(s, 8, 16);
-    s += __shfl_xor(s, 4, 16);
-    s += __shfl_xor(s, 2, 16);
-    s += __shfl_xor(s, 1, 16);
+    const int s = row16_isum_last(q);  // elements i & ~15 .. (i & ~15) + 15 sit in one row of lanes
     if (i < K) {
       xq[(i & ~31) | q4k_lane_pos(i & 31)] = (int8_t)q;
-      if ((i & 15) == 0) bs[i >> 4] = s;
+      if ((i & 15) == 15) bs[i >> 4] = s;
       if ((i & 255) == 0) xd[i >> 8] = best != 0 ? 1.0f / iscale : 0.0f;
     }
   }
@@ -935,7 +933,7 @@ __device__ __forceinline__ void gemv_q4k_rows(const GemvArgs& a, int unit, const
     if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
   }
   float* red = l.red + (item & 1) * (q4k_red_words(g.K) / 2);
-  q8k_wave_maxima(v, red, rs);
+  q8k_wave_maxima(v, g.K, red, rs);
   // the weight waves have read the previous item's quantized row
   lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
   q8k_write(v, g.K, red, l.xq, l.xd, l.bs);
