@@ -194,6 +194,7 @@ constexpr int kWBlocks = 6;                              // Q8_0 blocks per weig
 constexpr int kDenseBatch = 16;                          // 16-byte loads in flight per dense weight-wave thread
 constexpr int kQ4Blocks = 2;                             // Q4K super-blocks per weight-wave thread and unit
 constexpr int kQ4Terms = 9;   // f32 terms per Q4K super-block and row: 8 lane sums and the min term
+constexpr int kQ4TermStride = 12;  // LDS floats per (row, super-block): the 9 terms in three 16-byte words
 constexpr int kBatchMfma = 16;   // lockstep batches from this size run their Q8_0 linears as MFMA GEMMs
 constexpr int kTileRows = 32;    // output rows (16 gate/value pairs) of a GEMM unit (or 16)
 constexpr int kTileBatch = 64;   // batch rows of a GEMM unit

@@ -809,7 +809,8 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
 __host__ __device__ constexpr int q4k_red_words(int K) { return 2 * 2 * kRowWaves * row_slots(K); }
 
 // LDS of a Q4K unit: xs [norm_scratch_floats(K)] f32 | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
-// bs [nb][16] i32 | red [q4k_red_words(K)] | T [nb][9][ts] f32 | Y [2 ipw] f32.
+// bs [nb][16] i32 | red [q4k_red_words(K)] | T [nb][ts][kQ4TermStride] f32 (16-byte aligned) | Y [2 ipw] f32.
+// A (row, super-block)'s nine terms are contiguous, so that they move as three 16-byte words.
 struct Q4Lds {
   float* xs;
   int8_t* xq;
@@ -827,8 +828,8 @@ __device__ __forceinline__ Q4Lds q4_lds(unsigned char* smem, int K, int nb, int 
   l.xd = (float*)(l.xq + K);
   l.bs = (int*)(l.xd + ((nb + 3) & ~3));
   l.red = (float*)(l.bs + nb * 16);
-  l.T = l.red + q4k_red_words(K);
-  l.Y = l.T + nb * kQ4Terms * ts;
+  l.T = (float*)(((size_t)(l.red + q4k_red_words(K)) + 15) & ~(size_t)15);
+  l.Y = l.T + nb * ts * kQ4TermStride;
   return l;
 }
 
@@ -899,13 +900,13 @@ __device__ __forceinline__ void q8k_write(const float (&v)[KP], int K, const flo
 // acc over the nine term rows of row r: lane sums l < 8 in super-block order, the min term
 // subtracted in super-block order, then min_sum + (((s_0 + s_1) + ...) + s_7).
 __device__ __forceinline__ float q4k_row_sum(const float* T, int ts, int r, int nb) {
-  const float* t = T + r;
+  const float* t = T + (size_t)r * kQ4TermStride;
   float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   float mins = 0.0f;
   for (int blk = 0; blk < nb; ++blk) {
-    float v[kQ4Terms];
-#pragma unroll
-    for (int c = 0; c < kQ4Terms; ++c) v[c] = t[(blk * kQ4Terms + c) * ts];
+    const float* tb = t + (size_t)blk * ts * kQ4TermStride;
+    const float4 a = *(const float4*)tb, b = *(const float4*)(tb + 4);
+    const float v[kQ4Terms] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, tb[8]};
 #pragma unroll
     for (int c = 0; c < 8; ++c) s[c] = s[c] + v[c];
     mins = mins - v[8];
@@ -1056,10 +1057,10 @@ __device__ __forceinline__ void w_terms_q4k(const WItemQ4& it, unsigned char* sm
       const uint32_t hd = (uint32_t)it.h[k].x;
       const float d = f16_to_f32((uint16_t)(hd & 0xFFFF)) * xd;
       const float dm = f16_to_f32((uint16_t)(hd >> 16)) * xd;
-      float* T = l.T + blk * kQ4Terms * it.g.ts + r;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) T[c * it.g.ts] = d * (float)aux[c];
-      T[8 * it.g.ts] = dm * (float)sumi;
+      float* T = l.T + ((size_t)blk * it.g.ts + r) * kQ4TermStride;
+      *(float4*)T = float4{d * (float)aux[0], d * (float)aux[1], d * (float)aux[2], d * (float)aux[3]};
+      *(float4*)(T + 4) = float4{d * (float)aux[4], d * (float)aux[5], d * (float)aux[6], d * (float)aux[7]};
+      T[8] = dm * (float)sumi;
     }
     r += dr;
     blk += db;
