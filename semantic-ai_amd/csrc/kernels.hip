@@ -518,7 +518,7 @@ size_t phase_smem(const Phase& ph) {
       }
       if (g.L.fmt == FMT_Q4K) {
         const int nb = K / 256, nb4 = (nb + 3) & ~3, ts = 2 * g.ipw + 1;
-        return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 + (size_t)q4k_red_words(K) * 4 +
+        return (size_t)norm_scratch_floats(K) * 4 + K + (size_t)nb4 * 4 + (size_t)nb * 16 * 4 +
                (size_t)nb * ts * kQ4TermStride * 4 + 16 + (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C)

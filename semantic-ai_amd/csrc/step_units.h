@@ -804,19 +804,14 @@ __device__ __forceinline__ void w_terms(const WItem& it, unsigned char* smem) {
 // by super-block, and ends with min_sum + (((s_0 + s_1) + ...) + s_7).  The weight waves write
 // the nine f32 terms of every (row, super-block) into LDS; the row waves add them in order.
 
-// LDS words of the Q8K quantizer's per-wave maxima: two item parities x (max |x| bits, value) x
-// 8 row waves x row slots.
-__host__ __device__ constexpr int q4k_red_words(int K) { return 2 * 2 * kRowWaves * row_slots(K); }
-
 // LDS of a Q4K unit: xs [norm_scratch_floats(K)] f32 | xq [K] int8 (lane-grouped) | xd [nb, padded to 4] f32 |
-// bs [nb][16] i32 | red [q4k_red_words(K)] | T [nb][ts][kQ4TermStride] f32 (16-byte aligned) | Y [2 ipw] f32.
+// bs [nb][16] i32 | T [nb][ts][kQ4TermStride] f32 (16-byte aligned) | Y [2 ipw] f32.
 // A (row, super-block)'s nine terms are contiguous, so that they move as three 16-byte words.
 struct Q4Lds {
   float* xs;
   int8_t* xq;
   float* xd;
   int* bs;
-  float* red;
   float* T;
   float* Y;
 };
@@ -827,8 +822,7 @@ __device__ __forceinline__ Q4Lds q4_lds(unsigned char* smem, int K, int nb, int 
   l.xq = (int8_t*)(l.xs + norm_scratch_floats(K));
   l.xd = (float*)(l.xq + K);
   l.bs = (int*)(l.xd + ((nb + 3) & ~3));
-  l.red = (float*)(l.bs + nb * 16);
-  l.T = (float*)(((size_t)(l.red + q4k_red_words(K)) + 15) & ~(size_t)15);
+  l.T = (float*)(((size_t)(l.bs + nb * 16) + 15) & ~(size_t)15);
   l.Y = l.T + nb * ts * kQ4TermStride;
   return l;
 }
@@ -843,57 +837,41 @@ __device__ __forceinline__ Q8Geom q4_geom(int K, int items, int ipw, int parts, 
 // Byte offset of element e (< 32) of a 32-value group in the lane-grouped order.
 __host__ __device__ constexpr int q4k_lane_pos(int e) { return ((e & 7) << 2) | (e >> 3); }
 
-// BlockQ8K::from_float of a register row (elements t + 512 u): per 256 values, mx = the value of
-// largest magnitude (the first one on ties), iscale = -128 / mx, q = min(round(iscale * x), 127),
-// d = 1 / iscale (all zero when the block is); bs = sums of 16 consecutive quants.  A block is
-// the 4 waves of one half of the row threads in one slot.  The first part publishes each wave's
-// maximum (in `red`, by item parity) and synchronizes the row waves; the second part writes the
-// quants once the weight waves are done with the previous item's.
-template <int KP>
-__device__ __forceinline__ void q8k_wave_maxima(const float (&v)[KP], int K, float* red, RowSync& rs) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+// BlockQ8K::from_float of the chunked row (chunks c = t + 512 u of 4 elements): per 256 values,
+// mx = the value of largest magnitude (the first one on ties), iscale = -128 / mx,
+// q = min(round(iscale * x), 127), d = 1 / iscale (all zero when the block is); bs = sums of 16
+// consecutive quants.  A super-block is the 64 chunks of one wave and slot, so its maximum and
+// first index stay within the wave (no barrier); a 16-sum is the chunks of 4 lanes.
+template <int KU>
+__device__ __forceinline__ void q8k_quantize4(const v4f (&v)[KU], int K, int8_t* xq, float* xd, int* bs) {
+  const int nc = K / 4, lane = threadIdx.x % kWave;
 #pragma unroll
-  for (int u = 0; u < KP; ++u) {
-    if (u * kRowThreads >= K) break;  // uniform: slots past the row
-    const uint32_t a = __float_as_uint(fabsf(v[u]));
-    const uint32_t hm = half_max_bits(a);
-    const uint32_t m = max((uint32_t)__builtin_amdgcn_readlane((int)hm, 0), (uint32_t)__builtin_amdgcn_readlane((int)hm, 32));
-    const unsigned long long hit = __ballot(a == m);
-    const int first = (int)__builtin_ctzll(hit);
-    const float val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[u]), first));
-    if (lane == 0) {
-      red[(u * kRowWaves + wave) * 2] = __uint_as_float(m);
-      red[(u * kRowWaves + wave) * 2 + 1] = val;
-    }
-  }
-  rs.sync();
-}
-
-template <int KP>
-__device__ __forceinline__ void q8k_write(const float (&v)[KP], int K, const float* red, int8_t* xq, float* xd, int* bs) {
-  const int half = threadIdx.x / 256;
-#pragma unroll
-  for (int u = 0; u < KP; ++u) {
-    if (u * kRowThreads >= K) break;  // uniform: slots past the row
-    uint32_t best = 0;
-    float mx = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int o = (u * kRowWaves + 4 * half + w) * 2;
-      const uint32_t m = __float_as_uint(red[o]);
-      const float val = red[o + 1];
-      mx = m > best ? val : mx;
-      best = m > best ? m : best;
-    }
+  for (int u = 0; u < KU; ++u) {
+    const int c = threadIdx.x + u * kRowThreads;
+    if (c - lane >= nc) break;  // uniform per wave (nc is a multiple of 64)
+    const uint32_t a0 = __float_as_uint(fabsf(v[u].x)), a1 = __float_as_uint(fabsf(v[u].y));
+    const uint32_t a2 = __float_as_uint(fabsf(v[u].z)), a3 = __float_as_uint(fabsf(v[u].w));
+    const uint32_t lm = max(max(a0, a1), max(a2, a3));
+    const uint32_t hm = half_max_bits(lm);
+    const uint32_t best = max((uint32_t)__builtin_amdgcn_readlane((int)hm, 0), (uint32_t)__builtin_amdgcn_readlane((int)hm, 32));
+    // the first element of the largest magnitude: the first lane holding one, its first element
+    const int first = (int)__builtin_ctzll(__ballot(lm == best));
+    const float own = a0 == best ? v[u].x : (a1 == best ? v[u].y : (a2 == best ? v[u].z : v[u].w));
+    const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(own), first));
     const float iscale = best != 0 ? -128.0f / mx : 0.0f;
-    const int i = threadIdx.x + u * kRowThreads;
-    const int q = best != 0 ? sat_i8(fminf(roundf(iscale * v[u]), 127.0f)) : 0;
-    const int s = row16_isum_last(q);  // elements i & ~15 .. (i & ~15) + 15 sit in one row of lanes
-    if (i < K) {
+    const float xs[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+    int qs = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int q = best != 0 ? sat_i8(fminf(roundf(iscale * xs[k]), 127.0f)) : 0;
+      qs += q;
+      const int i = 4 * c + k;
       xq[(i & ~31) | q4k_lane_pos(i & 31)] = (int8_t)q;
-      if ((i & 15) == 15) bs[i >> 4] = s;
-      if ((i & 255) == 0) xd[i >> 8] = best != 0 ? 1.0f / iscale : 0.0f;
     }
+    qs += __builtin_amdgcn_update_dpp(0, qs, 0xB1, 0xf, 0xf, false);  // quad_perm [1, 0, 3, 2]
+    qs += __builtin_amdgcn_update_dpp(0, qs, 0x4E, 0xf, 0xf, false);  // quad_perm [2, 3, 0, 1]
+    if ((c & 3) == 0) bs[c >> 2] = qs;
+    if (lane == 0) xd[c >> 6] = best != 0 ? 1.0f / iscale : 0.0f;
   }
 }
 
@@ -923,21 +901,20 @@ __device__ __forceinline__ void gemv_q4k_rows(const GemvArgs& a, int unit, const
                                               RowSync& rs, unsigned item) {
   const Q8Geom g = q4_geom(a.L.in, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
   const Q4Lds l = q4_lds(smem, g.K, g.nb, g.ts);
-  constexpr bool kNorm = KP <= 8;
-  NormW<kNorm ? KP : 1> nwt;
-  if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, g.K, nwt);
-  float v[KP];
-  load_row(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
+  constexpr int KU = chunk_slots(KP * kRowThreads);
+  constexpr bool kNorm = KP <= 8;  // rows wider than 4096 are never normalized (d_model <= 4096)
+  NormW4<kNorm ? KU : 1> nwt;
+  if (kNorm && a.norm != NORM_NONE) load_norm_weights4(a.norm, a.nw, a.nb, g.K, nwt);
+  v4f v[KU];
+  load_row4(a.x + (size_t)g.b * a.x_stride, g.K, v, &rs.ws->r_issued);
   const int p = (a.epi == EPI_QKV_ROPE || a.advance_pos ? spos[g.b] : 0);
   const EpiIn in = gemv_epi_prefetch(a, g.b, g.i0 + min((int)threadIdx.x, g.ni - 1), p);
   if constexpr (kNorm) {
-    if (a.norm != NORM_NONE) norm_regs(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
+    if (a.norm != NORM_NONE) norm_row4(v, g.K, a.norm, nwt, a.eps, l.xs, rs);
   }
-  float* red = l.red + (item & 1) * (q4k_red_words(g.K) / 2);
-  q8k_wave_maxima(v, g.K, red, rs);
   // the weight waves have read the previous item's quantized row
   lds_wait(&rs.ws->t_parts, item * kWeightWaves, &rs.ws->stop);
-  q8k_write(v, g.K, red, l.xq, l.xd, l.bs);
+  q8k_quantize4(v, g.K, l.xq, l.xd, l.bs);
   lds_signal(&rs.ws->xq_parts);
   const bool many = g.NR > kWave;  // uniform
   if (many || threadIdx.x < kWave) {
