@@ -538,6 +538,40 @@ def bench_tts(args, steps, warmup):
                      "synthetic (seeded N(0, 0.02) weights, N(0, 1) latents, seeded prefilled K/V)", config)
     line["roofline"] = roofline_obj(achieved, kernel="the step's phase kernels, one call per step (host loop)",
                                     algorithmic_bytes_per_step=int(bytes_total / steps))
+    # the whole FlowLm step on the device (backbone, out_eos, one flow-head decode step): frames
+    # enqueued with device pointers, each fed the previous frame's latent and the sampler's
+    # pre-drawn noise, no host round trip; HIP events on the state's stream
+    ld = shape.latent_dim
+    d_noise = hip.DeviceBuffer.from_array(np.ascontiguousarray(W.latents(shape, steps, seed=5)))
+    d_lat = [hip.DeviceBuffer(ld * 4), hip.DeviceBuffer(ld * 4)]
+    d_eos = hip.DeviceBuffer(steps * 4)
+
+    def frames(stv, n):
+        for f in range(n):
+            model.tts_step_async(0 if f == 0 else d_lat[(f - 1) % 2].address, d_noise.address + f * ld * 4, 1,
+                                 d_lat[f % 2].address, d_eos.address + f * 4, stv)
+
+    wst = model.state_from_layer_caches(ks, vs, capacity=cap)
+    frames(wst, max(1, min(warmup, steps)))
+    wst.synchronize()
+    sd = model.state_from_layer_caches(ks, vs, capacity=cap)
+    sd.synchronize()
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(sd.stream)
+    frames(sd, steps)
+    e1.record(sd.stream)
+    sd.synchronize()
+    dms = e0.elapsed_ms(e1)
+    flow_bytes = sum(int(np.prod(sh)) * 4 for name, sh, _ in W.tensor_names(shape) if name.startswith("flow_net."))
+    dev_bytes = bytes_total + steps * flow_bytes
+    line["device_loop"] = {
+        "value": round(steps / (dms / 1e3), 2), "unit": "frames/s", "ms_per_frame": round(dms / steps, 4),
+        "workload": "FlowLm::step whole (backbone, out_eos, one flow-head decode step) with svl_tts_step_async, "
+                    "latents fed back on the device",
+        "roofline": roofline_obj(dev_bytes / (dms / 1e3) / 1e9, kernel="every launch of the frames (HIP events)",
+                                 algorithmic_bytes_per_step=int(dev_bytes / steps))}
+    log(f"device loop: {steps} frames: {dms:.2f} ms")
     if not args.no_cpu_baseline:
         import oracle
 
