@@ -98,6 +98,7 @@ struct WgSync {
   unsigned g_arrive;   // row waves whose stores of the phase are complete (grid barrier)
   unsigned g_release;  // grid barriers of the launch this workgroup has passed
   unsigned stop;       // raised when a wait gave up or the grid barrier aborted
+  unsigned w_staged;   // weight waves whose staged weight loads have landed (dense, one item per launch)
   float stats[2];      // a row's norm statistics (sum of squares, sum), published by row wave 0
 };
 
@@ -190,6 +191,7 @@ __device__ __forceinline__ void init_wg_sync(WgSync* ws) {
     ws->g_arrive = 0;
     ws->g_release = 0;
     ws->stop = 0;
+    ws->w_staged = 0;
   }
   __syncthreads();  // the only full-workgroup barrier: nothing is in flight yet
 }
@@ -1475,6 +1477,23 @@ __device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
   return l;
 }
 
+// A dense unit whose rows are whole KiB and whose LDS with the rows staged stays within
+// kDenseLdsCap stages them after Y [2 ipw]: every weight wave requests its share of the rows at
+// once, instead of each row's 16 chain threads streaming their own loads (few rows per unit leave
+// most weight threads idle).
+constexpr int kDenseLdsCap = 144 * 1024;
+__host__ __device__ constexpr int dense_base_bytes(int K, int ipw) {
+  return norm_scratch_floats(K) * 4 + 16 * (K / 16 + 4) * 4 + 2 * ipw * 4 + 64 + 16;
+}
+__host__ __device__ constexpr int dense_stage_bytes(int K, int ipw, int nr_max, bool bf16) {
+  return (K * (bf16 ? 2 : 4)) % 1024 == 0 && dense_base_bytes(K, ipw) + nr_max * K * (bf16 ? 2 : 4) <= kDenseLdsCap
+             ? nr_max * K * (bf16 ? 2 : 4)
+             : 0;
+}
+__device__ __forceinline__ unsigned char* dense_stage(const DenseLds& l, int ipw) {
+  return (unsigned char*)(((size_t)(l.Y + 2 * ipw) + 15) & ~(size_t)15);
+}
+
 template <int KP>
 __device__ __forceinline__ void store_row_chains(const float (&v)[KP], int K, float* xT) {
   const int stride = dense_chain_stride(K);
@@ -1514,8 +1533,10 @@ __device__ __forceinline__ void gemv_dense_rows(const GemvArgs& a, int unit, con
 
 // Weight-wave part of a dense item: issue the first loads of the thread's lane chain as soon as
 // the row waves have requested the input row, wait for the chain-major input, then stream the
-// chain (kDenseBatch loads in flight), sum the 16 lanes and write the row result.
-template <bool BF16W>
+// chain (kDenseBatch loads in flight), sum the 16 lanes and write the row result.  With STAGE (a
+// launch of one item per workgroup) and a unit that fits, the unit's rows are first staged in LDS
+// by all weight waves and the chains read them there (the same loads in the same order).
+template <bool BF16W, bool STAGE = false>
 __device__ __forceinline__ bool w_dense_at(const unsigned char* wbase, int K, int items, int ipw, int parts, int epi,
                                            int unit, WgSync* ws, unsigned char* smem, unsigned item) {
   constexpr int EPL = BF16W ? 8 : 4;  // elements per 16-byte load
@@ -1526,14 +1547,35 @@ __device__ __forceinline__ bool w_dense_at(const unsigned char* wbase, int K, in
   const int NL = K / (16 * EPL);  // loads per chain
   const int w = threadIdx.x - kRowThreads;
   const int rr = w / 16, lane16 = w % 16;
+  const int rowb = K * (BF16W ? 2 : 4);
+  const bool staged = STAGE && item == 0 &&
+                      dense_stage_bytes(K, ipw, epi == EPI_SILU_GATE ? 2 * ipw : ipw, BF16W) > 0;  // uniform
+  unsigned char* W = dense_stage(l, ipw);
+  if (staged) {
+    // 1 KiB pieces of the unit's rows (row r at W + r rowb), piece p by weight wave p % 8
+    const int wave = __builtin_amdgcn_readfirstlane(w / kWave), lane = w % kWave;
+    const int ppr = rowb / 1024, np = g.NR * ppr;
+    for (int pc = wave; pc < np; pc += kWeightWaves) {
+      const int r = pc / ppr, q = pc - r * ppr;
+      const size_t row = (size_t)gemv_phys_row(epi, ff_hidden, g.i0, g.ni, r);
+      lds_dma<16, false>(wbase + row * rowb + q * 1024 + lane * 16, W + pc * 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(kVmWait0);  // this wave's pieces have landed
+    lds_signal(&ws->w_staged);
+    if (!lds_wait<true>(&ws->w_staged, kWeightWaves, &ws->stop)) return false;
+  }
   bool ready = false;
   for (int r0 = 0; r0 < g.NR; r0 += 32) {
     const int r = r0 + rr;
-    const size_t row = (size_t)gemv_phys_row(epi, ff_hidden, g.i0, g.ni, min(r, g.NR - 1));
-    const v4i* src = (const v4i*)(wbase + (row * NL * 16 + lane16) * 16);  // load k at src[16 k]
+    const size_t row = staged ? (size_t)min(r, g.NR - 1) : (size_t)gemv_phys_row(epi, ff_hidden, g.i0, g.ni, min(r, g.NR - 1));
+    // load k at src[16 k]: in the staged rows, or in global memory
+    const v4i* src = (const v4i*)(wbase + (row * NL * 16 + lane16) * 16);
+    const SVL_LDS v4i* lsrc = (const SVL_LDS v4i*)(W + (row * NL * 16 + lane16) * 16);
+    // load k of the chain: from the staged rows (LDS) or streamed from global memory
+    auto wload = [&](int k) -> v4i { return staged ? lsrc[16 * k] : ldg_stream(src + 16 * k); };
     v4i buf[kDenseBatch];
 #pragma unroll
-    for (int u = 0; u < kDenseBatch; ++u) buf[u] = ldg_stream(src + 16 * min(u, NL - 1));
+    for (int u = 0; u < kDenseBatch; ++u) buf[u] = wload(min(u, NL - 1));
     if (!ready) {
       if (!lds_wait<true>(&ws->xq_parts, (item + 1) * kRowWaves, &ws->stop)) return false;
       ready = true;
@@ -1547,7 +1589,7 @@ __device__ __forceinline__ bool w_dense_at(const unsigned char* wbase, int K, in
         const int k = k0 + u;
         if (k < NL) {  // uniform
         const v4i wv = buf[u];
-        if (stream) buf[u] = ldg_stream(src + 16 * min(k + kDenseBatch, NL - 1));
+        if (stream) buf[u] = wload(min(k + kDenseBatch, NL - 1));
         float xv[EPL];
         if constexpr (BF16W) {
           const float4 x0 = *(const float4*)(xc + k * 8), x1 = *(const float4*)(xc + k * 8 + 4);
