@@ -1477,16 +1477,18 @@ __device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
   return l;
 }
 
-// A dense unit whose rows are whole KiB and whose LDS with the rows staged stays within
+// A dense unit whose lane chains are longer than the loads a chain thread keeps in flight
+// (kDenseBatch), whose rows are whole KiB and whose LDS with the rows staged stays within
 // kDenseLdsCap stages them after Y [2 ipw]: every weight wave requests its share of the rows at
 // once, instead of each row's 16 chain threads streaming their own loads (few rows per unit leave
-// most weight threads idle).
+// most weight threads idle).  Shorter chains already have their whole row in flight.
 constexpr int kDenseLdsCap = 144 * 1024;
 __host__ __device__ constexpr int dense_base_bytes(int K, int ipw) {
   return norm_scratch_floats(K) * 4 + 16 * (K / 16 + 4) * 4 + 2 * ipw * 4 + 64 + 16;
 }
 __host__ __device__ constexpr int dense_stage_bytes(int K, int ipw, int nr_max, bool bf16) {
-  return (K * (bf16 ? 2 : 4)) % 1024 == 0 && dense_base_bytes(K, ipw) + nr_max * K * (bf16 ? 2 : 4) <= kDenseLdsCap
+  return K / (bf16 ? 128 : 64) > kDenseBatch && (K * (bf16 ? 2 : 4)) % 1024 == 0 &&
+                 dense_base_bytes(K, ipw) + nr_max * K * (bf16 ? 2 : 4) <= kDenseLdsCap
              ? nr_max * K * (bf16 ? 2 : 4)
              : 0;
 }
