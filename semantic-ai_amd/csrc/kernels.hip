@@ -208,9 +208,10 @@ __global__ __launch_bounds__(kStepThreads) void gemv_phase_kernel(const float* h
       if (!lds_wait(&ws.xq_parts, kRowWaves, &ws.stop)) return;
       w_terms_q4k(it, smem);
     } else {
-      const bool ok = (hepn >> 24) ? w_dense_at<true, true>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi,
+      const bool nrm = ((hepn >> 8) & 0xff) != NORM_NONE;
+      const bool ok = (hepn >> 24) ? w_dense_at<true, true>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi, nrm,
                                                             unit, &ws, smem, 0)
-                                   : w_dense_at<false, true>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi,
+                                   : w_dense_at<false, true>((const unsigned char*)hw, hin, hitems, hipw, hparts, epi, nrm,
                                                              unit, &ws, smem, 0);
       if (!ok) return;
     }
@@ -522,8 +523,9 @@ size_t phase_smem(const Phase& ph) {
                (size_t)nb * ts * kQ4TermStride * 4 + 16 + (size_t)2 * g.ipw * 4 + 64;
       }
       if (g.L.fmt == FMT_F32C || g.L.fmt == FMT_BF16C)
-        return (size_t)dense_base_bytes(K, g.ipw) +
-               (size_t)dense_stage_bytes(K, g.ipw, g.epi == EPI_SILU_GATE ? 2 * g.ipw : g.ipw, g.L.fmt == FMT_BF16C);
+        return (size_t)dense_base_bytes(K, g.ipw, g.norm != NORM_NONE) +
+               (size_t)dense_stage_bytes(K, g.ipw, g.epi == EPI_SILU_GATE ? 2 * g.ipw : g.ipw, g.L.fmt == FMT_BF16C,
+                                         g.norm != NORM_NONE);
       return (size_t)norm_scratch_floats(K) * 4 + (kRowThreads / 16) * 4 + 64;
     }
     case PH_ATTN:

@@ -1469,10 +1469,11 @@ struct DenseLds {
   float* Y;   // [2 ipw]
 };
 
-__device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
+// Without a norm on the input the norm scratch is left out.
+__device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K, bool norm) {
   DenseLds l;
   l.xs = (float*)smem;
-  l.xT = l.xs + norm_scratch_floats(K);
+  l.xT = l.xs + (norm ? norm_scratch_floats(K) : 0);
   l.Y = l.xT + 16 * dense_chain_stride(K);
   return l;
 }
@@ -1483,12 +1484,12 @@ __device__ __forceinline__ DenseLds dense_lds(unsigned char* smem, int K) {
 // once, instead of each row's 16 chain threads streaming their own loads (few rows per unit leave
 // most weight threads idle).  Shorter chains already have their whole row in flight.
 constexpr int kDenseLdsCap = 144 * 1024;
-__host__ __device__ constexpr int dense_base_bytes(int K, int ipw) {
-  return norm_scratch_floats(K) * 4 + 16 * (K / 16 + 4) * 4 + 2 * ipw * 4 + 64 + 16;
+__host__ __device__ constexpr int dense_base_bytes(int K, int ipw, bool norm) {
+  return (norm ? norm_scratch_floats(K) * 4 : 0) + 16 * (K / 16 + 4) * 4 + 2 * ipw * 4 + 64 + 16;
 }
-__host__ __device__ constexpr int dense_stage_bytes(int K, int ipw, int nr_max, bool bf16) {
+__host__ __device__ constexpr int dense_stage_bytes(int K, int ipw, int nr_max, bool bf16, bool norm) {
   return K / (bf16 ? 128 : 64) > kDenseBatch && (K * (bf16 ? 2 : 4)) % 1024 == 0 &&
-                 dense_base_bytes(K, ipw) + nr_max * K * (bf16 ? 2 : 4) <= kDenseLdsCap
+                 dense_base_bytes(K, ipw, norm) + nr_max * K * (bf16 ? 2 : 4) <= kDenseLdsCap
              ? nr_max * K * (bf16 ? 2 : 4)
              : 0;
 }
@@ -1513,7 +1514,7 @@ __device__ __forceinline__ void gemv_dense_rows(const GemvArgs& a, int unit, con
                                                 RowSync& rs, unsigned item) {
   const int K = a.L.in;
   const Q8Geom g = q8_geom(K, gemv_items(a), a.ipw, a.parts, a.epi == EPI_SILU_GATE, unit);
-  const DenseLds l = dense_lds(smem, K);
+  const DenseLds l = dense_lds(smem, K, a.norm != NORM_NONE);
   constexpr bool kNorm = KP <= 8;
   NormW<kNorm ? KP : 1> nwt;
   if (kNorm && a.norm != NORM_NONE) load_norm_weights(a.norm, a.nw, a.nb, K, nwt);
@@ -1540,18 +1541,18 @@ __device__ __forceinline__ void gemv_dense_rows(const GemvArgs& a, int unit, con
 // by all weight waves and the chains read them there (the same loads in the same order).
 template <bool BF16W, bool STAGE = false>
 __device__ __forceinline__ bool w_dense_at(const unsigned char* wbase, int K, int items, int ipw, int parts, int epi,
-                                           int unit, WgSync* ws, unsigned char* smem, unsigned item) {
+                                           bool norm, int unit, WgSync* ws, unsigned char* smem, unsigned item) {
   constexpr int EPL = BF16W ? 8 : 4;  // elements per 16-byte load
   const int ff_hidden = items;  // read by gemv_phys_row for the SiLU gate only, where items = ff_hidden
   const Q8Geom g = q8_geom(K, items, ipw, parts, epi == EPI_SILU_GATE, unit);
-  const DenseLds l = dense_lds(smem, K);
+  const DenseLds l = dense_lds(smem, K, norm);
   const int stride = dense_chain_stride(K);
   const int NL = K / (16 * EPL);  // loads per chain
   const int w = threadIdx.x - kRowThreads;
   const int rr = w / 16, lane16 = w % 16;
   const int rowb = K * (BF16W ? 2 : 4);
   const bool staged = STAGE && item == 0 &&
-                      dense_stage_bytes(K, ipw, epi == EPI_SILU_GATE ? 2 * ipw : ipw, BF16W) > 0;  // uniform
+                      dense_stage_bytes(K, ipw, epi == EPI_SILU_GATE ? 2 * ipw : ipw, BF16W, norm) > 0;  // uniform
   unsigned char* W = dense_stage(l, ipw);
   if (staged) {
     // 1 KiB pieces of the unit's rows (row r at W + r rowb), piece p by weight wave p % 8
@@ -1624,7 +1625,8 @@ __device__ __forceinline__ bool w_dense(const Phase* ph, int unit, WgSync* ws, u
   const int epi = ld_const(&ph->g.epi);
   const int items = epi == EPI_SILU_GATE ? ld_const(&ph->g.ff_hidden) : ld_const(&ph->g.L.out);
   return w_dense_at<BF16W>((const unsigned char*)ld_const(&ph->g.L.w), ld_const(&ph->g.L.in), items,
-                           ld_const(&ph->g.ipw), ld_const(&ph->g.parts), epi, unit, ws, smem, item);
+                           ld_const(&ph->g.ipw), ld_const(&ph->g.parts), epi, ld_const(&ph->g.norm) != NORM_NONE, unit, ws,
+                           smem, item);
 }
 
 __device__ __forceinline__ bool is_chained_dense(int fmt) { return fmt == FMT_F32C || fmt == FMT_BF16C; }
