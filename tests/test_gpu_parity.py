@@ -345,6 +345,47 @@ def test_tts_small_prefilled_matches_oracle():
         assert np.array_equal(z, zo), (i, float(np.max(np.abs(z - zo))))
 
 
+# FF hidden 2048: the FF-out linear (f32, K = 2048) has lane chains of 32 loads and one row per
+# unit, so its units stage their rows in LDS before the chains run
+T_STAGED = W.tts_shape("tts-staged-ff-out", 256, 2, 4, 2048, flow_dim=64, flow_depth=1)
+
+
+def test_tts_staged_dense_rows_match_oracle_and_persistent(monkeypatch):
+    s = T_STAGED
+    _, g, o = build(s, "f32", seed=31)
+    ks, vs = W.prefill_caches(s, 40, seed=32)
+    gs = g.state_from_layer_caches(ks, vs, capacity=128)
+    os_ = o.state_from_layer_caches(ks, vs)
+    monkeypatch.setenv("SVL_STEP_LAUNCH", "persistent")  # read when a state is created
+    gp = g.state_from_layer_caches(ks, vs, capacity=128)
+    monkeypatch.delenv("SVL_STEP_LAUNCH")
+    lat = W.latents(s, 8, seed=33)
+    for i in range(8):
+        x = None if i == 0 else lat[i][None]
+        z = g.backbone_step(x, gs)[0]
+        zp = g.backbone_step(x, gp)[0]
+        zo = os_.tts_step(None if i == 0 else lat[i])
+        assert np.array_equal(z, zo), (i, float(np.max(np.abs(z - zo))))
+        assert np.array_equal(z, zp), i
+
+
+def test_stt_bf16_staged_dense_rows_match_oracle():
+    """bf16 linears with FF hidden 4096: the FF-out linear (K = 4096, bf16) has 32-load chains and
+    stages its rows."""
+    s = W.stt_shape("stt-staged-bf16", 256, 2, 4, 24.0, 24, card=64, n_q=4, text_card=100)
+    assert s.ff_hidden == 4096
+    _, g, o = build(s, "bf16", seed=34)
+    gs, os_ = g.init_state(), o.new_state()
+    audio = W.audio_tokens(s, 6, seed=35)[0]
+    text = s.text_card
+    for i in range(6):
+        tg, lg = g.step([text], audio[i][None], gs, want_logits=True)
+        to, lo = os_.stt_step(text, audio[i], want_logits=True)
+        assert np.array_equal(lg[0].view(np.uint32), lo.view(np.uint32)), i
+        assert tg[0] == to
+        text = int(tg[0])
+
+
 def test_transformer_forward_matches_oracle():
     s = W.Shape("fwd", W.MODEL_TRANSFORMER, 128, 2, 2, 1, 64, W.FF_PLAIN, 256, W.NORM_LAYER, 1e-5, 7,
                 layer_scale=1)
