@@ -24,7 +24,10 @@ Default run (--workload stt1b-q8): ONE JSON line whose `value` is the B = 1 rate
     4 host threads (the reference's default) over a bounded sample, with its tokens compared
     to the GPU's, the CPU model and an all-cores figure;
   * `copy_ceiling`: libsvl's copy kernel over 1 GiB (read and written), the achievable HBM rate
-    beside the vendor peak; each roofline also gives `frac_of_copy_ceiling`.
+    beside the vendor peak; each roofline also gives `frac_of_copy_ceiling`;
+  * `read_floor` in each roofline that states its bytes per launch: the same bytes moved by a bare
+    streaming read kernel launched back to back over cold buffers (the floor of any one launch of
+    that size), and `frac_of_read_floor` = that floor's time / the kernel's time per launch.
 Other workloads (--workload): stt1b-bf16-b1, stt2.6b-q4k-b1, tts-f32-b1 (one line each).
 
 `--calibrate-copy BYTES` runs libsvl's plain copy kernel over BYTES three times (the known-size
@@ -173,6 +176,44 @@ def copy_ceiling(nbytes=1 << 30):
     gbs = 2 * nbytes / (best / 1e3) / 1e9
     return {"GBps": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_read": nbytes,
             "bytes_written": nbytes, "kernel": "libsvl copy kernel (16-byte loads and stores)"}
+
+
+READ_SHAPES = [(256, 1024), (512, 512), (512, 1024), (1024, 512), (2048, 256)]
+
+
+def read_floor(bytes_per_launch, total=1 << 30):
+    """The per-launch floor of moving `bytes_per_launch` bytes: libsvl's bare streaming read kernel
+    launched back to back over distinct buffers of that size (together at least `total` bytes,
+    more than every cache, so each launch reads cold bytes as the step's kernels do), for several
+    grid shapes; HIP events over three passes after one warm-up pass.  Returns the best shape."""
+    import svl
+    from svl import hip
+
+    L = svl.load_library()
+    b = -(-int(bytes_per_launch) // 256) * 256
+    nb = max(2, -(-total // b))
+    buf, out = hip.DeviceBuffer(b * nb), hip.DeviceBuffer(2048 * 1024 * 4)
+    e0, e1 = hip.Event(), hip.Event()
+    best = None
+    for blocks, threads in READ_SHAPES:
+        def one_pass():
+            for i in range(nb):
+                svl._check(L.svl_bench_read(0, buf.address + i * b, b, blocks, threads, out.address, None))
+        one_pass()
+        e0.record(None)
+        for _ in range(3):
+            one_pass()
+        e1.record(None)
+        hip.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (3 * nb)
+        if best is None or us < best[0]:
+            best = (us, blocks, threads)
+    del buf, out
+    us, blocks, threads = best
+    gbs = b / (us / 1e6) / 1e9
+    return {"us_per_launch": round(us, 3), "GBps": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": b, "buffers": nb, "grid": [blocks, threads],
+            "kernel": "libsvl bare read kernel (non-temporal 16-byte loads), back to back over cold buffers"}
 
 
 def timed_launch(model, st, n, d_audio, d_out, warmup):
@@ -646,6 +687,11 @@ def main():
     for r in [line.get("roofline")] + ([line["b64"].get("roofline")] if "b64" in line else []):
         if r:
             r["frac_of_copy_ceiling"] = round(r["achieved"] / line["copy_ceiling"]["GBps"], 4)
+        # the same bytes per launch moved by a bare read kernel, launch after launch: the floor of
+        # any one launch of this size, gap included like the kernel's own figure
+        if r and r.get("algorithmic_bytes_per_launch") and r.get("avg_launch_us"):
+            r["read_floor"] = read_floor(r["algorithmic_bytes_per_launch"])
+            r["frac_of_read_floor"] = round(r["read_floor"]["us_per_launch"] / r["avg_launch_us"], 4)
     print(json.dumps(line), flush=True)
 
 

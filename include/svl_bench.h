@@ -17,6 +17,13 @@ extern "C" {
  * stream).  bytes must be a multiple of 16 and both pointers 16-byte aligned device memory. */
 int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* stream);
 
+/* A bare streaming read of src[0..bytes) on device `device` by `blocks` workgroups of `threads`
+ * threads (64 .. 1024, a multiple of 64; blocks 1 .. 65536), four non-temporal 16-byte loads in
+ * flight per thread; out[t] (device memory, blocks * threads words) receives a fold of the words
+ * thread t read.  bytes a multiple of 16, src 16-byte aligned.  Launched back to back over buffers
+ * larger than every cache, it gives the per-launch floor of moving a kernel's bytes. */
+int svl_bench_read(int device, const void* src, size_t bytes, int blocks, int threads, uint32_t* out, void* stream);
+
 /* The norm statistics of `rows` rows of `k` f32 values (x: device memory, row-major) exactly as
  * the decode step's RMSNorm / LayerNorm prologues compute them -- candle-nn's CPU order, one f32
  * accumulator per row adding the elements in index order: out[2 r] = sum of x^2, out[2 r + 1] =

@@ -294,6 +294,8 @@ hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t s);
 hipError_t launch_activation(int kind, const float* x, size_t n, float* y, hipStream_t s);
 hipError_t launch_fill_i32(int* p, int v, size_t n, hipStream_t s);
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
+// out[0 .. blocks * threads): one word per thread of a bare streaming read of src[0, bytes)
+hipError_t launch_read(const void* src, size_t bytes, int blocks, int threads, uint32_t* out, hipStream_t s);
 hipError_t launch_row_stats(const float* x, int rows, int K, int norm, float* out, hipStream_t s);
 
 }  // namespace svl

@@ -1014,4 +1014,30 @@ hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s) 
   return hipGetLastError();
 }
 
+// A bare streaming read: n 16-byte pieces, four non-temporal loads in flight per thread, folded
+// into one word per thread so that the loads stay live (out[thread] = xor of two words of each
+// piece the thread read).
+__global__ void __launch_bounds__(1024) read_kernel(const v4i* __restrict__ x, size_t n, uint32_t* out) {
+  const size_t nt = (size_t)gridDim.x * blockDim.x, g = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  size_t i = g;
+  for (; i + 3 * nt < n; i += 4 * nt) {
+    v4i a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = __builtin_nontemporal_load(x + i + u * nt);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= (uint32_t)a[u].x ^ (uint32_t)a[u].w;
+  }
+  for (; i < n; i += nt) {
+    const v4i a = __builtin_nontemporal_load(x + i);
+    acc ^= (uint32_t)a.x ^ (uint32_t)a.w;
+  }
+  out[g] = acc;
+}
+
+hipError_t launch_read(const void* src, size_t bytes, int blocks, int threads, uint32_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(read_kernel, dim3((unsigned)blocks), dim3((unsigned)threads), 0, s, (const v4i*)src, bytes / 16, out);
+  return hipGetLastError();
+}
+
 }  // namespace svl

@@ -1725,6 +1725,18 @@ static int bench_copy_impl(int device, const void* src, void* dst, size_t bytes,
   return 0;
 }
 
+static int bench_read_impl(int device, const void* src, size_t bytes, int blocks, int threads, uint32_t* out,
+                           void* stream) {
+  if ((bytes % 16) || ((uintptr_t)src % 16)) return set_error(SVL_ERR_INVALID_INPUT, "read needs 16-byte multiples and alignment");
+  if (blocks < 1 || blocks > 65536 || threads < 64 || threads > 1024 || threads % 64)
+    return set_error(SVL_ERR_INVALID_INPUT, "grid %d x %d: 1 .. 65536 workgroups of 64 .. 1024 threads (multiple of 64)",
+                     blocks, threads);
+  if (!out || (bytes && !src)) return set_error(SVL_ERR_INVALID_INPUT, "null argument");
+  HIP_TRY(hipSetDevice(device));
+  HIP_TRY(launch_read(src, bytes, blocks, threads, out, (hipStream_t)stream));
+  return 0;
+}
+
 static int bench_row_stats_impl(int device, const float* x, int rows, int k, int norm, float* out, void* stream) {
   if (!x || !out || rows <= 0) return set_error(SVL_ERR_INVALID_INPUT, "null argument or no rows");
   if (k < 4 || k > 4096 || k % 4) return set_error(SVL_ERR_INVALID_INPUT, "row length %d: 4 .. 4096, a multiple of 4", k);
@@ -2462,6 +2474,10 @@ int svl_device_count(int* count) {
 
 int svl_bench_copy(int device, const void* src, void* dst, size_t bytes, void* stream) {
   return guarded([&] { return bench_copy_impl(device, src, dst, bytes, stream); });
+}
+
+int svl_bench_read(int device, const void* src, size_t bytes, int blocks, int threads, uint32_t* out, void* stream) {
+  return guarded([&] { return bench_read_impl(device, src, bytes, blocks, threads, out, stream); });
 }
 
 int svl_bench_activation(int device, int kind, const float* x, size_t n, float* y, void* stream) {

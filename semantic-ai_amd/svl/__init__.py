@@ -44,7 +44,7 @@ EXPORTS = [
     "svl_state_synchronize", "svl_state_stream", "svl_transformer_forward", "svl_stt_step",
     "svl_stt_recognize", "svl_stt_recognize_async", "svl_stt_step_heads", "svl_stt_recognize_heads",
     "svl_stt_recognize_heads_async", "svl_tts_backbone_step",
-    "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_row_stats", "svl_bench_phase", "svl_bench_activation",
+    "svl_stt_recognize_noalloc", "svl_bench_copy", "svl_bench_read", "svl_bench_row_stats", "svl_bench_phase", "svl_bench_activation",
     "svl_tts_step", "svl_tts_step_async", "svl_stt_recognize_turns", "svl_stt_recognize_turns_async",
     "svl_state_load_voice", "svl_rvq_create", "svl_rvq_destroy", "svl_rvq_encode", "svl_rvq_encode_async",
     "svl_rvq_synchronize",
@@ -143,6 +143,7 @@ def load_library(path: str = LIB_PATH):
     L.svl_rvq_synchronize.argtypes = [vp]
     L.svl_bench_phase.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_int)]
     L.svl_bench_copy.argtypes = [C.c_int, vp, vp, sz, vp]
+    L.svl_bench_read.argtypes = [C.c_int, vp, sz, C.c_int, C.c_int, vp, vp]
     L.svl_bench_row_stats.argtypes = [C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp]
     L.svl_bench_activation.argtypes = [C.c_int, C.c_int, vp, sz, vp, vp]
     for name in EXPORTS:
