@@ -729,7 +729,7 @@ __device__ __forceinline__ void w_issue_at(const int8_t* wq, const uint16_t* sc,
         it.wa[k] = ldg_stream(wp);
         it.wb[k] = ldg_stream(wp + 1);
       }
-      it.wd[k] = ldg(sc + row * nb + blk);
+      it.wd[k] = ldg_stream(sc + row * nb + blk);
     }
     r += dr;
     blk += db;
