@@ -192,7 +192,7 @@ def read_floor(bytes_per_launch, total=1 << 30):
     L = svl.load_library()
     b = -(-int(bytes_per_launch) // 256) * 256
     nb = max(2, -(-total // b))
-    buf, out = hip.DeviceBuffer(b * nb), hip.DeviceBuffer(2048 * 1024 * 4)
+    buf, out = hip.DeviceBuffer(b * nb), hip.DeviceBuffer(4 * max(bl * th for bl, th in READ_SHAPES))
     e0, e1 = hip.Event(), hip.Event()
     best = None
     for blocks, threads in READ_SHAPES:

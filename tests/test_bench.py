@@ -50,3 +50,11 @@ def test_phase_bytes_of_a_q8_0_gemv_and_attention():
     kinds = {name: [pick(i) for i in ([1, 3, 1, 2048], [1, 3, 1, 5632], [1, 4, 1, 2048], [1, 6, 1, 2048])]
              for name, pick in bench.KERNEL_GROUPS.items()}
     assert sum(sum(v) for v in kinds.values()) == 4
+
+
+def test_read_floor_shapes_are_grids_the_read_kernel_accepts():
+    """svl_bench_read takes 1 .. 65536 workgroups of 64 .. 1024 threads (a multiple of 64); every
+    shape the read floor tries must be one, and each writes blocks x threads words."""
+    assert bench.READ_SHAPES
+    for blocks, threads in bench.READ_SHAPES:
+        assert 1 <= blocks <= 65536 and 64 <= threads <= 1024 and threads % 64 == 0
